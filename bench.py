@@ -1,0 +1,215 @@
+"""Benchmark of the INT8 attention hot path on one MI355X (BASELINE.json's metric).
+
+A step is one pass of the path over one synthetic batch, as the reference's DiT block runs it
+(src/stack.rs:1541-1616 then 1815-1838): fused RMSNorm+RoPE+quantize of Q and of K, the V
+transpose, then INT8-QK attention. Default workload: BASELINE config 3, B=1 H=32 S=129,024
+D=128, bf16 QKV ~ N(0,1) with a per-channel K offset ~ N(0,2), 3D RoPE over a 32x42x96 grid.
+Inputs are resident in HBM before timing; W untimed steps, then K timed steps between
+synchronizations. The attention kernel's own launches are timed with HIP events on the stream
+they are enqueued on (torch's current stream), giving the roofline figure.
+
+Prints one JSON line. `cpu_baseline` times the reference's CPU path (its f64 test oracle,
+restated in C: oracle/h3oracle.c) on this host on a bounded sample of query rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import re
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "h3-hrx_amd"))
+
+METRIC = "INT8 attn TOPS + ms/call at S=129k,H=32,D=128; % of gfx950 int8 MFMA peak"
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
+WORKLOADS = {
+    # name: (tokens, heads, rope grid (t, h, w))
+    "c3": (129024, 32, (32, 42, 96)),
+    "c2": (31104, 32, (24, 24, 54)),
+    "c1": (1024, 8, (1, 32, 32)),
+}
+
+
+def rope_tables(torch, dev, tokens, grid):
+    """3D RoPE cos/sin [tokens][48]: axes (t, h, w) x 16 frequencies, angle = f32(pos) *
+    inv_freq[j] (src/rope.rs:11-37, src/layout.rs:64-72), with a synthetic inv_freq
+    10000^(-j/16) since the checkpoint's table is not available."""
+    t_n, h_n, w_n = grid
+    i = torch.arange(tokens, device=dev, dtype=torch.int64)
+    pos = torch.stack([i // (h_n * w_n), (i // w_n) % h_n, i % w_n], dim=1).to(torch.float32)
+    inv = torch.pow(torch.tensor(10000.0, device=dev), -torch.arange(16, device=dev) / 16.0)
+    ang = (pos[:, :, None] * inv[None, None, :].to(torch.float32)).reshape(tokens, 48)
+    return torch.cos(ang).contiguous(), torch.sin(ang).contiguous()
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary, if present."""
+    p = ROOT / "profiles" / f"attention_i8qkhm_{workload}_pmc.md"
+    if not p.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
+    """The reference's CPU path (prepared_qk + f64 attention of the operands,
+    tests/kernels.rs:1704-1741, 2084-2111) restated in C, on sampled query rows, OpenMP over
+    (row, head). Returns the dict for the JSON line."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    threads = min(threads, 16)
+    rng = np.random.default_rng(1)
+    rows = np.sort(rng.choice(tokens, size=rows_per_head, replace=False)).astype(np.int32)
+    per_row_s, fixed_s, _ = O.cpu_baseline(q16, k16, v16, tokens, heads, rows, threads)
+    call_s = fixed_s + per_row_s * tokens / rows_per_head
+    ops = 4.0 * tokens * tokens * heads * 128
+    return {
+        "value": ops / call_s / 1e12,
+        "unit": "TOPS",
+        "ms_per_call": call_s * 1e3,
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{rows_per_head} query rows x {heads} heads of S={tokens} (f64 attention, "
+                   f"{per_row_s:.2f} s) plus the per-call K operand/mean/V^T pass "
+                   f"({fixed_s:.2f} s) measured; ms_per_call extrapolated linearly in rows"),
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-rows", type=int, default=8, help="query rows per head for the CPU leg")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(head/sequence sharding is a design note, not a code path)"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import h3attn as H
+
+    dev = torch.device("cuda:0")
+    tokens, heads, grid = WORKLOADS[args.workload]
+    width = heads * 128
+    cap = H.capacity(tokens)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    # fused QKV projection [tokens][3*width] bf16: N(0,1), K offset N(0, 2) per channel
+    fused = torch.randn((tokens, 3 * width), generator=g, device=dev, dtype=torch.float32)
+    k_off = torch.randn((width,), generator=g, device=dev) * math.sqrt(2.0)
+    fused[:, width:2 * width] += k_off
+    fused_bf16 = fused.to(torch.bfloat16)
+    del fused
+    qnorm = torch.ones(128, device=dev, dtype=torch.float32)
+    knorm = torch.ones(128, device=dev, dtype=torch.float32)
+    cos_t, sin_t = rope_tables(torch, dev, tokens, grid)
+    # operand buffers (IntQk), zero-filled once
+    qi = torch.zeros(heads * cap * 32, dtype=torch.int32, device=dev)
+    ki = torch.zeros_like(qi)
+    qs = torch.zeros(heads * cap, dtype=torch.float32, device=dev)
+    ks = torch.zeros_like(qs)
+    vt = torch.zeros(width * cap, dtype=torch.float16, device=dev)
+    out = torch.zeros((tokens, width), dtype=torch.float16, device=dev)
+    elem = H.H3_ELEM_BF16
+    pq = H.PrepareCfg(3 * width, 0, heads, H.EXTRA_Q, cap, 1e-5, elem)
+    pk = H.PrepareCfg(3 * width, width, heads, 1.0, cap, 1e-5, elem)
+    tc = H.TransposeCfg(width, cap, elem)
+    ac = H.AttentionCfg(width, width, width, tokens, cap, H.config_f32(1.0 / math.sqrt(128.0)))
+
+    att_events = []
+
+    def step(record: bool):
+        H.prepare_qk_rope_i8hm(pq, tokens, fused_bf16, qnorm, cos_t, sin_t, qi, qs)
+        H.prepare_qk_rope_i8hm(pk, tokens, fused_bf16, knorm, cos_t, sin_t, ki, ks)
+        H.transpose_qkv_v_f16(tc, tokens, tokens, fused_bf16, vt)
+        if record:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+        H.attention_i8qkhm(ac, tokens, heads, qi, qs, ki, ks, vt, out)
+        if record:
+            e1.record()
+            att_events.append((e0, e1))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    print(f"# warmup done: {args.workload} S={tokens} H={heads}", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    att_ms = [a.elapsed_time(b) for a, b in att_events]
+    att_avg = sum(att_ms) / len(att_ms)
+    ops = 4.0 * tokens * tokens * heads * 128  # QK + PV multiply-adds x2 (benches/kernels.rs:570)
+    value = ops / (ms_step * 1e-3) / 1e12
+    achieved = ops / (att_avg * 1e-3) / 1e12
+    out_ok = bool(torch.isfinite(out).all().item())
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"BASELINE config {args.workload[1:]}: B=1 H={heads} S={tokens} D=128, "
+                        "bf16 QKV N(0,1) + K offset N(0,2), RMSNorm(w=1)+3D RoPE, int8 QK with "
+                        "per-(token,head) scales, f16 PV, non-causal",
+            "tokens": tokens,
+            "heads": heads,
+            "head_dim": 128,
+            "capacity": cap,
+            "step": "prepare_qk_rope_i8hm(Q) + prepare_qk_rope_i8hm(K) + transpose_qkv_v_f16 "
+                    "+ attention_i8qkhm",
+        },
+        "attention_ms": round(att_avg, 4),
+        "attention_tops": round(achieved, 3),
+        "attention_frac_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
+        "output_finite": out_ok,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "traffic": traffic_from_profiles(args.workload),
+        },
+    }
+    if not args.no_cpu:
+        print("# cpu baseline...", file=sys.stderr, flush=True)
+        q16 = fused_bf16[:, :width].to(torch.float16).cpu().numpy().view(np.uint16)
+        k16 = fused_bf16[:, width:2 * width].to(torch.float16).cpu().numpy().view(np.uint16)
+        v16 = fused_bf16[:, 2 * width:].to(torch.float16).cpu().numpy().view(np.uint16)
+        line["cpu_baseline"] = cpu_baseline(np.ascontiguousarray(q16), np.ascontiguousarray(k16),
+                                            np.ascontiguousarray(v16), tokens, heads,
+                                            args.cpu_rows)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

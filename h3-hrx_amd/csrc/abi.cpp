@@ -1,0 +1,366 @@
+// C ABI of libh3attn (include/h3attn.h): argument and binding checks, then the HIP launchers.
+//
+// Every entry point validates before it touches the device, exactly as the reference's
+// dispatch::emit checks bindings before dispatch (src/dispatch.rs:264-276) and as each Loom
+// kernel's config.decl ranges bound its specialisation (kernels/*.loom). A failing check
+// returns its status, records a message for h3_last_error(), and launches nothing.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "internal.hpp"
+
+namespace h3 {
+
+static std::string& g_error_ref() {
+  thread_local std::string e;
+  return e;
+}
+
+int set_error(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error_ref() = buf;
+  return status;
+}
+
+namespace {
+
+int ok() {
+  g_error_ref().clear();
+  return H3_OK;
+}
+
+// src/dispatch.rs:264-276: every binding must cover the extent the kernel addresses.
+int check_bindings(const char* stage, const h3_view* views, const size_t* need, int n) {
+  for (int i = 0; i < n; ++i) {
+    if (views[i].bytes < need[i])
+      return set_error(H3_ERR_BINDING, "%s: binding %d is %zu bytes, the kernel addresses %zu", stage, i,
+                  views[i].bytes, need[i]);
+    if (need[i] > 0 && views[i].ptr == nullptr)
+      return set_error(H3_ERR_ARGUMENT, "%s: binding %d is null", stage, i);
+  }
+  return H3_OK;
+}
+
+// config.decl ... where [range(v, lo, hi), multiple_of(v, m)]: lo <= v <= hi, v % m == 0.
+bool in_range(uint32_t v, uint32_t lo, uint32_t hi, uint32_t multiple = 1) {
+  return v >= lo && v <= hi && v % multiple == 0;
+}
+
+int launched(const char* stage, hipError_t e) {
+  if (e != hipSuccess) return set_error(H3_ERR_LAUNCH, "%s: %s", stage, hipGetErrorString(e));
+  return ok();
+}
+
+int device_ready(const char* stage) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return set_error(H3_ERR_NO_DEVICE, "%s: no HIP device (%s)", stage, hipGetErrorString(e));
+  return H3_OK;
+}
+
+// kernels/prepare_qk_i8.loom:9-15 (+ prepare_qk_i8hm.loom:13, prepare_qk_rope_i8hm.loom:15-17)
+int check_prepare_cfg(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
+                      bool head_major) {
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  if (!in_range(cfg->row_stride, 128, 65536, 128))
+    return set_error(H3_ERR_CONFIG, "%s: row_stride %u outside [128, 65536] step 128", stage,
+                cfg->row_stride);
+  if (!in_range(cfg->head_offset, 0, 65536, 128))
+    return set_error(H3_ERR_CONFIG, "%s: head_offset %u outside [0, 65536] step 128", stage,
+                cfg->head_offset);
+  if (!in_range(cfg->heads, 1, 256))
+    return set_error(H3_ERR_CONFIG, "%s: heads %u outside [1, 256]", stage, cfg->heads);
+  if ((uint64_t)cfg->head_offset + 128ull * cfg->heads > cfg->row_stride)
+    return set_error(H3_ERR_CONFIG, "%s: head_offset %u + %u heads exceed row_stride %u", stage,
+                cfg->head_offset, cfg->heads, cfg->row_stride);
+  if (cfg->elem != H3_ELEM_F16 && cfg->elem != H3_ELEM_BF16)
+    return set_error(H3_ERR_CONFIG, "%s: unknown element format %u", stage, cfg->elem);
+  if (!in_range(tokens, 1, 1048576))
+    return set_error(H3_ERR_ARGUMENT, "%s: tokens %u outside [1, 1048576]", stage, tokens);
+  if (head_major) {
+    if (!in_range(cfg->token_capacity, 32, 1048576, 32))
+      return set_error(H3_ERR_CONFIG, "%s: token_capacity %u outside [32, 1048576] step 32", stage,
+                  cfg->token_capacity);
+    // "The host's capacity is at least tokens + 16, so a token's scale row is in bounds."
+    // (prepare_qk_i8hm.loom in-file 51-53): the kernel addresses rows < token_capacity.
+    if (tokens > cfg->token_capacity)
+      return set_error(H3_ERR_ARGUMENT, "%s: tokens %u exceed token_capacity %u", stage, tokens,
+                  cfg->token_capacity);
+  }
+  return H3_OK;
+}
+
+int prepare_common(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x,
+                   h3_view mean, h3_view codes, h3_view scales, hipStream_t stream,
+                   bool head_major) {
+  int st = check_prepare_cfg(stage, cfg, tokens, head_major);
+  if (st) return st;
+  const size_t rows_out = head_major ? (size_t)cfg->heads * cfg->token_capacity
+                                     : (size_t)tokens * cfg->heads;
+  h3_view views[4] = {x, mean, codes, scales};
+  size_t need[4] = {(size_t)tokens * cfg->row_stride * 2, mean.ptr ? (size_t)cfg->row_stride * 4 : 0,
+                    rows_out * 128, rows_out * 4};
+  if ((st = check_bindings(stage, views, need, 4))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_prepare_qk(*cfg, tokens, head_major, x.ptr,
+                                           static_cast<const float*>(mean.ptr),
+                                           static_cast<int32_t*>(codes.ptr),
+                                           static_cast<float*>(scales.ptr), stream));
+}
+
+int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x,
+                  h3_view weight, h3_view cos_t, h3_view sin_t) {
+  h3_view views[4] = {x, weight, cos_t, sin_t};
+  size_t need[4] = {(size_t)tokens * cfg->row_stride * 2, 128 * 4, (size_t)tokens * 48 * 4,
+                    (size_t)tokens * 48 * 4};
+  return check_bindings(stage, views, need, 4);
+}
+
+int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
+                     uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                     h3_view out, hipStream_t stream, bool head_major) {
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  // kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17
+  if (!in_range(cfg->q_stride, 128, 32768, 128))
+    return set_error(H3_ERR_CONFIG, "%s: q_stride %u outside [128, 32768] step 128", stage,
+                cfg->q_stride);
+  if (!in_range(cfg->kv_stride, 128, 32768, 128))
+    return set_error(H3_ERR_CONFIG, "%s: kv_stride %u outside [128, 32768] step 128", stage,
+                cfg->kv_stride);
+  if (!in_range(cfg->out_stride, 128, 32768, 128))
+    return set_error(H3_ERR_CONFIG, "%s: out_stride %u outside [128, 32768] step 128", stage,
+                cfg->out_stride);
+  if (!in_range(cfg->tokens, 1, 1048576))
+    return set_error(H3_ERR_CONFIG, "%s: tokens %u outside [1, 1048576]", stage, cfg->tokens);
+  if (!in_range(cfg->token_capacity, 32, 1048576, 16))
+    return set_error(H3_ERR_CONFIG, "%s: token_capacity %u outside [32, 1048576] step 16", stage,
+                cfg->token_capacity);
+  if (cfg->tokens > cfg->token_capacity)
+    return set_error(H3_ERR_CONFIG, "%s: tokens %u exceed token_capacity %u", stage, cfg->tokens,
+                cfg->token_capacity);
+  if (token_count < 1 || token_count > cfg->tokens)
+    return set_error(H3_ERR_ARGUMENT, "%s: token_count %u outside [1, tokens=%u]", stage, token_count,
+                cfg->tokens);
+  if (heads < 1 || heads > 65535)
+    return set_error(H3_ERR_ARGUMENT, "%s: heads %u outside [1, 65535]", stage, heads);
+  const size_t cap = cfg->token_capacity;
+  const size_t head_limit = cfg->out_stride / 128, kv_head_limit = cfg->kv_stride / 128;
+  if (cfg->q_stride / 128 < head_limit)
+    return set_error(H3_ERR_CONFIG, "%s: q_stride %u holds fewer heads than out_stride %u", stage,
+                cfg->q_stride, cfg->out_stride);
+  // The extents the kernel addresses: head-major views [head_limit*cap][32] i32 and
+  // [head_limit][cap] f32 (attention_i8qkhm...loom:394-401); token-major views
+  // [cap][q_stride/4] i32 and [cap][head_limit] f32 (attention_i8qk_family.loom:117-121).
+  size_t need[6];
+  if (head_major) {
+    need[0] = head_limit * cap * 128;
+    need[1] = head_limit * cap * 4;
+    need[2] = kv_head_limit * cap * 128;
+    need[3] = kv_head_limit * cap * 4;
+  } else {
+    need[0] = cap * cfg->q_stride;
+    need[1] = cap * head_limit * 4;
+    need[2] = cap * cfg->kv_stride;
+    need[3] = cap * kv_head_limit * 4;
+  }
+  need[4] = (size_t)cfg->kv_stride * cap * 2;
+  need[5] = (size_t)token_count * cfg->out_stride * 2;
+  h3_view views[6] = {qi, qs, ki, ks, vt, out};
+  int st = check_bindings(stage, views, need, 6);
+  if (st) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_attention(*cfg, head_major, token_count, heads,
+                                          static_cast<const int32_t*>(qi.ptr),
+                                          static_cast<const float*>(qs.ptr),
+                                          static_cast<const int32_t*>(ki.ptr),
+                                          static_cast<const float*>(ks.ptr),
+                                          static_cast<const uint16_t*>(vt.ptr),
+                                          static_cast<uint16_t*>(out.ptr), stream));
+}
+
+int transpose_common(const char* stage, const h3_transpose_cfg* cfg, uint32_t launch_rows,
+                     uint32_t rows, h3_view x, h3_view out, hipStream_t stream, bool qkv) {
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  // kernels/transpose_f16.loom:7-9
+  if (!in_range(cfg->width, 32, 65536, 32))
+    return set_error(H3_ERR_CONFIG, "%s: width %u outside [32, 65536] step 32", stage, cfg->width);
+  if (!in_range(cfg->row_capacity, 32, 1048576, 32))
+    return set_error(H3_ERR_CONFIG, "%s: row_capacity %u outside [32, 1048576] step 32", stage,
+                cfg->row_capacity);
+  if (cfg->elem != H3_ELEM_F16 && cfg->elem != H3_ELEM_BF16)
+    return set_error(H3_ERR_CONFIG, "%s: unknown element format %u", stage, cfg->elem);
+  // range(%rows, 1, 1048576), le(%rows, %cap) (transpose_f16.loom in-file 34)
+  if (rows < 1 || rows > cfg->row_capacity || launch_rows < rows ||
+      launch_rows > cfg->row_capacity)
+    return set_error(H3_ERR_ARGUMENT, "%s: rows %u / launch_rows %u outside [1, row_capacity=%u]",
+                stage, rows, launch_rows, cfg->row_capacity);
+  const uint32_t stride = qkv ? 3 * cfg->width : cfg->width;
+  h3_view views[2] = {x, out};
+  size_t need[2] = {(size_t)rows * stride * 2, (size_t)cfg->width * cfg->row_capacity * 2};
+  int st = check_bindings(stage, views, need, 2);
+  if (st) return st;
+  if ((st = device_ready(stage))) return st;
+  const uint32_t tile = (qkv && cfg->width % 64 == 0) ? 64 : 32;
+  return launched(stage, launch_transpose(cfg->width, cfg->row_capacity, stride,
+                                          qkv ? 2 * cfg->width : 0, cfg->elem, tile, launch_rows,
+                                          rows, x.ptr, static_cast<uint16_t*>(out.ptr), stream));
+}
+
+}  // namespace
+}  // namespace h3
+
+using namespace h3;
+
+extern "C" {
+
+const char* h3_last_error(void) { return g_error_ref().c_str(); }
+
+const char* h3_version(void) { return "h3attn 0.1.0 gfx950"; }
+
+int h3_prepare_qk_i8(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x, h3_view mean,
+                     h3_view codes, h3_view scales, h3_stream stream) {
+  return prepare_common("prepare_qk_i8", cfg, tokens, x, mean, codes, scales,
+                        reinterpret_cast<hipStream_t>(stream), false);
+}
+
+int h3_prepare_qk_i8hm(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x, h3_view mean,
+                       h3_view codes, h3_view scales, h3_stream stream) {
+  return prepare_common("prepare_qk_i8hm", cfg, tokens, x, mean, codes, scales,
+                        reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int h3_prepare_qk_rope_i8hm(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x,
+                            h3_view weight, h3_view cos_t, h3_view sin_t, h3_view codes,
+                            h3_view scales, h3_stream stream) {
+  const char* stage = "prepare_qk_rope_i8hm";
+  int st = check_prepare_cfg(stage, cfg, tokens, true);
+  if (st) return st;
+  if ((st = rope_bindings(stage, cfg, tokens, x, weight, cos_t, sin_t))) return st;
+  const size_t rows_out = (size_t)cfg->heads * cfg->token_capacity;
+  h3_view views[2] = {codes, scales};
+  size_t need[2] = {rows_out * 128, rows_out * 4};
+  if ((st = check_bindings(stage, views, need, 2))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_prepare_qk_rope(
+                             *cfg, tokens, x.ptr, static_cast<const float*>(weight.ptr),
+                             static_cast<const float*>(cos_t.ptr),
+                             static_cast<const float*>(sin_t.ptr),
+                             static_cast<int32_t*>(codes.ptr), static_cast<float*>(scales.ptr),
+                             reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_prepare_k_rope_smooth_i8hm(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x,
+                                  h3_view weight, h3_view cos_t, h3_view sin_t, h3_view mean,
+                                  h3_view codes, h3_view scales, h3_stream stream) {
+  const char* stage = "prepare_k_rope_smooth_i8hm";
+  int st = check_prepare_cfg(stage, cfg, tokens, true);
+  if (st) return st;
+  if ((st = rope_bindings(stage, cfg, tokens, x, weight, cos_t, sin_t))) return st;
+  const size_t rows_out = (size_t)cfg->heads * cfg->token_capacity;
+  h3_view views[3] = {mean, codes, scales};
+  size_t need[3] = {(size_t)cfg->heads * 128 * 4, rows_out * 128, rows_out * 4};
+  if ((st = check_bindings(stage, views, need, 3))) return st;
+  if ((st = device_ready(stage))) return st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = launch_rope_colmean(*cfg, tokens, x.ptr, static_cast<const float*>(weight.ptr),
+                                     static_cast<const float*>(cos_t.ptr),
+                                     static_cast<const float*>(sin_t.ptr),
+                                     static_cast<float*>(mean.ptr), s);
+  if (e != hipSuccess) return launched(stage, e);
+  return launched(stage, launch_prepare_qk_rope_mean(
+                             *cfg, tokens, x.ptr, static_cast<const float*>(weight.ptr),
+                             static_cast<const float*>(cos_t.ptr),
+                             static_cast<const float*>(sin_t.ptr),
+                             static_cast<const float*>(mean.ptr),
+                             static_cast<int32_t*>(codes.ptr), static_cast<float*>(scales.ptr), s));
+}
+
+int h3_rope_qknorm_f16(const h3_rope_cfg* cfg, uint32_t tokens, h3_view x, h3_view qweight,
+                       h3_view kweight, h3_view cos_t, h3_view sin_t, h3_view q_out,
+                       h3_view k_out, h3_view v_out, h3_stream stream) {
+  const char* stage = "rope_qknorm_f16";
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  if (!in_range(cfg->row_stride, 128, 65536, 128) || !in_range(cfg->heads, 1, 256) ||
+      !in_range(cfg->kv_heads, 1, 256) || !in_range(cfg->k_offset, 0, 65536, 128) ||
+      cfg->elem > H3_ELEM_BF16)
+    return set_error(H3_ERR_CONFIG, "%s: config outside the declared ranges", stage);
+  const uint64_t end = (uint64_t)cfg->k_offset + 128ull * cfg->kv_heads * (cfg->copy_v ? 2 : 1);
+  if (128ull * cfg->heads > cfg->k_offset || end > cfg->row_stride)
+    return set_error(H3_ERR_CONFIG, "%s: heads/kv_heads/k_offset exceed row_stride %u", stage,
+                cfg->row_stride);
+  if (!in_range(tokens, 1, 1048576))
+    return set_error(H3_ERR_ARGUMENT, "%s: tokens %u outside [1, 1048576]", stage, tokens);
+  h3_view views[8] = {x, qweight, kweight, cos_t, sin_t, q_out, k_out, v_out};
+  size_t need[8] = {(size_t)tokens * cfg->row_stride * 2,
+                    128 * 4,
+                    128 * 4,
+                    (size_t)tokens * 48 * 4,
+                    (size_t)tokens * 48 * 4,
+                    (size_t)tokens * cfg->heads * 128 * 2,
+                    (size_t)tokens * cfg->kv_heads * 128 * 2,
+                    cfg->copy_v ? (size_t)tokens * cfg->kv_heads * 128 * 2 : 0};
+  int st = check_bindings(stage, views, need, 8);
+  if (st) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_rope_qknorm(
+                             *cfg, tokens, x.ptr, static_cast<const float*>(qweight.ptr),
+                             static_cast<const float*>(kweight.ptr),
+                             static_cast<const float*>(cos_t.ptr),
+                             static_cast<const float*>(sin_t.ptr),
+                             static_cast<uint16_t*>(q_out.ptr), static_cast<uint16_t*>(k_out.ptr),
+                             static_cast<uint16_t*>(v_out.ptr),
+                             reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_colmean_f32(uint32_t width, uint32_t elem, uint32_t tokens, h3_view x, h3_view mean,
+                   h3_stream stream) {
+  const char* stage = "colmean_f32";
+  // kernels/colmean_f32.loom:5
+  if (!in_range(width, 256, 65536, 256))
+    return set_error(H3_ERR_CONFIG, "%s: width %u outside [256, 65536] step 256", stage, width);
+  if (elem > H3_ELEM_BF16) return set_error(H3_ERR_CONFIG, "%s: unknown element format", stage);
+  if (!in_range(tokens, 1, 1048576))
+    return set_error(H3_ERR_ARGUMENT, "%s: tokens %u outside [1, 1048576]", stage, tokens);
+  h3_view views[2] = {x, mean};
+  size_t need[2] = {(size_t)tokens * width * 2, (size_t)width * 4};
+  int st = check_bindings(stage, views, need, 2);
+  if (st) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_colmean(width, width, elem, tokens, x.ptr,
+                                        static_cast<float*>(mean.ptr),
+                                        reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_transpose_f16(const h3_transpose_cfg* cfg, uint32_t launch_rows, uint32_t rows, h3_view x,
+                     h3_view out, h3_stream stream) {
+  return transpose_common("transpose_f16", cfg, launch_rows, rows, x, out,
+                          reinterpret_cast<hipStream_t>(stream), false);
+}
+
+int h3_transpose_qkv_v_f16(const h3_transpose_cfg* cfg, uint32_t launch_rows, uint32_t rows,
+                           h3_view x, h3_view out, h3_stream stream) {
+  return transpose_common("transpose_qkv_v_f16", cfg, launch_rows, rows, x, out,
+                          reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int h3_attention_i8qkhm(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                        h3_stream stream) {
+  return attention_common("attention_i8qkhm", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int h3_attention_i8qk(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                      h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                      h3_stream stream) {
+  return attention_common("attention_i8qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), false);
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+// Internal declarations shared by the HIP translation units of libh3attn.
+// Device helpers for 16-bit activations and the launchers behind the C ABI in include/h3attn.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/h3attn.h"
+
+namespace h3 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// Widen four 16-bit activations (f16 or bf16 bit patterns held in two dwords) to f32 exactly.
+__device__ __forceinline__ v4f widen4(uint2 bits, int elem) {
+  v4f out;
+  if (elem == H3_ELEM_BF16) {
+    out[0] = __uint_as_float(bits.x << 16);
+    out[1] = __uint_as_float(bits.x & 0xffff0000u);
+    out[2] = __uint_as_float(bits.y << 16);
+    out[3] = __uint_as_float(bits.y & 0xffff0000u);
+  } else {
+    v4h h = __builtin_bit_cast(v4h, bits);
+    out[0] = (float)h[0];
+    out[1] = (float)h[1];
+    out[2] = (float)h[2];
+    out[3] = (float)h[3];
+  }
+  return out;
+}
+
+// Records `msg` for h3_last_error() and returns `status` (abi.cpp).
+int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Launchers (host). Shapes and bindings are validated by the caller (abi.cpp).
+hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int head_major,
+                             const void* x, const float* mean, int32_t* codes, float* scales,
+                             hipStream_t stream);
+hipError_t launch_prepare_qk_rope(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                                  const float* weight, const float* cos_t, const float* sin_t,
+                                  int32_t* codes, float* scales, hipStream_t stream);
+hipError_t launch_rope_qknorm(const h3_rope_cfg& cfg, uint32_t tokens, const void* x,
+                              const float* qweight, const float* kweight, const float* cos_t,
+                              const float* sin_t, uint16_t* q_out, uint16_t* k_out,
+                              uint16_t* v_out, hipStream_t stream);
+hipError_t launch_colmean(uint32_t width, uint32_t row_stride, uint32_t elem, uint32_t tokens,
+                          const void* x, float* mean, hipStream_t stream);
+hipError_t launch_rope_colmean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                               const float* weight, const float* cos_t, const float* sin_t,
+                               float* mean, hipStream_t stream);
+hipError_t launch_prepare_qk_rope_mean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                                       const float* weight, const float* cos_t,
+                                       const float* sin_t, const float* mean, int32_t* codes,
+                                       float* scales, hipStream_t stream);
+hipError_t launch_transpose(uint32_t width, uint32_t row_capacity, uint32_t row_stride,
+                            uint32_t col_offset, uint32_t elem, uint32_t tile, uint32_t launch_rows,
+                            uint32_t rows, const void* x, uint16_t* out, hipStream_t stream);
+hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_t token_count,
+                            uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
+                            const float* ks, const uint16_t* vt, uint16_t* out,
+                            hipStream_t stream);
+
+}  // namespace h3

@@ -1,0 +1,415 @@
+// Operand preparation for INT8 attention on gfx950: Hadamard-rotated per-(token, head) INT8
+// quantisation, the fused RMSNorm + RoPE variant, the f16 RoPE kernel, K column means and the
+// V transposes. All of these are HBM-bound byte work: each (token, head) row of 128 channels is
+// handled by one 32-lane half of a wave64 (four channels per lane, one 8-byte load per lane),
+// so a 256-thread workgroup covers eight rows and every global access is a full 256-byte row.
+//
+// The arithmetic is built with -ffp-contract=off: every float operation below is one IEEE
+// operation in the order written, which is what makes the quantizer bit-exact with the
+// reference's fp32 op order (kernels/prepare_qk_i8.loom:63-188).
+#include "internal.hpp"
+
+namespace h3 {
+namespace {
+
+constexpr int kRowsPerBlock = 8;  // 256 threads = 8 half-waves = 8 (token, head) rows
+
+// Butterfly partner exchange inside a 32-lane half-wave.
+__device__ __forceinline__ float xor32(float v, int mask) { return __shfl_xor(v, mask, 32); }
+
+// The unnormalised Sylvester Hadamard H_128 over the 32 lanes of a half-wave, lane l holding
+// elements 4l..4l+3, in the reference's fp32 order (kernels/prepare_qk_i8.loom:84-156):
+// an in-lane stage over element bits 0-1, then lane butterflies k = 1, 2, 4, 8, 16 where the
+// lane with bit k clear keeps s + partner and the lane with bit k set keeps partner - s.
+__device__ __forceinline__ v4f hadamard128(v4f y, int lane) {
+  float ab_p = y[0] + y[1], ab_m = y[0] - y[1];
+  float cd_p = y[2] + y[3], cd_m = y[2] - y[3];
+  v4f s;
+  s[0] = ab_p + cd_p;
+  s[1] = ab_m + cd_m;
+  s[2] = ab_p - cd_p;
+  s[3] = ab_m - cd_m;
+#pragma unroll
+  for (int k = 1; k < 32; k <<= 1) {
+    const bool hi = (lane & k) != 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float p = xor32(s[j], k);
+      s[j] = hi ? (p - s[j]) : (s[j] + p);
+    }
+  }
+  return s;
+}
+
+// Quantise one rotated row (kernels/prepare_qk_i8.loom:157-188): amax over the half-wave,
+// sc = amax/127, inv = 127/amax (correctly rounded divisions), codes = clamp(rne(r*inv), +-127)
+// packed low byte first. Returns the packed word of this lane; *scale gets amax/127 * extra.
+__device__ __forceinline__ uint32_t quantize_row(v4f r, float extra, float* scale) {
+  float m = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
+#pragma unroll
+  for (int k = 16; k >= 1; k >>= 1) m = fmaxf(m, xor32(m, k));
+  float amax = fmaxf(m, 1.0000000000000001e-30f);
+  float sc = amax / 127.0f;
+  float inv = 127.0f / amax;
+  uint32_t word = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float q = __builtin_rintf(r[j] * inv);
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    word |= ((uint32_t)(int)q & 0xffu) << (8 * j);
+  }
+  *scale = sc * extra;
+  return word;
+}
+
+__device__ __forceinline__ uint2 load4(const void* base, size_t elem_index) {
+  return *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + elem_index);
+}
+
+// Per-head RMSNorm(weight, eps) + rotate-half RoPE on channels < 96, rounded to f16 and widened
+// back, in this build's fixed fp32 order: lane partial ((v0^2 + v1^2) + v2^2) + v3^2, butterfly
+// sum over lanes k = 1..16, mean = ss/128, r = 1/sqrt(mean + eps) (two correctly rounded
+// operations), xn = (v*r)*w, then lanes 0-11 (channels 0-47) out = xn*cos - xn_{+48}*sin,
+// lanes 12-23 (channels 48-95) out = xn*cos + xn_{-48}*sin, lanes 24-31 out = xn.
+// The maths is the reference's (kernels/prepare_qk_rope_i8hm.loom:110-130,
+// kernels/rope_qknorm_f16.loom); the device code is shared by every kernel that needs it, so
+// fused and separate routes produce identical bits.
+__device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* weight,
+                                                const float* cos_row, const float* sin_row,
+                                                float eps) {
+  float part = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
+#pragma unroll
+  for (int k = 1; k < 32; k <<= 1) part = part + xor32(part, k);
+  float ms = part * 0.0078125f;
+  float me = ms + eps;
+  float r = 1.0f / __builtin_sqrtf(me);
+  const float4 w = *reinterpret_cast<const float4*>(weight + 4 * lane);
+  v4f xn;
+  xn[0] = (v[0] * r) * w.x;
+  xn[1] = (v[1] * r) * w.y;
+  xn[2] = (v[2] * r) * w.z;
+  xn[3] = (v[3] * r) * w.w;
+  const bool lo = lane < 12, pair = lane < 24;
+  const int partner = lo ? lane + 12 : (pair ? lane - 12 : lane);
+  const int pairlane = lo ? lane : (pair ? lane - 12 : 0);
+  v4f px;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) px[j] = __shfl(xn[j], partner, 32);
+  const float4 c = *reinterpret_cast<const float4*>(cos_row + 4 * pairlane);
+  const float4 s = *reinterpret_cast<const float4*>(sin_row + 4 * pairlane);
+  const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
+  v4f out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float a = xn[j] * cc[j];
+    float b = px[j] * ss[j];
+    float o = lo ? (a - b) : (a + b);
+    o = pair ? o : xn[j];
+    out[j] = (float)(_Float16)o;
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------- quantizer kernels
+
+template <bool kHeadMajor>
+__global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
+                                                    const float* __restrict__ mean,
+                                                    int32_t* __restrict__ codes,
+                                                    float* __restrict__ scales, uint32_t tokens,
+                                                    uint32_t row_stride, uint32_t head_offset,
+                                                    uint32_t heads, uint32_t capacity,
+                                                    float extra, uint32_t elem) {
+  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  if (row >= tokens * heads) return;
+  // head-major rows walk tokens fastest (contiguous code stores), token-major rows walk heads
+  const uint32_t t = kHeadMajor ? row % tokens : row / heads;
+  const uint32_t h = kHeadMajor ? row / tokens : row % heads;
+  const uint32_t col = head_offset + 128u * h + 4u * lane;
+  v4f y = widen4(load4(x, (size_t)t * row_stride + col), elem);
+  if (mean) {
+    const float4 m = *reinterpret_cast<const float4*>(mean + col);
+    y[0] = y[0] - m.x;
+    y[1] = y[1] - m.y;
+    y[2] = y[2] - m.z;
+    y[3] = y[3] - m.w;
+  }
+  v4f r = hadamard128(y, lane);
+  float scale;
+  uint32_t word = quantize_row(r, extra, &scale);
+  size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
+  codes[out_row * 32 + lane] = (int32_t)word;
+  if (lane == 0) scales[out_row] = scale;
+}
+
+// RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
+// (kernels/prepare_qk_rope_i8hm.loom:94-239; mean == nullptr is the reference's unsmoothed
+// kernel, a mean is this build's fused K-smoothing second pass).
+__global__ __launch_bounds__(256) void k_prepare_qk_rope(
+    const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const float* __restrict__ mean, int32_t* __restrict__ codes,
+    float* __restrict__ scales, uint32_t tokens, uint32_t row_stride, uint32_t head_offset,
+    uint32_t heads, uint32_t capacity, float extra, float eps, uint32_t elem) {
+  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  if (row >= tokens * heads) return;
+  const uint32_t t = row % tokens;
+  const uint32_t h = row / tokens;
+  const uint32_t col = head_offset + 128u * h + 4u * lane;
+  v4f v = widen4(load4(x, (size_t)t * row_stride + col), elem);
+  v4f y = rmsnorm_rope_f16(v, lane, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48, eps);
+  if (mean) {
+    const float4 m = *reinterpret_cast<const float4*>(mean + 128u * h + 4u * lane);
+    y[0] = y[0] - m.x;
+    y[1] = y[1] - m.y;
+    y[2] = y[2] - m.z;
+    y[3] = y[3] - m.w;
+  }
+  v4f r = hadamard128(y, lane);
+  float scale;
+  uint32_t word = quantize_row(r, extra, &scale);
+  size_t out_row = (size_t)h * capacity + t;
+  codes[out_row * 32 + lane] = (int32_t)word;
+  if (lane == 0) scales[out_row] = scale;
+}
+
+// RMSNorm + RoPE of Q and K heads to f16, V optionally copied (kernels/rope_qknorm_f16.loom).
+// Rows are (token, head) over heads + kv_heads (+ kv_heads copy rows).
+__global__ __launch_bounds__(256) void k_rope_qknorm(
+    const void* __restrict__ x, const float* __restrict__ qweight,
+    const float* __restrict__ kweight, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out,
+    uint16_t* __restrict__ v_out, uint32_t tokens, uint32_t row_stride, uint32_t heads,
+    uint32_t kv_heads, uint32_t k_offset, float eps, uint32_t elem, uint32_t copy_v) {
+  const uint32_t per_token = heads + kv_heads + (copy_v ? kv_heads : 0);
+  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  if (row >= tokens * per_token) return;
+  const uint32_t t = row / per_token;
+  const uint32_t j = row % per_token;
+  if (j >= heads + kv_heads) {  // V copy: bits unchanged (bf16 input is rounded to f16)
+    const uint32_t vh = j - heads - kv_heads;
+    const uint32_t col = k_offset + 128u * kv_heads + 128u * vh + 4u * lane;
+    uint2 bits = load4(x, (size_t)t * row_stride + col);
+    if (elem == H3_ELEM_BF16) {
+      v4f f = widen4(bits, elem);
+      v4h hv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+      bits = __builtin_bit_cast(uint2, hv);
+    }
+    *reinterpret_cast<uint2*>(v_out + (size_t)t * kv_heads * 128 + 128u * vh + 4u * lane) = bits;
+    return;
+  }
+  const bool is_q = j < heads;
+  const uint32_t h = is_q ? j : j - heads;
+  const uint32_t col = (is_q ? 0u : k_offset) + 128u * h + 4u * lane;
+  v4f v = widen4(load4(x, (size_t)t * row_stride + col), elem);
+  v4f o = rmsnorm_rope_f16(v, lane, is_q ? qweight : kweight, cos_t + (size_t)t * 48,
+                           sin_t + (size_t)t * 48, eps);
+  v4h hv = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+  uint16_t* dst = is_q ? q_out + (size_t)t * heads * 128 : k_out + (size_t)t * kv_heads * 128;
+  *reinterpret_cast<v4h*>(dst + 128u * h + 4u * lane) = hv;
+}
+
+// ---------------------------------------------------------------- column means
+
+// mean[c] = (sum_t x[t][c]) / tokens, one lane per column summing tokens in order
+// (kernels/colmean_f32.loom in-file 30-40). Eight loads are issued ahead of the dependent adds.
+__global__ __launch_bounds__(64) void k_colmean(const void* __restrict__ x,
+                                                float* __restrict__ mean, uint32_t tokens,
+                                                uint32_t width, uint32_t row_stride,
+                                                uint32_t elem) {
+  const uint32_t c = blockIdx.x * 64 + threadIdx.x;
+  if (c >= width) return;
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(x) + c;
+  float acc = 0.0f;
+  uint32_t t = 0;
+  constexpr int kAhead = 16;
+  for (; t + kAhead <= tokens; t += kAhead) {
+    uint16_t v[kAhead];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) v[i] = p[(size_t)(t + i) * row_stride];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i)
+      acc = acc + (elem == H3_ELEM_BF16 ? __uint_as_float((uint32_t)v[i] << 16)
+                                        : (float)__builtin_bit_cast(_Float16, v[i]));
+  }
+  for (; t < tokens; ++t) {
+    uint16_t v = p[(size_t)t * row_stride];
+    acc = acc + (elem == H3_ELEM_BF16 ? __uint_as_float((uint32_t)v << 16)
+                                      : (float)__builtin_bit_cast(_Float16, v));
+  }
+  mean[c] = acc / (float)tokens;
+}
+
+// First pass of the fused K smoothing: the column mean of RMSNorm+RoPE(K) rounded to f16, over
+// all tokens, in sequential fp32 order per column. One workgroup per head: its eight half-waves
+// rotate 32 tokens of that head into LDS, then 128 lanes add their column in token order.
+__global__ __launch_bounds__(256) void k_rope_colmean(
+    const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, float* __restrict__ mean, uint32_t tokens,
+    uint32_t row_stride, uint32_t head_offset, float eps, uint32_t elem) {
+  constexpr int kStep = 32;
+  __shared__ float tile[kStep][128 + 4];
+  const uint32_t h = blockIdx.x;
+  const int half = threadIdx.x >> 5, lane = threadIdx.x & 31;
+  const uint32_t col = head_offset + 128u * h + 4u * lane;
+  float acc = 0.0f;
+  for (uint32_t t0 = 0; t0 < tokens; t0 += kStep) {
+#pragma unroll
+    for (int i = 0; i < kStep / kRowsPerBlock; ++i) {
+      const int tt = i * kRowsPerBlock + half;
+      const uint32_t t = t0 + tt;
+      if (t < tokens) {
+        v4f v = widen4(load4(x, (size_t)t * row_stride + col), elem);
+        v4f o = rmsnorm_rope_f16(v, lane, weight, cos_t + (size_t)t * 48,
+                                 sin_t + (size_t)t * 48, eps);
+        *reinterpret_cast<float4*>(&tile[tt][4 * lane]) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < 128) {
+      const uint32_t n = min((uint32_t)kStep, tokens - t0);
+      for (uint32_t i = 0; i < n; ++i) acc = acc + tile[i][threadIdx.x];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < 128) mean[128u * h + threadIdx.x] = acc / (float)tokens;
+}
+
+// ---------------------------------------------------------------- transposes
+
+// x [rows][row_stride] (width columns at col_offset) -> out [width][capacity] f16 through a
+// 64x64 LDS tile (rows padded to 66 halves). Output columns [rows, clear_to) are zeroed,
+// columns >= clear_to are left alone (kernels/transpose_f16.loom, transpose_qkv_v_f16.loom).
+__global__ __launch_bounds__(256) void k_transpose(const uint16_t* __restrict__ x,
+                                                   uint16_t* __restrict__ out, uint32_t rows,
+                                                   uint32_t clear_to, uint32_t width,
+                                                   uint32_t capacity, uint32_t row_stride,
+                                                   uint32_t col_offset, uint32_t elem) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const uint32_t c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  // load: 64 rows x 64 columns, lane -> row i/16 (+16k), columns 4*(i%16)..+3
+  const int lr = threadIdx.x >> 4, lc = (threadIdx.x & 15) * 4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t r = r0 + lr + 16 * k;
+    const uint32_t c = c0 + lc;
+    uint16_t v[4] = {0, 0, 0, 0};
+    if (r < rows && c < width) {
+      uint2 bits = *reinterpret_cast<const uint2*>(x + (size_t)r * row_stride + col_offset + c);
+      if (elem == H3_ELEM_BF16) {
+        v4f f = widen4(bits, elem);
+        v4h hv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
+        bits = __builtin_bit_cast(uint2, hv);
+      }
+      v[0] = bits.x & 0xffff;
+      v[1] = bits.x >> 16;
+      v[2] = bits.y & 0xffff;
+      v[3] = bits.y >> 16;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile[lr + 16 * k][lc + j] = v[j];
+  }
+  __syncthreads();
+  // store: output row (channel) c0 + i/16 (+16k), output columns r0 + 4*(i%16)..+3
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t oc = c0 + lr + 16 * k;
+    const uint32_t orow = r0 + lc;
+    if (oc >= width) continue;
+    uint16_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = tile[lc + j][lr + 16 * k];
+    uint16_t* dst = out + (size_t)oc * capacity + orow;
+    if (orow + 4 <= clear_to) {
+      *reinterpret_cast<uint2*>(dst) =
+          make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (orow + j < clear_to) dst[j] = v[j];
+    }
+  }
+}
+
+inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int head_major,
+                             const void* x, const float* mean, int32_t* codes, float* scales,
+                             hipStream_t stream) {
+  const uint32_t rows = tokens * cfg.heads;
+  dim3 grid(div_up(rows, kRowsPerBlock));
+  if (head_major)
+    hipLaunchKernelGGL(k_prepare_qk<true>, grid, dim3(256), 0, stream, x, mean, codes, scales,
+                       tokens, cfg.row_stride, cfg.head_offset, cfg.heads, cfg.token_capacity,
+                       cfg.extra_scale, cfg.elem);
+  else
+    hipLaunchKernelGGL(k_prepare_qk<false>, grid, dim3(256), 0, stream, x, mean, codes, scales,
+                       tokens, cfg.row_stride, cfg.head_offset, cfg.heads, 0u, cfg.extra_scale,
+                       cfg.elem);
+  return hipGetLastError();
+}
+
+hipError_t launch_prepare_qk_rope(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                                  const float* weight, const float* cos_t, const float* sin_t,
+                                  int32_t* codes, float* scales, hipStream_t stream) {
+  return launch_prepare_qk_rope_mean(cfg, tokens, x, weight, cos_t, sin_t, nullptr, codes, scales,
+                                     stream);
+}
+
+hipError_t launch_prepare_qk_rope_mean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                                       const float* weight, const float* cos_t,
+                                       const float* sin_t, const float* mean, int32_t* codes,
+                                       float* scales, hipStream_t stream) {
+  const uint32_t rows = tokens * cfg.heads;
+  hipLaunchKernelGGL(k_prepare_qk_rope, dim3(div_up(rows, kRowsPerBlock)), dim3(256), 0, stream,
+                     x, weight, cos_t, sin_t, mean, codes, scales, tokens, cfg.row_stride,
+                     cfg.head_offset, cfg.heads, cfg.token_capacity, cfg.extra_scale, cfg.eps,
+                     cfg.elem);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_qknorm(const h3_rope_cfg& cfg, uint32_t tokens, const void* x,
+                              const float* qweight, const float* kweight, const float* cos_t,
+                              const float* sin_t, uint16_t* q_out, uint16_t* k_out,
+                              uint16_t* v_out, hipStream_t stream) {
+  const uint32_t per_token = cfg.heads + cfg.kv_heads + (cfg.copy_v ? cfg.kv_heads : 0);
+  hipLaunchKernelGGL(k_rope_qknorm, dim3(div_up(tokens * per_token, kRowsPerBlock)), dim3(256), 0,
+                     stream, x, qweight, kweight, cos_t, sin_t, q_out, k_out, v_out, tokens,
+                     cfg.row_stride, cfg.heads, cfg.kv_heads, cfg.k_offset, cfg.eps, cfg.elem,
+                     cfg.copy_v);
+  return hipGetLastError();
+}
+
+hipError_t launch_colmean(uint32_t width, uint32_t row_stride, uint32_t elem, uint32_t tokens,
+                          const void* x, float* mean, hipStream_t stream) {
+  hipLaunchKernelGGL(k_colmean, dim3(div_up(width, 64)), dim3(64), 0, stream, x, mean, tokens,
+                     width, row_stride, elem);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_colmean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                               const float* weight, const float* cos_t, const float* sin_t,
+                               float* mean, hipStream_t stream) {
+  hipLaunchKernelGGL(k_rope_colmean, dim3(cfg.heads), dim3(256), 0, stream, x, weight, cos_t,
+                     sin_t, mean, tokens, cfg.row_stride, cfg.head_offset, cfg.eps, cfg.elem);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose(uint32_t width, uint32_t row_capacity, uint32_t row_stride,
+                            uint32_t col_offset, uint32_t elem, uint32_t tile, uint32_t launch_rows,
+                            uint32_t rows, const void* x, uint16_t* out, hipStream_t stream) {
+  uint32_t clear_to = div_up(launch_rows, tile) * tile;
+  if (clear_to > row_capacity) clear_to = row_capacity;
+  if (clear_to == 0) return hipSuccess;
+  dim3 grid(div_up(width, 64), div_up(clear_to, 64));
+  hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, stream,
+                     reinterpret_cast<const uint16_t*>(x), out, rows, clear_to, width,
+                     row_capacity, row_stride, col_offset, elem);
+  return hipGetLastError();
+}
+
+}  // namespace h3

@@ -1,0 +1,305 @@
+"""Python binding of libh3attn (the C ABI in include/h3attn.h) over torch device tensors.
+
+This is the host-side mirror used by the tests and the benchmark: each function takes torch
+tensors already resident on the GPU, passes their device pointers and byte lengths to the C ABI,
+and enqueues on torch's current stream. The library is required: importing works without a
+GPU, but every call needs the built libh3attn.so and fails loudly without it; there is no CPU
+fallback anywhere in this package.
+
+Function names and arguments follow the reference's kernels (kernels/*.loom in h3-hrx) and
+their host call sites (src/stack.rs), e.g. prepare_qk_i8hm(cfg, tokens, x, mean, codes, scales).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import pathlib
+from typing import Optional
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE.parent / "libh3attn.so"
+
+H3_OK, H3_ERR_BINDING, H3_ERR_CONFIG, H3_ERR_ARGUMENT, H3_ERR_LAUNCH, H3_ERR_NO_DEVICE = range(6)
+H3_ELEM_F16, H3_ELEM_BF16 = 0, 1
+STATUS_NAMES = {0: "ok", 1: "binding", 2: "config", 3: "argument", 4: "launch", 5: "no device"}
+
+
+class H3Error(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{STATUS_NAMES.get(status, status)}] {message}")
+        self.status = status
+        self.message = message
+
+
+class View(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("bytes", ctypes.c_size_t)]
+
+
+class PrepareCfg(ctypes.Structure):
+    _fields_ = [
+        ("row_stride", ctypes.c_uint32),
+        ("head_offset", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("extra_scale", ctypes.c_float),
+        ("token_capacity", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("elem", ctypes.c_uint32),
+    ]
+
+
+class RopeCfg(ctypes.Structure):
+    _fields_ = [
+        ("row_stride", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("k_offset", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("copy_v", ctypes.c_uint32),
+        ("elem", ctypes.c_uint32),
+    ]
+
+
+class TransposeCfg(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_uint32),
+        ("row_capacity", ctypes.c_uint32),
+        ("elem", ctypes.c_uint32),
+    ]
+
+
+class AttentionCfg(ctypes.Structure):
+    _fields_ = [
+        ("q_stride", ctypes.c_uint32),
+        ("kv_stride", ctypes.c_uint32),
+        ("out_stride", ctypes.c_uint32),
+        ("tokens", ctypes.c_uint32),
+        ("token_capacity", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class StackDims(ctypes.Structure):
+    _fields_ = [
+        ("heads", ctypes.c_uint32),
+        ("tokens", ctypes.c_uint32),
+        ("eps", ctypes.c_float),
+        ("elem", ctypes.c_uint32),
+        ("ksmooth", ctypes.c_int),
+        ("fused", ctypes.c_int),
+    ]
+
+
+class IntQk(ctypes.Structure):
+    _fields_ = [
+        ("qi", View), ("ki", View), ("qs", View), ("ks", View),
+        ("kmean", View), ("zmean", View), ("vt", View), ("head_major", ctypes.c_int),
+    ]
+
+
+# (name, argtypes) of every exported entry point; restype is int unless noted.
+_P = ctypes.POINTER
+_S = ctypes.c_void_p
+SIGNATURES = {
+    "h3_last_error": ([], ctypes.c_char_p),
+    "h3_version": ([], ctypes.c_char_p),
+    "h3_prepare_qk_i8": ([_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
+    "h3_prepare_qk_i8hm": ([_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
+    "h3_prepare_qk_rope_i8hm": (
+        [_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_prepare_k_rope_smooth_i8hm": (
+        [_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_rope_qknorm_f16": (
+        [_P(RopeCfg), ctypes.c_uint32, View, View, View, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_colmean_f32": ([ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, View, View, _S], ctypes.c_int),
+    "h3_transpose_f16": ([_P(TransposeCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, _S], ctypes.c_int),
+    "h3_transpose_qkv_v_f16": (
+        [_P(TransposeCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, _S], ctypes.c_int),
+    "h3_attention_i8qkhm": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View, _S],
+        ctypes.c_int),
+    "h3_attention_i8qk": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View, _S],
+        ctypes.c_int),
+    "h3_capacity": ([ctypes.c_uint32, ctypes.c_int], ctypes.c_uint32),
+    "h3_stack_build": ([_P(StackDims), ctypes.c_void_p], ctypes.c_int),
+    "h3_stack_destroy": ([ctypes.c_void_p], None),
+    "h3_stack_capacity": ([ctypes.c_void_p], ctypes.c_uint32),
+    "h3_stack_attend_fused": (
+        [ctypes.c_void_p, ctypes.c_uint32, View, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_stack_attend": ([ctypes.c_void_p, ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
+    "h3_stack_operands": ([ctypes.c_void_p, _P(IntQk)], ctypes.c_int),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libh3attn.so (built in-tree by h3-hrx_amd/build.py). Raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().h3_last_error().decode()
+
+
+def check(status: int) -> None:
+    if status != H3_OK:
+        raise H3Error(status, last_error())
+
+
+def config_f32(v: float) -> float:
+    """compile::num's %.17g spelling parsed as f32 (src/compile.rs:38-83)."""
+    import numpy as np
+
+    return float(np.float32(float("%.17g" % v)))
+
+
+EXTRA_Q = config_f32(1.0 / math.sqrt(128.0) / 128.0)  # src/stack.rs:622-625
+
+
+# ------------------------------------------------------------------------- tensor plumbing
+
+def view(t) -> View:
+    """A binding of a torch tensor (any dtype): device pointer and byte length."""
+    if t is None:
+        return View(None, 0)
+    if hasattr(t, "data_ptr"):
+        if not t.is_contiguous():
+            raise ValueError("bindings must be contiguous")
+        return View(t.data_ptr(), t.numel() * t.element_size())
+    if isinstance(t, View):
+        return t
+    raise TypeError(f"cannot bind {type(t)}")
+
+
+def raw_view(ptr: int, nbytes: int) -> View:
+    return View(ptr, nbytes)
+
+
+def stream_ptr(stream=None) -> int:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def elem_of(t) -> int:
+    import torch
+
+    if t.dtype == torch.bfloat16:
+        return H3_ELEM_BF16
+    if t.dtype in (torch.float16, torch.int16, torch.uint16):
+        return H3_ELEM_F16
+    raise TypeError(f"activations must be f16 or bf16, not {t.dtype}")
+
+
+# ------------------------------------------------------------------------- entry points
+
+def prepare_qk_i8(cfg: PrepareCfg, tokens: int, x, mean, codes, scales, stream=None) -> None:
+    check(lib().h3_prepare_qk_i8(ctypes.byref(cfg), tokens, view(x), view(mean), view(codes),
+                                 view(scales), stream_ptr(stream)))
+
+
+def prepare_qk_i8hm(cfg: PrepareCfg, tokens: int, x, mean, codes, scales, stream=None) -> None:
+    check(lib().h3_prepare_qk_i8hm(ctypes.byref(cfg), tokens, view(x), view(mean), view(codes),
+                                   view(scales), stream_ptr(stream)))
+
+
+def prepare_qk_rope_i8hm(cfg: PrepareCfg, tokens: int, x, weight, cos_t, sin_t, codes, scales,
+                         stream=None) -> None:
+    check(lib().h3_prepare_qk_rope_i8hm(ctypes.byref(cfg), tokens, view(x), view(weight),
+                                        view(cos_t), view(sin_t), view(codes), view(scales),
+                                        stream_ptr(stream)))
+
+
+def prepare_k_rope_smooth_i8hm(cfg: PrepareCfg, tokens: int, x, weight, cos_t, sin_t, mean,
+                               codes, scales, stream=None) -> None:
+    check(lib().h3_prepare_k_rope_smooth_i8hm(ctypes.byref(cfg), tokens, view(x), view(weight),
+                                              view(cos_t), view(sin_t), view(mean), view(codes),
+                                              view(scales), stream_ptr(stream)))
+
+
+def rope_qknorm_f16(cfg: RopeCfg, tokens: int, x, qweight, kweight, cos_t, sin_t, q_out, k_out,
+                    v_out=None, stream=None) -> None:
+    check(lib().h3_rope_qknorm_f16(ctypes.byref(cfg), tokens, view(x), view(qweight),
+                                   view(kweight), view(cos_t), view(sin_t), view(q_out),
+                                   view(k_out), view(v_out), stream_ptr(stream)))
+
+
+def colmean_f32(width: int, tokens: int, x, mean, elem: int = H3_ELEM_F16, stream=None) -> None:
+    check(lib().h3_colmean_f32(width, elem, tokens, view(x), view(mean), stream_ptr(stream)))
+
+
+def transpose_f16(cfg: TransposeCfg, launch_rows: int, rows: int, x, out, stream=None) -> None:
+    check(lib().h3_transpose_f16(ctypes.byref(cfg), launch_rows, rows, view(x), view(out),
+                                 stream_ptr(stream)))
+
+
+def transpose_qkv_v_f16(cfg: TransposeCfg, launch_rows: int, rows: int, x, out,
+                        stream=None) -> None:
+    check(lib().h3_transpose_qkv_v_f16(ctypes.byref(cfg), launch_rows, rows, view(x), view(out),
+                                       stream_ptr(stream)))
+
+
+def attention_i8qkhm(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                     stream=None) -> None:
+    check(lib().h3_attention_i8qkhm(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                    view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
+
+
+def attention_i8qk(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                   stream=None) -> None:
+    check(lib().h3_attention_i8qk(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                  view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
+
+
+def capacity(tokens: int, causal: bool = False) -> int:
+    """src/stack.rs:299-302."""
+    return lib().h3_capacity(tokens, int(causal))
+
+
+class Stack:
+    """The INT8 attention block of the reference's Stack (src/stack.rs): build once, then
+    attend_fused (prepare_fused_operands + attention) or attend (the separate route)."""
+
+    def __init__(self, heads: int, tokens: int, eps: float = 1e-5, elem: int = H3_ELEM_F16,
+                 ksmooth: bool = False, fused: bool = True):
+        self.dims = StackDims(heads, tokens, eps, elem, int(ksmooth), int(fused))
+        handle = ctypes.c_void_p()
+        check(lib().h3_stack_build(ctypes.byref(self.dims), ctypes.byref(handle)))
+        self.handle = handle
+        self.capacity = lib().h3_stack_capacity(handle)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().h3_stack_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def attend_fused(self, t, fused, qnorm, knorm, cos_t, sin_t, out, stream=None) -> None:
+        check(lib().h3_stack_attend_fused(self.handle, t, view(fused), view(qnorm), view(knorm),
+                                          view(cos_t), view(sin_t), view(out), stream_ptr(stream)))
+
+    def attend(self, t, q, k, v, out, stream=None) -> None:
+        check(lib().h3_stack_attend(self.handle, t, view(q), view(k), view(v), view(out),
+                                    stream_ptr(stream)))
+
+    def operands(self) -> IntQk:
+        ops = IntQk()
+        check(lib().h3_stack_operands(self.handle, ctypes.byref(ops)))
+        return ops

@@ -1,0 +1,245 @@
+/*
+ * h3attn.h — C ABI of libh3attn: the MI355X (gfx950) INT8 attention path of h3-hrx.
+ *
+ * Each entry point replaces one reference kernel launch made through
+ * `dispatch::emit(sink, kernel, profile, stage, workload, scalars, bindings, required)`
+ * (reference src/dispatch.rs:254-316) on a kernel obtained from `Compiler::get`
+ * (src/compile.rs:320-326). A reference launch carries
+ *   - the kernel's config map (src/compile.rs:19-22)  -> the cfg struct of each entry point,
+ *   - the workload and device scalars                  -> the uint32_t arguments,
+ *   - bindings (buffer views) with required lengths    -> h3_view {pointer, bytes} arguments.
+ *
+ * Conventions, all mirroring the reference's contract:
+ *   - Pointers are device pointers. The library never allocates and never synchronises: work
+ *     is enqueued on `stream` in order (src/dispatch.rs:86-133) and may be captured in a graph.
+ *   - Before any launch every binding's byte length is checked against the extent the kernel
+ *     addresses; a short binding returns H3_ERR_BINDING and launches nothing
+ *     (src/dispatch.rs:264-276). h3_last_error() then reads
+ *     "{stage}: binding {i} is {n} bytes, the kernel addresses {need}".
+ *   - Config values outside the ranges the reference declares (`config.decl ... where [...]`
+ *     in each kernel .loom file) return H3_ERR_CONFIG and launch nothing.
+ *   - Activations are 16-bit: H3_ELEM_F16 as in the reference, or H3_ELEM_BF16 (an extension:
+ *     widened to f32 exactly, so the quantizer arithmetic is unchanged).
+ *   - Head-major operands: codes [heads][capacity][32] i32 (four int8 codes per word, low byte
+ *     first), scales [heads][capacity] f32. Token-major: codes [tokens][heads*32], scales
+ *     [tokens][heads]. Values: one fp32 scale per (token, head) = absmax/127 * extra_scale.
+ *   - V^T: [width][row_capacity] f16. Rows of the output past the token count are not written.
+ */
+#ifndef H3ATTN_H
+#define H3ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *h3_stream; /* hipStream_t; NULL is the default stream */
+
+/* A binding: a device buffer and its length in bytes (reference `View`, src/stack.rs:204-213). */
+typedef struct {
+  void *ptr;
+  size_t bytes;
+} h3_view;
+
+enum {
+  H3_OK = 0,
+  H3_ERR_BINDING = 1,  /* a binding is shorter than the extent the kernel addresses */
+  H3_ERR_CONFIG = 2,   /* a config value outside its declared range */
+  H3_ERR_ARGUMENT = 3, /* a workload/scalar argument outside its range, or a null pointer */
+  H3_ERR_LAUNCH = 4,   /* the HIP runtime refused the launch */
+  H3_ERR_NO_DEVICE = 5 /* no usable gfx950 device */
+};
+
+enum { H3_ELEM_F16 = 0, H3_ELEM_BF16 = 1 };
+
+/* Message of the last failing call on this thread ("" after success). */
+const char *h3_last_error(void);
+/* Library version string. */
+const char *h3_version(void);
+
+/* ------------------------------------------------------------------ operand preparation */
+
+/* Config of h3.prepare_qk_i8 / prepare_qk_i8hm / prepare_qk_rope_i8hm
+ * (kernels/prepare_qk_i8.loom:9-15, prepare_qk_i8hm.loom:5-13, prepare_qk_rope_i8hm.loom:7-17):
+ *   row_stride   multiple of 128 in [128, 65536): elements per input row
+ *   head_offset  multiple of 128 in [0, 65536): first channel of head 0
+ *   heads        [1, 256)
+ *   extra_scale  multiplies absmax/127 into the stored scale (Q: 1/sqrt(128)/128, K: 1)
+ *   token_capacity  head-major row capacity, multiple of 32 in [32, 1048576)
+ *   eps          RMSNorm epsilon (RoPE variants only)
+ *   elem         H3_ELEM_F16 or H3_ELEM_BF16 */
+typedef struct {
+  uint32_t row_stride;
+  uint32_t head_offset;
+  uint32_t heads;
+  float extra_scale;
+  uint32_t token_capacity;
+  float eps;
+  uint32_t elem;
+} h3_prepare_cfg;
+
+/* h3_prepare_qk_i8 (kernels/prepare_qk_i8.loom:17-192; token-major).
+ * Per (token, head): y = x - mean; r = H_128 y (unnormalised Sylvester Hadamard, the
+ * reference's fp32 butterfly order); amax = max(max|r|, 1e-30); codes = clamp(rne(r*127/amax),
+ * +-127) packed four per i32; scale = amax/127 * extra_scale.
+ *   x [tokens][row_stride] 16-bit, mean [row_stride] f32 -> codes [tokens][heads*32] i32,
+ *   scales [tokens][heads] f32. tokens in [1, 1048576). */
+int h3_prepare_qk_i8(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x, h3_view mean,
+                     h3_view codes, h3_view scales, h3_stream stream);
+
+/* h3_prepare_qk_i8hm (kernels/prepare_qk_i8hm.loom:13-196): as above, written head-major:
+ * codes [heads][token_capacity][32], scales [heads][token_capacity]. Requires
+ * tokens <= token_capacity; rows past tokens are untouched (the caller zeroes them once). */
+int h3_prepare_qk_i8hm(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x, h3_view mean,
+                       h3_view codes, h3_view scales, h3_stream stream);
+
+/* h3_prepare_qk_rope_i8hm (kernels/prepare_qk_rope_i8hm.loom:19-243): per-head RMSNorm
+ * (weight[128], eps), rotate-half RoPE on channels < 96 (pairs c <-> c+48, tables cos/sin
+ * [tokens][48] f32), f16 rounding, then the quantizer with zero mean; head-major output.
+ * x is the fused QKV row [tokens][row_stride]; head_offset selects Q (0) or K (inner). */
+int h3_prepare_qk_rope_i8hm(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x,
+                            h3_view weight, h3_view cos_t, h3_view sin_t, h3_view codes,
+                            h3_view scales, h3_stream stream);
+
+/* K-mean smoothing fused with RMSNorm + RoPE + quantize (no reference counterpart: the reference
+ * keeps rope_qknorm_f16 -> colmean_f32 -> prepare_qk_i8hm(mean) for smoothing,
+ * src/stack.rs:1306-1326, 1727-1791). Two passes on `stream`: the column mean of the rotated f16
+ * K over all tokens into `mean` ([heads*128] f32, sequential fp32 order), then the quantizer on
+ * rotated K minus that mean. Byte-identical to the separate route. */
+int h3_prepare_k_rope_smooth_i8hm(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x,
+                                  h3_view weight, h3_view cos_t, h3_view sin_t, h3_view mean,
+                                  h3_view codes, h3_view scales, h3_stream stream);
+
+/* Config of h3.rope_qknorm_f16 (kernels/rope_qknorm_f16.loom; src/stack.rs:563-577). */
+typedef struct {
+  uint32_t row_stride; /* elements per fused QKV row */
+  uint32_t heads;      /* query heads */
+  uint32_t kv_heads;   /* key/value heads */
+  uint32_t k_offset;   /* first K channel (heads*128) */
+  float eps;
+  uint32_t copy_v; /* 1: also copy the V slice into v_out [tokens][kv_heads*128] */
+  uint32_t elem;
+} h3_rope_cfg;
+
+/* h3_rope_qknorm_f16 (kernels/rope_qknorm_f16.loom:1-173): RMSNorm + RoPE of Q and K to f16
+ * q_out [tokens][heads*128], k_out [tokens][kv_heads*128]; V copied when copy_v. The same
+ * device arithmetic as h3_prepare_qk_rope_i8hm, so the fused and separate routes agree
+ * byte-for-byte (tests/kernels.rs:3153-3276). */
+int h3_rope_qknorm_f16(const h3_rope_cfg *cfg, uint32_t tokens, h3_view x, h3_view qweight,
+                       h3_view kweight, h3_view cos_t, h3_view sin_t, h3_view q_out,
+                       h3_view k_out, h3_view v_out, h3_stream stream);
+
+/* h3_colmean_f32 (kernels/colmean_f32.loom): mean[c] = (sum_t x[t][c]) / tokens in sequential
+ * fp32 order. width: multiple of 256 in [256, 65536); x [tokens][width] 16-bit. */
+int h3_colmean_f32(uint32_t width, uint32_t elem, uint32_t tokens, h3_view x, h3_view mean,
+                   h3_stream stream);
+
+/* Config of h3.transpose_f16 / transpose_qkv_v_f16 (kernels/transpose_f16.loom:7-9). */
+typedef struct {
+  uint32_t width;        /* multiple of 32 in [32, 65536) */
+  uint32_t row_capacity; /* multiple of 32 in [32, 1048576) */
+  uint32_t elem;         /* bf16 input is rounded to f16 */
+} h3_transpose_cfg;
+
+/* h3_transpose_f16 (kernels/transpose_f16.loom): x [rows][width] -> out [width][row_capacity]
+ * f16. The launch covers ceil(launch_rows/32) tiles of 32 columns: columns >= rows inside them
+ * are zeroed (launch over the whole capacity to clear reused storage, src/stack.rs:1804-1811).
+ * rows <= launch_rows; both <= row_capacity. */
+int h3_transpose_f16(const h3_transpose_cfg *cfg, uint32_t launch_rows, uint32_t rows, h3_view x,
+                     h3_view out, h3_stream stream);
+
+/* h3_transpose_qkv_v_f16 (kernels/transpose_qkv_v_f16.loom): as above, reading the V third of
+ * a fused [rows][3*width] QKV projection; tiles of 64 columns when width % 64 == 0, else 32. */
+int h3_transpose_qkv_v_f16(const h3_transpose_cfg *cfg, uint32_t launch_rows, uint32_t rows,
+                           h3_view x, h3_view out, h3_stream stream);
+
+/* ------------------------------------------------------------------ attention */
+
+/* Config of h3.attention_i8qk_* / attention_i8qkhm_mha8_k64_lds_f16_wmma
+ * (kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17):
+ *   q_stride, kv_stride, out_stride  multiples of 128 in [128, 32768): channels per token
+ *   tokens          [1, 1048576): keys (and query rows) of the sequence
+ *   token_capacity  multiple of 16 in [32, 1048576), >= tokens
+ *   scale           declared and unused, as in the reference (the softmax scale rides in
+ *                   Q's extra_scale, src/stack.rs:622-625). */
+typedef struct {
+  uint32_t q_stride;
+  uint32_t kv_stride;
+  uint32_t out_stride;
+  uint32_t tokens;
+  uint32_t token_capacity;
+  float scale;
+} h3_attention_cfg;
+
+/* h3_attention_i8qkhm (kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom): non-causal MHA
+ * over head-major INT8 operands.
+ *   out[t][h*128 + c] = sum_j softmax_j(S_tj * qs_t * ks_j) vt[h*128 + c][j],
+ *   S_tj = sum_e qcode_te * kcode_je (exact int32), for t < token_count, h < heads.
+ *   qi, ki [heads][token_capacity][32] i32; qs, ks [heads][token_capacity] f32;
+ *   vt [kv_stride][token_capacity] f16 (columns >= tokens must be finite, the transposes
+ *   zero them); out [token_count][out_stride] f16. token_count in [1, tokens]. */
+int h3_attention_i8qkhm(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                        h3_stream stream);
+
+/* h3_attention_i8qk (kernels/attention_i8qk_family.loom: attention_i8qk_mha_lds_f16_wmma): the
+ * same attention over token-major operands: qi [capacity][q_stride/4] i32, qs [capacity][heads],
+ * ki [capacity][kv_stride/4], ks [capacity][heads]. */
+int h3_attention_i8qk(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                      h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                      h3_stream stream);
+
+/* ------------------------------------------------------------------ stack (host mirror) */
+
+/* Row capacity the reference allocates for a sequence of `tokens` (src/stack.rs:299-302):
+ * waves = (causal || tokens >= 4096) ? 8 : 4;
+ * max(ceil((t+16)/32)*32, ceil(t/(16*waves))*16*waves, ceil(t/256)*256). */
+uint32_t h3_capacity(uint32_t tokens, int causal);
+
+/* Attention block dimensions (the subset of the reference's StackDims, src/stack.rs, this path
+ * reads). heads == kv_heads, head_dim 128, rope_dim 96. */
+typedef struct {
+  uint32_t heads;
+  uint32_t tokens;
+  float eps;      /* RMSNorm epsilon */
+  uint32_t elem;  /* element format of the fused QKV projection */
+  int ksmooth;    /* H3_KSMOOTH=1: K-mean smoothing on (separate, unfused route) */
+  int fused;      /* H3_FUSED_OPERANDS != 0: fused RoPE+quantize operands */
+} h3_stack_dims;
+
+typedef struct h3_stack h3_stack;
+
+/* Stack::build (src/stack.rs:260-987, INT8 branch): chooses the route (fused head-major operands,
+ * head-major separate, or token-major below 4096 tokens), derives every kernel config
+ * (src/stack.rs:597-766), and allocates the zero-filled IntQk operand buffers
+ * (src/stack.rs:845-908). The only allocating call; attend/prepare never allocate. */
+int h3_stack_build(const h3_stack_dims *dims, h3_stack **out);
+void h3_stack_destroy(h3_stack *stack);
+uint32_t h3_stack_capacity(const h3_stack *stack);
+
+/* Stack::prepare_fused_operands (src/stack.rs:1541-1616) followed by attention: reads the fused
+ * QKV projection [t][3*heads*128], per-head norm weights, cos/sin [t][48]; writes the attention
+ * output [t][heads*128] f16. */
+int h3_stack_attend_fused(h3_stack *stack, uint32_t t, h3_view fused, h3_view qnorm,
+                          h3_view knorm, h3_view cos_t, h3_view sin_t, h3_view out,
+                          h3_stream stream);
+
+/* Stack::attend (src/stack.rs:1669-1839) on post-RoPE f16 q, k, v [t][heads*128]
+ * (the unfused route): [colmean(K) when smoothing] -> prep_q || prep_k || transpose(V) ->
+ * attention. */
+int h3_stack_attend(h3_stack *stack, uint32_t t, h3_view q, h3_view k, h3_view v, h3_view out,
+                    h3_stream stream);
+
+/* Operand buffers of the stack (IntQk, src/stack.rs:229-238), for inspection by tests. */
+typedef struct {
+  h3_view qi, ki, qs, ks, kmean, zmean, vt;
+  int head_major;
+} h3_int_qk;
+int h3_stack_operands(const h3_stack *stack, h3_int_qk *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

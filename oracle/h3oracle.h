@@ -1,0 +1,119 @@
+/*
+ * h3oracle — CPU restatement of h3-hrx's INT8 (SageAttention-style) attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links, loads or calls this code.
+ * It is the checker for the HIP kernels (tests/, __graft_entry__.smoke()) and the timed CPU
+ * baseline in bench.py. Every function cites the reference file:line it restates
+ * (paths relative to the zacharydenton/h3-hrx source tree).
+ *
+ * Pinning status (what checks each function, besides the HIP kernels it judges):
+ *   h3o_prepare_qk_f32      fp32 op-order restatement of kernels/prepare_qk_i8.loom:63-188.
+ *                           Pinned by the reference's own f64 oracle (tests/kernels.rs:1704-1741)
+ *                           on its closed-form inputs: codes may differ only at rounding ties
+ *                           (< 1/500 words, tests/kernels.rs:1797-1802), scales within
+ *                           1e-7 + 1e-4 rel (1803-1810); by the zero-head and f16::MAX-head
+ *                           special cases; by exactness of the butterfly against the dense
+ *                           Sylvester product where fp32 sums are exact; and by an independent
+ *                           numpy restatement (tests/test_oracle.py).
+ *   h3o_prepared_qk_f64     restatement of the reference test oracle tests/kernels.rs:1704-1741.
+ *   h3o_colmean_f32         kernels/colmean_f32.loom (in-file 30-40): sequential fp32 sum.
+ *                           Pinned by exact integer-valued sums and by numpy cumulative float32.
+ *   h3o_rope_qknorm_f16     this build's RMSNorm + rotate-half RoPE in a fixed fp32 order
+ *                           (kernels/prepare_qk_rope_i8hm.loom:110-130 defines the maths; its
+ *                           reduction order and rsqrt are not pinned by the reference). Pinned
+ *                           to the reference's f64 oracle (tests/kernels.rs:1146-1180) within
+ *                           2e-2 abs + 2e-2 rel, and by the identity-rotation special case.
+ *   h3o_transpose_f16       kernels/transpose_f16.loom: bit permutation plus zero tail.
+ *   h3o_attention_f64       the attention the operands define, tests/kernels.rs:1891-1913 and
+ *                           2084-2111: softmax_j(sum(qc*kc) * qs * ks) . V in f64. Pinned by
+ *                           closed forms: uniform keys give the mean of V, a single dominant key
+ *                           returns its V row, and brute-force numpy on small shapes.
+ */
+#ifndef H3ORACLE_H
+#define H3ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element formats of activations: raw 16-bit patterns */
+enum { H3O_F16 = 0, H3O_BF16 = 1 };
+
+float h3o_half_to_float(uint16_t h);
+uint16_t h3o_float_to_half(float f); /* IEEE binary16, round to nearest even */
+float h3o_bf16_to_float(uint16_t h);
+
+/* %.17g spelling of a double parsed back as f32, as compile::num + the Loom config parse do
+ * (src/compile.rs:38-83). */
+float h3o_config_f32(double v);
+
+/* Quantizer, bit-exact fp32 order of kernels/prepare_qk_i8.loom:63-188.
+ *   x      [tokens][row_stride] 16-bit elements (fmt H3O_F16 or H3O_BF16)
+ *   mean   [row_stride] f32 (may be NULL: zero mean)
+ *   head_major == 0: codes [tokens][heads*32] i32, scales [tokens][heads]
+ *   head_major != 0: codes [heads*capacity][32] i32, scales [heads][capacity]
+ * Rows >= tokens are not written. */
+void h3o_prepare_qk_f32(const uint16_t *x, int fmt, const float *mean, int tokens, int row_stride,
+                        int head_offset, int heads, float extra, int head_major, int capacity,
+                        int32_t *codes, float *scales);
+
+/* One head row: y[128] f32 (already mean-subtracted) -> 32 packed words + scale. */
+void h3o_quantize_row(const float *y, float extra, int32_t *words, float *scale);
+
+/* Unnormalised Sylvester H_128 in the reference's fp32 butterfly order. */
+void h3o_hadamard128_f32(const float *y, float *r);
+
+/* The reference test oracle tests/kernels.rs:1704-1741 (f64, ties away from zero).
+ * x f16 [tokens][heads*128], mean [heads*128]; codes_out f64 [tokens][heads*128] (may be NULL). */
+void h3o_prepared_qk_f64(const uint16_t *x, const float *mean, int tokens, int heads, double extra,
+                         int32_t *words, float *scales, double *codes_out);
+
+/* kernels/colmean_f32.loom: mean[c] = (sum_t f32(x[t][c])) / f32(tokens), sequential. */
+void h3o_colmean_f32(const uint16_t *x, int fmt, int tokens, int width, int row_stride,
+                     float *mean);
+
+/* RMSNorm(weight, eps) + rotate-half RoPE on channels < 96 (pairs c <-> c+48), rounded to f16.
+ * x [tokens][row_stride] (heads x 128 at head_offset), weight[128], cos/sin [tokens][48].
+ * out f16 bits [tokens][out_stride] at column h*128. Fixed fp32 order of this build's kernel. */
+void h3o_rope_qknorm_f16(const uint16_t *x, int fmt, int tokens, int row_stride, int head_offset,
+                         int heads, const float *weight, const float *cos_t, const float *sin_t,
+                         float eps, uint16_t *out, int out_stride);
+
+/* The reference's f64 RMSNorm+RoPE oracle (tests/kernels.rs:1146-1180), f64 out. */
+void h3o_rope_qknorm_f64(const uint16_t *x, int fmt, int tokens, int row_stride, int head_offset,
+                         int heads, const float *weight, const float *cos_t, const float *sin_t,
+                         double eps, double *out);
+
+/* V transpose: x [rows][row_stride] (width columns at col_offset) -> out [width][capacity],
+ * columns [rows, clear_to) zeroed, columns >= clear_to untouched. bf16 input is rounded to f16. */
+void h3o_transpose_f16(const uint16_t *x, int fmt, int rows, int row_stride, int col_offset,
+                       int width, int capacity, int clear_to, uint16_t *out);
+
+/* Attention of the operands, f64 (tests/kernels.rs:1891-1913, 2084-2111).
+ *   codes  int8 [heads][capacity][128] (head-major, unpacked) for q and k
+ *   qs, ks [heads][capacity]; vt f16 [heads*128][capacity]
+ *   rows: the query rows to evaluate (n_rows of them); out f64 [n_rows][heads][128]
+ * threads: OpenMP threads (<= 0: all). Returns 0. */
+int h3o_attention_f64(const int8_t *qc, const float *qs, const int8_t *kc, const float *ks,
+                      const uint16_t *vt, int tokens, int capacity, int heads, const int *rows,
+                      int n_rows, double *out, int threads);
+
+/* Unpack codes: head-major packed words [heads*capacity][32] -> int8 [heads*capacity][128]. */
+void h3o_unpack_codes(const int32_t *words, size_t n_rows, int8_t *codes);
+
+/* CPU baseline: the reference's CPU path for one call on sampled query rows — f64 prepared_qk
+ * of Q (rows sampled) and K (all tokens), then f64 attention of those operands. Returns the
+ * seconds of the per-row part; *fixed_seconds gets the per-call part. threads as above. */
+double h3o_cpu_baseline(const uint16_t *q, const uint16_t *k, const uint16_t *v, int tokens,
+                        int heads, const int *rows, int n_rows, int threads, double *out,
+                        double *fixed_seconds);
+
+int h3o_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,219 @@
+"""numpy front end of the CPU oracle (oracle/h3oracle.c) — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and
+only as the checker or the timed CPU baseline; the shipped library (h3-hrx_amd/) never does.
+Besides wrapping the C restatement, it holds the reference's closed-form test inputs
+(tests/kernels.rs:190-194 `values`) and small numpy helpers.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB = HERE / "_build" / "libh3oracle.so"
+F16, BF16 = 0, 1
+
+_P = np.ctypeslib.ndpointer
+_lib = None
+
+
+def build() -> pathlib.Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        u16 = _P(np.uint16, flags="C")
+        f32 = _P(np.float32, flags="C")
+        f64 = _P(np.float64, flags="C")
+        i32 = _P(np.int32, flags="C")
+        i8 = _P(np.int8, flags="C")
+        c_int, c_float, c_double = ctypes.c_int, ctypes.c_float, ctypes.c_double
+        L.h3o_half_to_float.argtypes = [ctypes.c_uint16]
+        L.h3o_half_to_float.restype = c_float
+        L.h3o_float_to_half.argtypes = [c_float]
+        L.h3o_float_to_half.restype = ctypes.c_uint16
+        L.h3o_config_f32.argtypes = [c_double]
+        L.h3o_config_f32.restype = c_float
+        L.h3o_prepare_qk_f32.argtypes = [u16, c_int, ctypes.c_void_p, c_int, c_int, c_int, c_int,
+                                         c_float, c_int, c_int, i32, f32]
+        L.h3o_prepare_qk_f32.restype = None
+        L.h3o_quantize_row.argtypes = [f32, c_float, i32, f32]
+        L.h3o_quantize_row.restype = None
+        L.h3o_hadamard128_f32.argtypes = [f32, f32]
+        L.h3o_hadamard128_f32.restype = None
+        L.h3o_prepared_qk_f64.argtypes = [u16, f32, c_int, c_int, c_double, i32, f32,
+                                          ctypes.c_void_p]
+        L.h3o_prepared_qk_f64.restype = None
+        L.h3o_colmean_f32.argtypes = [u16, c_int, c_int, c_int, c_int, f32]
+        L.h3o_colmean_f32.restype = None
+        L.h3o_rope_qknorm_f16.argtypes = [u16, c_int, c_int, c_int, c_int, c_int, f32, f32, f32,
+                                          c_float, u16, c_int]
+        L.h3o_rope_qknorm_f16.restype = None
+        L.h3o_rope_qknorm_f64.argtypes = [u16, c_int, c_int, c_int, c_int, c_int, f32, f32, f32,
+                                          c_double, f64]
+        L.h3o_rope_qknorm_f64.restype = None
+        L.h3o_transpose_f16.argtypes = [u16, c_int, c_int, c_int, c_int, c_int, c_int, c_int, u16]
+        L.h3o_transpose_f16.restype = None
+        L.h3o_attention_f64.argtypes = [i8, f32, i8, f32, u16, c_int, c_int, c_int,
+                                        _P(np.int32, flags="C"), c_int, f64, c_int]
+        L.h3o_attention_f64.restype = c_int
+        L.h3o_unpack_codes.argtypes = [i32, ctypes.c_size_t, i8]
+        L.h3o_unpack_codes.restype = None
+        L.h3o_cpu_baseline.argtypes = [u16, u16, u16, c_int, c_int, _P(np.int32, flags="C"),
+                                       c_int, c_int, f64, ctypes.POINTER(c_double)]
+        L.h3o_cpu_baseline.restype = c_double
+        L.h3o_max_threads.argtypes = []
+        L.h3o_max_threads.restype = c_int
+        _lib = L
+    return _lib
+
+
+# --------------------------------------------------------------------- reference test inputs
+
+def values(n: int, scale: float) -> np.ndarray:
+    """tests/kernels.rs:190-194: ((i*37 % 101) - 50) * scale / 50 in f32."""
+    i = np.arange(n, dtype=np.int64)
+    return ((((i * 37) % 101).astype(np.float32) - np.float32(50.0)) * np.float32(scale)
+            / np.float32(50.0)).astype(np.float32)
+
+
+def f16_bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32).astype(np.float16)).view(np.uint16)
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round f32 to bf16 (nearest even) and return the bit patterns."""
+    u = np.ascontiguousarray(np.asarray(a, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def widen(bits: np.ndarray, fmt: int) -> np.ndarray:
+    if fmt == BF16:
+        return (bits.astype(np.uint32) << 16).view(np.float32)
+    return bits.view(np.float16).astype(np.float32)
+
+
+def capacity(tokens: int, causal: bool = False) -> int:
+    """src/stack.rs:299-302."""
+    waves = 8 if (causal or tokens >= 4096) else 4
+    cap = -(-(tokens + 16) // 32) * 32
+    cap = max(cap, -(-tokens // (16 * waves)) * 16 * waves)
+    return max(cap, -(-tokens // 256) * 256)
+
+
+EXTRA_Q_F64 = 1.0 / math.sqrt(128.0) / 128.0
+
+
+def config_f32(v: float) -> float:
+    return float(lib().h3o_config_f32(v))
+
+
+# --------------------------------------------------------------------- oracle calls
+
+def prepare_qk(x_bits: np.ndarray, fmt: int, mean, tokens: int, row_stride: int, head_offset: int,
+               heads: int, extra: float, head_major: bool = False, cap: int = 0):
+    """fp32 restatement of the quantizer; returns (codes i32, scales f32)."""
+    if head_major:
+        codes = np.zeros((heads * cap, 32), np.int32)
+        scales = np.zeros((heads, cap), np.float32)
+    else:
+        codes = np.zeros((tokens, heads * 32), np.int32)
+        scales = np.zeros((tokens, heads), np.float32)
+    m = None
+    if mean is not None:
+        m = np.ascontiguousarray(mean, dtype=np.float32)
+    lib().h3o_prepare_qk_f32(np.ascontiguousarray(x_bits, np.uint16), fmt,
+                             None if m is None else m.ctypes.data, tokens, row_stride,
+                             head_offset, heads, extra, int(head_major), cap, codes, scales)
+    return codes, scales
+
+
+def prepared_qk_f64(x_bits: np.ndarray, mean: np.ndarray, tokens: int, heads: int, extra: float):
+    """tests/kernels.rs:1704-1741; returns (words, scales, codes f64)."""
+    words = np.zeros((tokens, heads * 32), np.int32)
+    scales = np.zeros((tokens, heads), np.float32)
+    codes = np.zeros((tokens, heads * 128), np.float64)
+    lib().h3o_prepared_qk_f64(np.ascontiguousarray(x_bits, np.uint16),
+                              np.ascontiguousarray(mean, np.float32), tokens, heads, extra, words,
+                              scales, codes.ctypes.data)
+    return words, scales, codes
+
+
+def colmean(x_bits: np.ndarray, fmt: int, tokens: int, width: int, row_stride: int) -> np.ndarray:
+    out = np.zeros(width, np.float32)
+    lib().h3o_colmean_f32(np.ascontiguousarray(x_bits, np.uint16), fmt, tokens, width,
+                          row_stride, out)
+    return out
+
+
+def rope_qknorm_f16(x_bits, fmt, tokens, row_stride, head_offset, heads, weight, cos_t, sin_t,
+                    eps) -> np.ndarray:
+    out = np.zeros((tokens, heads * 128), np.uint16)
+    lib().h3o_rope_qknorm_f16(np.ascontiguousarray(x_bits, np.uint16), fmt, tokens, row_stride,
+                              head_offset, heads, np.ascontiguousarray(weight, np.float32),
+                              np.ascontiguousarray(cos_t, np.float32),
+                              np.ascontiguousarray(sin_t, np.float32), eps, out, heads * 128)
+    return out
+
+
+def rope_qknorm_f64(x_bits, fmt, tokens, row_stride, head_offset, heads, weight, cos_t, sin_t,
+                    eps) -> np.ndarray:
+    out = np.zeros((tokens, heads, 128), np.float64)
+    lib().h3o_rope_qknorm_f64(np.ascontiguousarray(x_bits, np.uint16), fmt, tokens, row_stride,
+                              head_offset, heads, np.ascontiguousarray(weight, np.float32),
+                              np.ascontiguousarray(cos_t, np.float32),
+                              np.ascontiguousarray(sin_t, np.float32), eps, out)
+    return out
+
+
+def transpose(x_bits, fmt, rows, row_stride, col_offset, width, cap, clear_to, out=None):
+    if out is None:
+        out = np.zeros((width, cap), np.uint16)
+    lib().h3o_transpose_f16(np.ascontiguousarray(x_bits, np.uint16), fmt, rows, row_stride,
+                            col_offset, width, cap, clear_to, out)
+    return out
+
+
+def unpack(words: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(words, np.int32)
+    return w.view(np.int8).reshape(*w.shape[:-1], w.shape[-1] * 4)
+
+
+def attention_f64(qc, qs, kc, ks, vt, tokens, cap, heads, rows, threads=0) -> np.ndarray:
+    """Head-major int8 codes qc/kc [heads][cap][128], scales [heads][cap], vt [heads*128][cap]
+    f16 bits; returns f64 [len(rows)][heads][128]."""
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros((len(rows), heads, 128), np.float64)
+    lib().h3o_attention_f64(np.ascontiguousarray(qc, np.int8), np.ascontiguousarray(qs, np.float32),
+                            np.ascontiguousarray(kc, np.int8), np.ascontiguousarray(ks, np.float32),
+                            np.ascontiguousarray(vt, np.uint16), tokens, cap, heads, rows,
+                            len(rows), out, threads)
+    return out
+
+
+def cpu_baseline(q_bits, k_bits, v_bits, tokens, heads, rows, threads=0):
+    """Times the reference's CPU path; returns (per_row_seconds, fixed_seconds, out)."""
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros((len(rows), heads, 128), np.float64)
+    fixed = ctypes.c_double(0.0)
+    per_row = lib().h3o_cpu_baseline(np.ascontiguousarray(q_bits, np.uint16),
+                                     np.ascontiguousarray(k_bits, np.uint16),
+                                     np.ascontiguousarray(v_bits, np.uint16), tokens, heads, rows,
+                                     len(rows), threads, out, ctypes.byref(fixed))
+    return per_row, fixed.value, out
+
+
+def max_threads() -> int:
+    return int(lib().h3o_max_threads())

@@ -1,0 +1,159 @@
+"""The C ABI on a CPU host: libh3attn.so loads, exports every symbol include/h3attn.h declares,
+and refuses bad configs and short bindings before touching a device (src/dispatch.rs:264-276).
+No kernel is launched here."""
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+import h3attn as H
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "h3attn.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(h3_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) >= 19
+    out = subprocess.run(["nm", "-D", "--defined-only", str(H.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (h3_\w+)", out))
+    missing = [n for n in names if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    lib = H.lib()
+    for n in names:
+        assert getattr(lib, n) is not None
+    assert set(H.SIGNATURES) <= set(names)
+
+
+def test_capacity_matches_the_reference_formula():
+    import oracle as O
+
+    for t in [1, 23, 63, 64, 65, 129, 1024, 4095, 4096, 4097, 31104, 129024, 130272, 1048544]:
+        assert H.capacity(t) == O.capacity(t), t
+
+
+def fake(nbytes):
+    """A binding that is never dereferenced: the checks reject the call before any launch."""
+    return H.raw_view(0x1000, nbytes)
+
+
+def prep_cfg(heads=4, cap=64):
+    return H.PrepareCfg(heads * 128, 0, heads, 1.0, cap, 1e-5, H.H3_ELEM_F16)
+
+
+def call_prepare(cfg, tokens, x, mean, codes, scales):
+    return H.lib().h3_prepare_qk_i8hm(ctypes.byref(cfg), tokens, x, mean, codes, scales, None)
+
+
+def test_short_binding_is_refused_with_the_reference_message():
+    cfg = prep_cfg()
+    tokens = 37
+    need_x = tokens * 512 * 2
+    st = call_prepare(cfg, tokens, fake(need_x - 2), fake(2048), fake(4 * 64 * 128),
+                      fake(4 * 64 * 4))
+    assert st == H.H3_ERR_BINDING
+    assert H.last_error() == (
+        f"prepare_qk_i8hm: binding 0 is {need_x - 2} bytes, the kernel addresses {need_x}")
+    st = call_prepare(cfg, tokens, fake(need_x), fake(2048), fake(4 * 64 * 128 - 1),
+                      fake(4 * 64 * 4))
+    assert st == H.H3_ERR_BINDING and "binding 2" in H.last_error()
+
+
+@pytest.mark.parametrize("field,value", [("row_stride", 100), ("row_stride", 0),
+                                         ("heads", 0), ("heads", 300), ("head_offset", 64),
+                                         ("token_capacity", 48), ("elem", 7)])
+def test_prepare_config_outside_declared_ranges_is_refused(field, value):
+    cfg = prep_cfg()
+    setattr(cfg, field, value)
+    st = call_prepare(cfg, 37, fake(1 << 30), fake(1 << 20), fake(1 << 30), fake(1 << 30))
+    assert st == H.H3_ERR_CONFIG, H.last_error()
+
+
+def test_tokens_beyond_capacity_are_refused():
+    st = call_prepare(prep_cfg(cap=32), 37, fake(1 << 30), fake(1 << 20), fake(1 << 30),
+                      fake(1 << 30))
+    assert st == H.H3_ERR_ARGUMENT and "exceed token_capacity" in H.last_error()
+
+
+def att_cfg(tokens=97, cap=128, heads=4):
+    w = heads * 128
+    return H.AttentionCfg(w, w, w, tokens, cap, 1.0)
+
+
+def call_attention(cfg, token_count, heads, sizes):
+    views = [fake(n) for n in sizes]
+    return H.lib().h3_attention_i8qkhm(ctypes.byref(cfg), token_count, heads, *views, None)
+
+
+def test_attention_checks_every_binding():
+    heads, tokens, cap = 4, 97, 128
+    need = [heads * cap * 128, heads * cap * 4, heads * cap * 128, heads * cap * 4,
+            heads * 128 * cap * 2, tokens * heads * 128 * 2]
+    for i in range(6):
+        sizes = list(need)
+        sizes[i] -= 1
+        st = call_attention(att_cfg(tokens, cap, heads), tokens, heads, sizes)
+        assert st == H.H3_ERR_BINDING and f"binding {i} " in H.last_error()
+
+
+@pytest.mark.parametrize("field,value", [("q_stride", 100), ("kv_stride", 0),
+                                         ("out_stride", 40000), ("tokens", 0),
+                                         ("token_capacity", 24), ("tokens", 200)])
+def test_attention_config_outside_declared_ranges_is_refused(field, value):
+    cfg = att_cfg()
+    setattr(cfg, field, value)
+    st = call_attention(cfg, 1, 4, [1 << 40] * 6)
+    assert st == H.H3_ERR_CONFIG, H.last_error()
+
+
+def test_attention_token_count_must_lie_in_the_sequence():
+    st = call_attention(att_cfg(), 98, 4, [1 << 40] * 6)
+    assert st == H.H3_ERR_ARGUMENT and "token_count" in H.last_error()
+
+
+def test_transpose_checks_rows_and_bindings():
+    cfg = H.TransposeCfg(256, 128, H.H3_ELEM_F16)
+    lib = H.lib()
+    assert lib.h3_transpose_f16(ctypes.byref(cfg), 200, 100, fake(1 << 30), fake(1 << 30),
+                                None) == H.H3_ERR_ARGUMENT
+    st = lib.h3_transpose_qkv_v_f16(ctypes.byref(cfg), 100, 100, fake(100 * 768 * 2 - 1),
+                                    fake(1 << 30), None)
+    assert st == H.H3_ERR_BINDING and "binding 0" in H.last_error()
+    cfg.width = 48
+    assert lib.h3_transpose_f16(ctypes.byref(cfg), 10, 10, fake(1 << 30), fake(1 << 30),
+                                None) == H.H3_ERR_CONFIG
+
+
+def test_colmean_width_range():
+    lib = H.lib()
+    assert lib.h3_colmean_f32(128, 0, 10, fake(1 << 20), fake(1 << 20), None) == H.H3_ERR_CONFIG
+    assert lib.h3_colmean_f32(512, 0, 10, fake(10 * 512 * 2 - 2), fake(2048),
+                              None) == H.H3_ERR_BINDING
+
+
+def test_rope_config_checks():
+    lib = H.lib()
+    cfg = H.RopeCfg(128 * 12, 4, 4, 512, 1e-5, 1, H.H3_ELEM_F16)
+    ok_sizes = [3 * 1536 * 2, 512, 512, 3 * 48 * 4, 3 * 48 * 4, 3 * 512 * 2, 3 * 512 * 2,
+                3 * 512 * 2]
+    sizes = list(ok_sizes)
+    sizes[3] -= 4
+    st = lib.h3_rope_qknorm_f16(ctypes.byref(cfg), 3, *[fake(n) for n in sizes], None)
+    assert st == H.H3_ERR_BINDING and "binding 3" in H.last_error()
+    cfg.k_offset = 256  # K would overlap Q
+    st = lib.h3_rope_qknorm_f16(ctypes.byref(cfg), 3, *[fake(n) for n in ok_sizes], None)
+    assert st == H.H3_ERR_CONFIG
+
+
+def test_python_layer_raises_with_status():
+    with pytest.raises(H.H3Error) as e:
+        H.check(H.lib().h3_colmean_f32(128, 0, 10, fake(1), fake(1), None))
+    assert e.value.status == H.H3_ERR_CONFIG
