@@ -1,20 +1,30 @@
 // INT8-QK flash attention for gfx950 (CDNA4).
 //
 // One workgroup = 4 wave64s x 32 queries of one head; keys stream through double-buffered
-// 64-key LDS tiles. Per wave and key tile:
+// 64-key LDS tiles; two workgroups share a CU (two waves per SIMD), so one wave's softmax
+// overlaps the other's matrix work. Per wave and key tile:
 //   QK   S^T (64 keys x 32 queries) = K (64 x 128 i8) . Q^T on v_mfma_i32_32x32x32_i8, exact
 //        int32. With keys as the MFMA rows, lane l owns query l%32 and 32 of the tile's keys:
 //        key(b, r, l) = 32b + 8(r/4) + 4(l/32) + r%4 for block b in {0,1}, accumulator reg r.
-//        Every softmax statistic (running max, sum, Q scale) is a per-lane scalar; only the max
-//        is exchanged, once per tile, with the lane's partner in the other half-wave.
-//   softmax  u = f32(S) * ks_key; online max in u units; p = exp2(u*qs*log2e - m*qs*log2e).
+//        Every softmax statistic (running max, sum, Q scale) is a per-lane scalar; only the
+//        tile max is exchanged, once per tile, with the lane's partner in the other half-wave.
+//   dequant  The accumulators start from the bit pattern of 1.5*2^23 instead of 0, so after
+//        the MFMA each holds the float 1.5*2^23 + S exactly (|S| <= 128*128*128 < 2^22). One
+//        FMA per score then gives u = S*ks: u = acc*ks + (-1.5*2^23*ks), the second term
+//        precomputed per key when the tile is staged. No int->float conversion is issued.
+//   softmax  online, base 2, in units of u: p = exp2(u*qs*log2e - m). The running max m is
+//        raised only when a tile's max exceeds it by more than 8 (p <= 2^8 stays exact enough
+//        in f16 and in the f32 sums); only then are the output accumulators rescaled, so in
+//        the steady state the O accumulators are touched by nothing but the MFMAs.
 //   PV   O^T (128 ch x 32 queries) += V^T . P^T on v_mfma_f32_32x32x16_f16. The B operand of a
 //        16-key MFMA step is eight consecutive accumulator registers of one S^T block, converted
 //        to f16 in place: no cross-lane shuffle. The matching A operand needs, in lane half h,
 //        keys {8(j/4) + 4h + j%4 : j < 8} of each 16-key group; the V^T tile is therefore
 //        stored in LDS with key bits 2 and 3 swapped inside every 16-key group, which turns each
-//        A operand into one aligned 16-byte LDS read.
+//        A operand into one aligned 16-byte LDS read. The row sum is accumulated from the same
+//        packed f16 probabilities with v_dot2 (two per instruction).
 // LDS rows are padded to 144 bytes so the 32 rows a half-wave reads land on distinct banks.
+// Full key tiles run without any masking; only the final partial tile is masked.
 // Workgroups are remapped so consecutive query blocks of one head run on the same XCD and
 // share its L2 while they walk the same K/V stream.
 //
@@ -33,8 +43,14 @@ constexpr int kKeys = 64;                                   // keys per LDS tile
 constexpr int kRowBytes = 144;                              // 128 data bytes + 16 pad
 constexpr int kKBytes = kKeys * kRowBytes;                  // 9216
 constexpr int kVBytes = 128 * kRowBytes;                    // 18432
-constexpr int kStageBytes = kKBytes + kVBytes + kKeys * 4;  // 27904
+constexpr int kScaleOffset = kKBytes + kVBytes;             // ks[64] then -M*ks[64]
+constexpr int kStageBytes = kScaleOffset + 2 * kKeys * 4;   // 28160
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMagicBits = 0x4B400000;  // float 12582912 = 1.5 * 2^23
+constexpr float kMagic = 12582912.0f;
+constexpr float kRescaleSlack = 8.0f;   // raise the running max only past 2^8 growth
+
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 struct Args {
   const int32_t* qi;
@@ -64,7 +80,8 @@ struct Prefetch {
   float ks;
 };
 
-template <bool kHeadMajor>
+// Global -> registers. kMasked: keys >= tokens read as zero (only the final tile).
+template <bool kHeadMajor, bool kMasked>
 __device__ __forceinline__ void load_tile(const Args& a, uint32_t kv_head, uint32_t k0,
                                           Prefetch& pf) {
   const int tid = threadIdx.x;
@@ -73,14 +90,13 @@ __device__ __forceinline__ void load_tile(const Args& a, uint32_t kv_head, uint3
     const int c = tid + 256 * i;  // 512 chunks of 16 bytes: key c/8, part c%8
     const uint32_t key = k0 + (c >> 3);
     const int part = c & 7;
-    v4i val = {0, 0, 0, 0};
-    if (key < a.tokens) {
-      const int32_t* src =
-          kHeadMajor ? a.ki + ((size_t)kv_head * a.capacity + key) * 32 + part * 4
-                     : a.ki + (size_t)key * a.kv_words + kv_head * 32 + part * 4;
-      val = *reinterpret_cast<const v4i*>(src);
+    const int32_t* src = kHeadMajor ? a.ki + ((size_t)kv_head * a.capacity + key) * 32 + part * 4
+                                    : a.ki + (size_t)key * a.kv_words + kv_head * 32 + part * 4;
+    if (!kMasked || key < a.tokens) {
+      pf.k[i] = *reinterpret_cast<const v4i*>(src);
+    } else {
+      pf.k[i] = v4i{0, 0, 0, 0};
     }
-    pf.k[i] = val;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -88,21 +104,19 @@ __device__ __forceinline__ void load_tile(const Args& a, uint32_t kv_head, uint3
     const int d = c >> 3, part = c & 7;
     const uint32_t key = k0 + 8 * part;
     const uint16_t* src = a.vt + ((size_t)kv_head * 128 + d) * a.capacity + key;
-    v4i val;
-    if (key + 8 <= a.tokens) {
-      val = *reinterpret_cast<const v4i*>(src);
+    if (!kMasked || key + 8 <= a.tokens) {
+      pf.v[i] = *reinterpret_cast<const v4i*>(src);
     } else {
       uint16_t h[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) h[j] = (key + j < a.tokens) ? src[j] : (uint16_t)0;
-      val = __builtin_bit_cast(v4i, h);
+      pf.v[i] = __builtin_bit_cast(v4i, h);
     }
-    pf.v[i] = val;
   }
   if (tid < kKeys) {
     const uint32_t key = k0 + tid;
     float s = 0.0f;
-    if (key < a.tokens)
+    if (!kMasked || key < a.tokens)
       s = kHeadMajor ? a.ks[(size_t)kv_head * a.capacity + key]
                      : a.ks[(size_t)key * a.kv_head_limit + kv_head];
     pf.ks = s;
@@ -124,16 +138,124 @@ __device__ __forceinline__ void store_tile(char* stage, const Prefetch& pf) {
     // keys 8*part..+3 and +4..+7 of 16-key group part/2, placed with key bits 2 and 3 swapped
     const int group = part >> 1, odd = part & 1;
     char* row = vbase + d * kRowBytes + group * 32;
-    int2 lo = {pf.v[i][0], pf.v[i][1]};
-    int2 hi = {pf.v[i][2], pf.v[i][3]};
-    *reinterpret_cast<int2*>(row + (4 * odd) * 2) = lo;
-    *reinterpret_cast<int2*>(row + (8 + 4 * odd) * 2) = hi;
+    *reinterpret_cast<v2i*>(row + (4 * odd) * 2) = v2i{pf.v[i][0], pf.v[i][1]};
+    *reinterpret_cast<v2i*>(row + (8 + 4 * odd) * 2) = v2i{pf.v[i][2], pf.v[i][3]};
   }
-  if (tid < kKeys) reinterpret_cast<float*>(stage + kKBytes + kVBytes)[tid] = pf.ks;
+  if (tid < kKeys) {
+    float* sc = reinterpret_cast<float*>(stage + kScaleOffset);
+    sc[tid] = pf.ks;
+    sc[kKeys + tid] = -(kMagic * pf.ks);
+  }
+}
+
+// Per-wave state carried across key tiles.
+struct State {
+  v16f acc[4];   // O^T, 4 blocks of 32 channels
+  float m;       // running max in log2 units (u * qs * log2e)
+  float l;       // this lane's partial row sum over its key slots
+};
+
+// One 64-key tile from LDS stage `stage`. kMasked: keys >= tokens get probability 0.
+template <bool kMasked>
+__device__ __forceinline__ void tile_step(const char* stage, const v4i (&qop)[4], float qsl,
+                                          State& st, int n, int half, uint32_t k0,
+                                          uint32_t tokens) {
+  const char* kst = stage;
+  const char* vst = stage + kKBytes;
+  const float* kss = reinterpret_cast<const float*>(stage + kScaleOffset);
+
+  // ---- S^T = K . Q^T, accumulated on top of the 1.5*2^23 float bias
+  const v16i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  v16i s[2];
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+    v4i kop = *reinterpret_cast<const v4i*>(kst + (32 * bb + n) * kRowBytes + 16 * half);
+    s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[0], magic, 0, 0, 0);
+  }
+#pragma unroll
+  for (int dc = 1; dc < 4; ++dc) {
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      v4i kop = *reinterpret_cast<const v4i*>(kst + (32 * bb + n) * kRowBytes + 32 * dc + 16 * half);
+      s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[dc], s[bb], 0, 0, 0);
+    }
+  }
+
+  // ---- u = S * ks in one FMA per score; tile max
+  float u[2][16];
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kb = 32 * bb + 8 * i + 4 * half;
+      const float4 k4 = *reinterpret_cast<const float4*>(kss + kb);
+      const float4 c4 = *reinterpret_cast<const float4*>(kss + kKeys + kb);
+      const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+      const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v = __builtin_fmaf(__int_as_float(s[bb][4 * i + j]), kv[j], cv[j]);
+        if (kMasked && k0 + kb + j >= tokens) v = -INFINITY;
+        u[bb][4 * i + j] = v;
+      }
+    }
+  }
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(u[bb][r], u[bb][r + 1]));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  const float mt = tmax * qsl;
+
+  // ---- lazy rescale: only when some row's max grew past the slack
+  if (__any(mt > st.m + kRescaleSlack)) {
+    const float mn = fmaxf(st.m, mt);
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mn);
+    st.m = mn;
+    st.l *= alpha;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[db][r] *= alpha;
+  }
+
+  // ---- probabilities, packed to f16 B operands, row sum by v_dot2
+  const float neg = -st.m;
+  v8h pb[4];
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r], qsl, neg));
+      float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r + 1], qsl, neg));
+      if (kMasked) {
+        if (u[bb][r] == -INFINITY) p0 = 0.0f;
+        if (u[bb][r + 1] == -INFINITY) p1 = 0.0f;
+      }
+      v2h pair = {(_Float16)p0, (_Float16)p1};
+      st.l = __builtin_amdgcn_fdot2(pair, v2h{(_Float16)1.0f, (_Float16)1.0f}, st.l, false);
+      pb[2 * bb + r / 8][r % 8] = pair[0];
+      pb[2 * bb + r / 8][r % 8 + 1] = pair[1];
+    }
+  }
+
+  // ---- O^T += V^T . P^T
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      v8h vop = *reinterpret_cast<const v8h*>(vst + (32 * db + n) * kRowBytes + (16 * g + 8 * half) * 2);
+      st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pb[g], st.acc[db], 0, 0, 0);
+    }
+  }
 }
 
 template <bool kHeadMajor>
-__global__ __launch_bounds__(256) void k_attention(Args a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_attention(Args a) {
   __shared__ __attribute__((aligned(16))) char smem[2 * kStageBytes];
 
   // XCD-aware remap: hardware hands block b to XCD b % 8; give each XCD a contiguous range of
@@ -169,108 +291,40 @@ __global__ __launch_bounds__(256) void k_attention(Args a) {
                                : a.qs[(size_t)q_read * a.head_limit + head];
   const float qsl = qsv * kLog2e;
 
-  v16f acc[4];
+  State st;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[db][r] = 0.0f;
-  float m_run = -1.0e30f;  // running max in u units (f32(S) * ks)
-  float l_run = 0.0f;      // this lane's partial sum over its key slots
+    for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
+  st.m = -1.0e30f;
+  st.l = 0.0f;
 
+  const uint32_t full = a.tokens / kKeys;             // unmasked tiles
   const uint32_t n_tiles = (a.tokens + kKeys - 1) / kKeys;
   Prefetch pf;
-  load_tile<kHeadMajor>(a, kv_head, 0, pf);
+  if (full > 0)
+    load_tile<kHeadMajor, false>(a, kv_head, 0, pf);
+  else
+    load_tile<kHeadMajor, true>(a, kv_head, 0, pf);
   store_tile(smem, pf);
   __syncthreads();
 
-  for (uint32_t kt = 0; kt < n_tiles; ++kt) {
-    const bool more = kt + 1 < n_tiles;
-    if (more) load_tile<kHeadMajor>(a, kv_head, (kt + 1) * kKeys, pf);
-    const char* stage = smem + (kt & 1) * kStageBytes;
-    const char* kst = stage;
-    const char* vst = stage + kKBytes;
-    const float* kss = reinterpret_cast<const float*>(stage + kKBytes + kVBytes);
-
-    // ---- S^T = K . Q^T
-    v16i s[2];
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[bb][r] = 0;
-#pragma unroll
-    for (int dc = 0; dc < 4; ++dc) {
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        v4i kop = *reinterpret_cast<const v4i*>(kst + (32 * bb + n) * kRowBytes + 32 * dc + 16 * half);
-        s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[dc], s[bb], 0, 0, 0);
-      }
-    }
-
-    // ---- scores in u units, tile max
-    float u[2][16];
-    float tmax = -INFINITY;
-    const uint32_t k0 = kt * kKeys;
-    const bool partial = k0 + kKeys > a.tokens;
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kb = 32 * bb + 8 * i + 4 * half;
-        const float4 k4 = *reinterpret_cast<const float4*>(kss + kb);
-        const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v = (float)s[bb][4 * i + j] * kv[j];
-          if (partial && k0 + kb + j >= a.tokens) v = -INFINITY;
-          u[bb][4 * i + j] = v;
-        }
-      }
-    }
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(u[bb][r], u[bb][r + 1]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qsl);
-    const float neg = -(m_new * qsl);
-    m_run = m_new;
-
-    // ---- probabilities, packed to f16 B operands
-    v8h pb[4];
-    float psum = 0.0f;
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r], qsl, neg));
-        if (partial && u[bb][r] == -INFINITY) p = 0.0f;
-        psum += p;
-        pb[2 * bb + r / 8][r % 8] = (_Float16)p;
-      }
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-
-    // ---- O^T += V^T . P^T
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        v8h vop = *reinterpret_cast<const v8h*>(vst + (32 * db + n) * kRowBytes + (16 * g + 8 * half) * 2);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pb[g], acc[db], 0, 0, 0);
-      }
-    }
-
-    if (more) store_tile(smem + ((kt + 1) & 1) * kStageBytes, pf);
+  for (uint32_t kt = 0; kt < full; ++kt) {
+    const uint32_t next = kt + 1;
+    if (next < full)
+      load_tile<kHeadMajor, false>(a, kv_head, next * kKeys, pf);
+    else if (next < n_tiles)
+      load_tile<kHeadMajor, true>(a, kv_head, next * kKeys, pf);
+    tile_step<false>(smem + (kt & 1) * kStageBytes, qop, qsl, st, n, half, kt * kKeys, a.tokens);
+    if (next < n_tiles) store_tile(smem + (next & 1) * kStageBytes, pf);
     __syncthreads();
   }
+  if (full < n_tiles)
+    tile_step<true>(smem + (full & 1) * kStageBytes, qop, qsl, st, n, half, full * kKeys,
+                    a.tokens);
 
   // ---- normalise and store rows < token_count
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = st.l + __shfl_xor(st.l, 32);
   const float inv = 1.0f / l_tot;
   if (q_tile < tiles32 && q < a.token_count && q < a.tokens) {
     uint16_t* dst = a.out + (size_t)q * a.out_stride + head * 128;
@@ -278,8 +332,8 @@ __global__ __launch_bounds__(256) void k_attention(Args a) {
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        v4h o = {(_Float16)(acc[db][4 * i + 0] * inv), (_Float16)(acc[db][4 * i + 1] * inv),
-                 (_Float16)(acc[db][4 * i + 2] * inv), (_Float16)(acc[db][4 * i + 3] * inv)};
+        v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
+                 (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
         *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
       }
     }
