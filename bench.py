@@ -84,6 +84,22 @@ def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
     }
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(torch) -> None:
+    """A plain device-to-device copy of COPY_BYTES (reads COPY_BYTES, writes COPY_BYTES). Under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE its per-dispatch counts give the factor that turns
+    the counters' units into HBM bytes for the attention kernel's traffic figure."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "dispatches": 3}), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +108,8 @@ def main() -> None:
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-rows", type=int, default=8, help="query rows per head for the CPU leg")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy (the HBM-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -100,6 +118,10 @@ def main() -> None:
 
     import numpy as np
     import torch
+
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
 
     import h3attn as H
 

@@ -44,8 +44,16 @@ FLAGS = [
 ]
 
 
+# Per-file extras. The attention kernel is checked to a tolerance (never bit-exact) and never
+# sees NaN operands, so it may drop the NaN-quieting canonicalisations IEEE mode otherwise adds
+# to every max; infinities stay honoured (masked keys are -inf). The quantizer files keep full
+# IEEE semantics.
+EXTRA = {"attention.hip": ["-fno-honor-nans"]}
+
+
 def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
-    cmd = [hipcc(), "-x", "hip", *FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), "-x", "hip", *FLAGS, *EXTRA.get(src.name, []), f"-I{INCLUDE}", "-c",
+           str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
