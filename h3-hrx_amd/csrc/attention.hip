@@ -1,13 +1,16 @@
 // INT8-QK flash attention for gfx950 (CDNA4).
 //
-// One workgroup = 4 wave64s x 32 queries of one head; keys stream through double-buffered
-// 64-key LDS tiles; two workgroups share a CU (two waves per SIMD), so one wave's softmax
-// overlaps the other's matrix work. Per wave and key tile:
+// One workgroup = 4 wave64s x 32 queries of one head; keys stream through 64-key LDS tiles;
+// two workgroups share a CU (two waves per SIMD). Per wave and key tile:
 //   QK   S^T (64 keys x 32 queries) = K (64 x 128 i8) . Q^T on v_mfma_i32_32x32x32_i8, exact
-//        int32. With keys as the MFMA rows, lane l owns query l%32 and 32 of the tile's keys:
-//        key(b, r, l) = 32b + 8(r/4) + 4(l/32) + r%4 for block b in {0,1}, accumulator reg r.
-//        Every softmax statistic (running max, sum, Q scale) is a per-lane scalar; only the
-//        tile max is exchanged, once per tile, with the lane's partner in the other half-wave.
+//        int32. With keys as the MFMA rows, lane l owns query l%32; accumulator register r of
+//        block b holds MFMA row m = 32b + 8(r/4) + 4(l/32) + r%4. Every softmax statistic
+//        (running max, sum, Q scale) is a per-lane scalar; only the tile max is exchanged, once
+//        per tile, with the lane's partner in the other half-wave (v_permlane32_swap).
+//   K row order  LDS row m of a K tile holds key swap23(m) (bits 2 and 3 exchanged), so the
+//        eight accumulator registers 8(g%2)..+7 of block g/2 hold keys 16g + 8(l/32) + 0..7 in
+//        order: exactly the B operand layout of a 16-key f16 MFMA step, with V^T in natural key
+//        order. P never leaves its registers.
 //   dequant  The accumulators start from the bit pattern of 1.5*2^23 instead of 0, so after
 //        the MFMA each holds the float 1.5*2^23 + S exactly (|S| <= 128*128*128 < 2^22). One
 //        FMA per score then gives u = S*ks: u = acc*ks + (-1.5*2^23*ks), the second term
@@ -16,15 +19,28 @@
 //        raised only when a tile's max exceeds it by more than 8 (p <= 2^8 stays exact enough
 //        in f16 and in the f32 sums); only then are the output accumulators rescaled, so in
 //        the steady state the O accumulators are touched by nothing but the MFMAs.
-//   PV   O^T (128 ch x 32 queries) += V^T . P^T on v_mfma_f32_32x32x16_f16. The B operand of a
-//        16-key MFMA step is eight consecutive accumulator registers of one S^T block, converted
-//        to f16 in place: no cross-lane shuffle. The matching A operand needs, in lane half h,
-//        keys {8(j/4) + 4h + j%4 : j < 8} of each 16-key group; the V^T tile is therefore
-//        stored in LDS with key bits 2 and 3 swapped inside every 16-key group, which turns each
-//        A operand into one aligned 16-byte LDS read. The row sum is accumulated from the same
-//        packed f16 probabilities with v_dot2 (two per instruction).
-// LDS rows are padded to 144 bytes so the 32 rows a half-wave reads land on distinct banks.
-// Full key tiles run without any masking; only the final partial tile is masked.
+//   PV   O^T (128 ch x 32 queries) += V^T . P^T on v_mfma_f32_32x32x16_f16; the row sum is
+//        accumulated from the same packed f16 probabilities with v_dot2.
+//
+// Software pipeline (one wave, step j): the matrix work of two tiles runs under the vector work
+// of one, in a fixed issue order:
+//   phase A  QK(j+1): 8 int8 MFMAs   with  exp/pack/sum of tile j's first 16 key slots
+//   phase B  PV(j):  16 f16 MFMAs     with  exp/pack/sum of its last 16 slots (feeding PV(j)'s
+//                                          later MFMAs), then dequant + max of tile j+1 and the
+//                                          raise of the running max
+// so every MFMA has independent VALU work to co-issue with. LDS operands are read two MFMAs
+// ahead.
+//
+// Staging: K and V^T tiles go from HBM straight into LDS with buffer_load ... lds (LDS-DMA; no
+// registers, no LDS store instructions), through rings of three stages each. Step j reads
+// K(j+1) and V(j) and issues the loads of K(j+3) and V(j+2), so every load has two steps to
+// land. A wave waits only for its own loads of the previous step before the step's barrier
+// (s_waitcnt vmcnt(7)), never for the ones it has just issued. LDS rows are 128 bytes with
+// their 16-byte chunks XOR-swizzled by (row/2)%8, so the 32 rows a half-wave reads fall on
+// distinct banks. The key scales ks and -1.5*2^23*ks go through registers (one small load per
+// wave per step, stored a step later) since the second is computed.
+// Global loads use buffer descriptors whose range ends at the last valid key, so keys past the
+// sequence read as zero with no per-element test; only the final partial tile is masked.
 // Workgroups are remapped so consecutive query blocks of one head run on the same XCD and
 // share its L2 while they walk the same K/V stream.
 //
@@ -40,17 +56,21 @@ constexpr int kWaves = 4;
 constexpr int kQueriesPerWave = 32;
 constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;  // 128
 constexpr int kKeys = 64;                                   // keys per LDS tile
-constexpr int kRowBytes = 144;                              // 128 data bytes + 16 pad
-constexpr int kKBytes = kKeys * kRowBytes;                  // 9216
-constexpr int kVBytes = 128 * kRowBytes;                    // 18432
-constexpr int kScaleOffset = kKBytes + kVBytes;             // ks[64] then -M*ks[64]
-constexpr int kStageBytes = kScaleOffset + 2 * kKeys * 4;   // 28160
+constexpr int kRowBytes = 128;                              // unpadded, chunks swizzled
+constexpr int kKRows = kKeys * kRowBytes;                   // 8192
+constexpr int kKStage = kKRows + 2 * kKeys * 4;             // + ks[64], -M*ks[64]: 8704
+constexpr int kVStage = 128 * kRowBytes;                    // 16384
+constexpr int kLoadsPerStep = 7;                            // per wave: 2 K + 4 V^T DMA + 1 ks
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMagicBits = 0x4B400000;  // float 12582912 = 1.5 * 2^23
 constexpr float kMagic = 12582912.0f;
 constexpr float kRescaleSlack = 8.0f;   // raise the running max only past 2^8 growth
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+// s_waitcnt: vmcnt <= kLoadsPerStep, lgkmcnt 0, expcnt untouched (gfx9 field layout)
+constexpr int kWaitPrevStep = kLoadsPerStep | (7 << 4) | (0 << 8);
+constexpr int kWaitAll = 0 | (7 << 4) | (0 << 8);
 
-typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 struct Args {
   const int32_t* qi;
@@ -63,7 +83,7 @@ struct Args {
   uint32_t token_count;
   uint32_t capacity;
   uint32_t q_words;   // q_stride / 4 (token-major row pitch of qi, in words)
-  uint32_t kv_words;  // kv_stride / 4
+  uint32_t kv_bytes;  // kv_stride (token-major row pitch of ki, in bytes)
   uint32_t out_stride;
   uint32_t q_blocks;  // ceil(token_count / 128)
   uint32_t heads;     // workload heads (grid y of the reference)
@@ -73,79 +93,107 @@ struct Args {
   uint32_t per_xcd;    // ceil(total / 8)
 };
 
-// Registers holding one key tile on its way from global memory to LDS.
-struct Prefetch {
-  v4i k[2];
-  v4i v[4];
-  float ks;
+__device__ __forceinline__ uint32_t swap23(uint32_t m) {
+  return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcWord3);
+}
+
+// Per-thread constants of the staging loads.
+struct Stager {
+  uint32_t koff[2];  // byte offset inside a K tile of this lane's 16 bytes, per DMA load
+  uint32_t voff[4];  // byte offset inside a V^T tile (from the head block base + 2*k0)
+  uint32_t soff;     // ks element offset (bytes) of this lane's scale row
+  uint32_t srow;     // MFMA row whose scales this lane stores (lanes 0..15 of each wave)
+  int wave;
 };
 
-// Global -> registers. kMasked: keys >= tokens read as zero (only the final tile).
-template <bool kHeadMajor, bool kMasked>
-__device__ __forceinline__ void load_tile(const Args& a, uint32_t kv_head, uint32_t k0,
-                                          Prefetch& pf) {
-  const int tid = threadIdx.x;
+// LDS byte o of a K/V^T stage holds row o/128, logical chunk ((o/16)%8) ^ ((row/2)%8).
+template <bool kHeadMajor>
+__device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane) {
+  Stager s;
+  s.wave = wave;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = tid + 256 * i;  // 512 chunks of 16 bytes: key c/8, part c%8
-    const uint32_t key = k0 + (c >> 3);
-    const int part = c & 7;
-    const int32_t* src = kHeadMajor ? a.ki + ((size_t)kv_head * a.capacity + key) * 32 + part * 4
-                                    : a.ki + (size_t)key * a.kv_words + kv_head * 32 + part * 4;
-    if (!kMasked || key < a.tokens) {
-      pf.k[i] = *reinterpret_cast<const v4i*>(src);
-    } else {
-      pf.k[i] = v4i{0, 0, 0, 0};
-    }
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t o = wave * 2048 + t * 1024 + 16 * lane;
+    const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
+    const uint32_t key = swap23(row);
+    s.koff[t] = (kHeadMajor ? key * 128 : key * a.kv_bytes) + 16 * chunk;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + 256 * i;  // 1024 chunks: channel c/8, keys 8*(c%8)..+7
-    const int d = c >> 3, part = c & 7;
-    const uint32_t key = k0 + 8 * part;
-    const uint16_t* src = a.vt + ((size_t)kv_head * 128 + d) * a.capacity + key;
-    if (!kMasked || key + 8 <= a.tokens) {
-      pf.v[i] = *reinterpret_cast<const v4i*>(src);
-    } else {
-      uint16_t h[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) h[j] = (key + j < a.tokens) ? src[j] : (uint16_t)0;
-      pf.v[i] = __builtin_bit_cast(v4i, h);
-    }
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t o = wave * 4096 + t * 1024 + 16 * lane;
+    const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
+    s.voff[t] = row * a.capacity * 2 + 16 * chunk;
   }
-  if (tid < kKeys) {
-    const uint32_t key = k0 + tid;
-    float s = 0.0f;
-    if (!kMasked || key < a.tokens)
-      s = kHeadMajor ? a.ks[(size_t)kv_head * a.capacity + key]
-                     : a.ks[(size_t)key * a.kv_head_limit + kv_head];
-    pf.ks = s;
+  s.srow = 16 * wave + (lane & 15);
+  const uint32_t skey = swap23(s.srow);
+  s.soff = kHeadMajor ? skey * 4 : skey * a.kv_head_limit * 4;
+  return s;
+}
+
+// LDS-DMA of K tile k0 (rows past the sequence load as zero) into stage `kst`, and the load of
+// its scales into a register.
+template <bool kHeadMajor>
+__device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32_t kv_head,
+                                         uint32_t k0, char* kst) {
+  const uint32_t live = a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
+  const char* base;
+  uint32_t bytes;
+  const float* sbase;
+  uint32_t sbytes;
+  if (kHeadMajor) {
+    base = reinterpret_cast<const char*>(a.ki) + ((size_t)kv_head * a.capacity + k0) * 128;
+    bytes = live * 128;
+    sbase = a.ks + (size_t)kv_head * a.capacity + k0;
+    sbytes = live * 4;
+  } else {
+    base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * 128;
+    bytes = live ? (live - 1) * a.kv_bytes + 128 : 0;
+    sbase = a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
+    sbytes = live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0;
+  }
+  const __amdgpu_buffer_rsrc_t rk = rsrc(base, bytes);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rk, (lds_void*)(kst + sg.wave * 2048 + t * 1024), 16, sg.koff[t], 0, 0, 0);
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(sbase, sbytes),
+                                                                         sg.soff, 0, 0));
+}
+
+// LDS-DMA of V^T tile k0 into stage `vst`. The range ends at the end of this head's V^T block;
+// columns past `tokens` inside it are zero (the transposes clear them) or belong to the next
+// row, and are multiplied by probability 0.
+__device__ __forceinline__ void stage_v(const Args& a, const Stager& sg, uint32_t kv_head,
+                                        uint32_t k0, char* vst) {
+  const uint32_t blk = 128 * a.capacity;  // elements of this head's V^T block
+  const char* base = reinterpret_cast<const char*>(a.vt) + ((size_t)kv_head * blk + k0) * 2;
+  const __amdgpu_buffer_rsrc_t rv = rsrc(base, k0 < blk ? (blk - k0) * 2 : 0u);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rv, (lds_void*)(vst + sg.wave * 4096 + t * 1024), 16, sg.voff[t], 0, 0, 0);
+}
+
+// Scales of a staged K tile: ks and -1.5*2^23*ks at its MFMA-row index.
+__device__ __forceinline__ void store_scales(char* kst, const Stager& sg, float ks) {
+  if ((threadIdx.x & 63) < 16) {
+    float* sc = reinterpret_cast<float*>(kst + kKRows);
+    sc[sg.srow] = ks;
+    sc[kKeys + sg.srow] = -(kMagic * ks);
   }
 }
 
-__device__ __forceinline__ void store_tile(char* stage, const Prefetch& pf) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = tid + 256 * i;
-    *reinterpret_cast<v4i*>(stage + (c >> 3) * kRowBytes + (c & 7) * 16) = pf.k[i];
-  }
-  char* vbase = stage + kKBytes;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + 256 * i;
-    const int d = c >> 3, part = c & 7;
-    // keys 8*part..+3 and +4..+7 of 16-key group part/2, placed with key bits 2 and 3 swapped
-    const int group = part >> 1, odd = part & 1;
-    char* row = vbase + d * kRowBytes + group * 32;
-    *reinterpret_cast<v2i*>(row + (4 * odd) * 2) = v2i{pf.v[i][0], pf.v[i][1]};
-    *reinterpret_cast<v2i*>(row + (8 + 4 * odd) * 2) = v2i{pf.v[i][2], pf.v[i][3]};
-  }
-  if (tid < kKeys) {
-    float* sc = reinterpret_cast<float*>(stage + kScaleOffset);
-    sc[tid] = pf.ks;
-    sc[kKeys + tid] = -(kMagic * pf.ks);
-  }
+// Barrier between pipeline steps: this wave's LDS writes, and its staging loads from before the
+// current step, are complete; the loads issued in this step stay in flight.
+template <int kWait>
+__device__ __forceinline__ void step_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWait);
+  asm volatile("s_barrier" ::: "memory");
 }
 
 // Per-wave state carried across key tiles.
@@ -153,110 +201,207 @@ struct State {
   v16f acc[4];   // O^T, 4 blocks of 32 channels
   float m;       // running max in log2 units (u * qs * log2e)
   float l;       // this lane's partial row sum over its key slots
+  float alpha;   // rescale of acc still owed for the last raise of m (1: none)
 };
 
-// One 64-key tile from LDS stage `stage`. kMasked: keys >= tokens get probability 0.
-template <bool kMasked>
-__device__ __forceinline__ void tile_step(const char* stage, const v4i (&qop)[4], float qsl,
-                                          State& st, int n, int half, uint32_t k0,
-                                          uint32_t tokens) {
-  const char* kst = stage;
-  const char* vst = stage + kKBytes;
-  const float* kss = reinterpret_cast<const float*>(stage + kScaleOffset);
+// Issue-order fence: the scheduler keeps each chunk's MFMA, LDS reads and VALU work together.
+#define H3_CHUNK_END() __builtin_amdgcn_sched_barrier(0)
 
-  // ---- S^T = K . Q^T, accumulated on top of the 1.5*2^23 float bias
+// Probabilities of key slots r, r+1 of S^T block bb: exp2, pack to f16 (B operand of PV), sum.
+template <bool kMasked>
+__device__ __forceinline__ void exp_pair(const float (&u)[2][16], int bb, int r, float qsl,
+                                         float negm, v8h (&pb)[4], float& l) {
+  float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r], qsl, negm));
+  float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r + 1], qsl, negm));
+  if (kMasked) {
+    if (u[bb][r] == -INFINITY) p0 = 0.0f;
+    if (u[bb][r + 1] == -INFINITY) p1 = 0.0f;
+  }
+  const v2h pair = {(_Float16)p0, (_Float16)p1};
+  l = __builtin_amdgcn_fdot2(pair, v2h{(_Float16)1.0f, (_Float16)1.0f}, l, false);
+  pb[2 * bb + r / 8][r % 8] = pair[0];
+  pb[2 * bb + r / 8][r % 8 + 1] = pair[1];
+}
+
+// max3 kept where it is written: as an opaque instruction it is neither reassociated into one
+// tree at the end of the step nor moved out of its issue chunk.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Dequantize four key slots (S^T block bb, registers 4i..4i+3) of a fresh tile into u. key0 is
+// the key of the first of them; the other three follow it.
+template <bool kMasked>
+__device__ __forceinline__ void dequant4(const v16i (&s)[2], int bb, int i, float4 k4, float4 c4,
+                                         float (&u)[2][16], float& tmax, uint32_t key0,
+                                         uint32_t tokens) {
+  const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+  const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = __builtin_fmaf(__int_as_float(s[bb][4 * i + j]), kv[j], cv[j]);
+    if (kMasked && key0 + j >= tokens) v = -INFINITY;
+    u[bb][4 * i + j] = v;
+  }
+  tmax = max3(tmax, max3(u[bb][4 * i], u[bb][4 * i + 1], u[bb][4 * i + 2]), u[bb][4 * i + 3]);
+}
+
+// Key of the first of the four slots (bb, 4i..4i+3) in lane half `half`: swap23 of the MFMA row.
+__device__ __forceinline__ uint32_t slot_key(int bb, int i, int half) {
+  return 32 * bb + 16 * (i >> 1) + 8 * half + 4 * (i & 1);
+}
+
+// The tile max of both half-waves: v_permlane32_swap exchanges lanes l and l+32 on the vector
+// pipe (no LDS round trip).
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Tile max -> lazy raise of the running max; the accumulator rescale is owed to the next step.
+__device__ __forceinline__ void raise_max(float tmax, float qsl, State& st) {
+  tmax = half_swap_max(tmax);
+  const float mt = tmax * qsl;
+  const float m_new = mt > st.m + kRescaleSlack ? mt : st.m;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  st.l *= alpha;
+  st.alpha *= alpha;
+  st.m = m_new;
+}
+
+// LDS byte offset, inside a row, of logical 16-byte chunk 2x + half for rows with (row/2)%8 = sw.
+__device__ __forceinline__ uint32_t chunk_off(int x, int half, uint32_t sw) {
+  return 16 * ((2 * x + half) ^ sw);
+}
+
+// The first tile's QK and dequant (no softmax work to overlap yet).
+template <bool kMasked>
+__device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4], float qsl,
+                                           State& st, float (&u)[2][16], int n, int half,
+                                           uint32_t tokens) {
   const v16i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
                       kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
                       kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  const uint32_t sw = (n >> 1) & 7;
+  const char* krow = kst + n * kRowBytes;
+  const float* kss = reinterpret_cast<const float*>(kst + kKRows);
   v16i s[2];
 #pragma unroll
-  for (int bb = 0; bb < 2; ++bb) {
-    v4i kop = *reinterpret_cast<const v4i*>(kst + (32 * bb + n) * kRowBytes + 16 * half);
-    s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[0], magic, 0, 0, 0);
-  }
-#pragma unroll
-  for (int dc = 1; dc < 4; ++dc) {
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      v4i kop = *reinterpret_cast<const v4i*>(kst + (32 * bb + n) * kRowBytes + 32 * dc + 16 * half);
-      s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[dc], s[bb], 0, 0, 0);
-    }
-  }
-
-  // ---- u = S * ks in one FMA per score; tile max
-  float u[2][16];
-#pragma unroll
-  for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kb = 32 * bb + 8 * i + 4 * half;
-      const float4 k4 = *reinterpret_cast<const float4*>(kss + kb);
-      const float4 c4 = *reinterpret_cast<const float4*>(kss + kKeys + kb);
-      const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
-      const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v = __builtin_fmaf(__int_as_float(s[bb][4 * i + j]), kv[j], cv[j]);
-        if (kMasked && k0 + kb + j >= tokens) v = -INFINITY;
-        u[bb][4 * i + j] = v;
-      }
-    }
+  for (int c = 0; c < 8; ++c) {
+    const int bb = c & 1, dc = c >> 1;
+    const v4i kop = *reinterpret_cast<const v4i*>(krow + bb * 32 * kRowBytes + chunk_off(dc, half, sw));
+    s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
   }
   float tmax = -INFINITY;
 #pragma unroll
-  for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(u[bb][r], u[bb][r + 1]));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-  const float mt = tmax * qsl;
+  for (int q = 0; q < 8; ++q) {
+    const int bb = q >> 2, i = q & 3;
+    const int kb = 32 * bb + 8 * i + 4 * half;
+    dequant4<kMasked>(s, bb, i, *reinterpret_cast<const float4*>(kss + kb),
+                      *reinterpret_cast<const float4*>(kss + kKeys + kb), u, tmax,
+                      slot_key(bb, i, half), tokens);
+  }
+  raise_max(tmax, qsl, st);
+}
 
-  // ---- lazy rescale: only when some row's max grew past the slack
-  if (__any(mt > st.m + kRescaleSlack)) {
-    const float mn = fmaxf(st.m, mt);
-    const float alpha = __builtin_amdgcn_exp2f(st.m - mn);
-    st.m = mn;
-    st.l *= alpha;
+// One pipeline step: QK(j+1) and PV(j) under tile j's softmax and tile j+1's dequant.
+//   kst    LDS stage of K(j+1) (unused when !kNext), vst  LDS stage of V(j)
+//   u      in: tile j's dequantized scores; out: tile j+1's
+//   knext0 first key of tile j+1
+template <bool kNext, bool kMaskNext, bool kMaskCur>
+__device__ __forceinline__ void step(const char* kst, const char* vst, const v4i (&qop)[4],
+                                     float qsl, State& st, float (&u)[2][16], int n, int half,
+                                     uint32_t knext0, uint32_t tokens) {
+  // The rescale owed by the last raise of m, now that PV(j-1) has accumulated.
+  if (__any(st.alpha != 1.0f)) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st.acc[db][r] *= alpha;
+      for (int r = 0; r < 16; ++r) st.acc[db][r] *= st.alpha;
+    st.alpha = 1.0f;
   }
-
-  // ---- probabilities, packed to f16 B operands, row sum by v_dot2
-  const float neg = -st.m;
+  const v16i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  const float negm = -st.m;
+  const uint32_t sw = (n >> 1) & 7;
+  const char* krow = kst + n * kRowBytes;  // + 32*bb rows + chunk_off(dc)
+  const char* vrow = vst + n * kRowBytes;  // + 32*db rows + chunk_off(g)
+  const float* kss = reinterpret_cast<const float*>(kst + kKRows);
+  v16i s[2];
   v8h pb[4];
+  v4i kop[8];
+  v8h vop[16];
+  float4 k4[8], c4[8];
+  float la = 0.0f, lb = 0.0f;
+
+  // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
+  if (kNext) {
+    kop[0] = *reinterpret_cast<const v4i*>(krow + chunk_off(0, half, sw));
+    kop[1] = *reinterpret_cast<const v4i*>(krow + 32 * kRowBytes + chunk_off(0, half, sw));
+  }
 #pragma unroll
-  for (int bb = 0; bb < 2; ++bb) {
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r], qsl, neg));
-      float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r + 1], qsl, neg));
-      if (kMasked) {
-        if (u[bb][r] == -INFINITY) p0 = 0.0f;
-        if (u[bb][r + 1] == -INFINITY) p1 = 0.0f;
-      }
-      v2h pair = {(_Float16)p0, (_Float16)p1};
-      st.l = __builtin_amdgcn_fdot2(pair, v2h{(_Float16)1.0f, (_Float16)1.0f}, st.l, false);
-      pb[2 * bb + r / 8][r % 8] = pair[0];
-      pb[2 * bb + r / 8][r % 8 + 1] = pair[1];
+  for (int c = 0; c < 8; ++c) {
+    const int bb = c & 1, dc = c >> 1;
+    if (kNext && c + 2 < 8) {
+      const int w = c + 2;
+      kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
     }
+    if (c >= 6) {
+      const int w = c - 6;
+      vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
+    }
+    if (kNext)
+      s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
+    exp_pair<kMaskCur>(u, 0, 2 * c, qsl, negm, pb, la);
+    H3_CHUNK_END();
   }
 
-  // ---- O^T += V^T . P^T
+  // ---- phase B: PV(j) || probabilities of slots 16..31, then dequant + max of tile j+1
+  float tmax = -INFINITY;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      v8h vop = *reinterpret_cast<const v8h*>(vst + (32 * db + n) * kRowBytes + (16 * g + 8 * half) * 2);
-      st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pb[g], st.acc[db], 0, 0, 0);
+  for (int c = 0; c < 16; ++c) {
+    const int g = c >> 2, db = c & 3;
+    if (c + 2 < 16) {
+      const int w = c + 2;
+      vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
+    if (kNext && c >= 4 && c < 12) {  // scales of dequant quarter c-4, two chunks ahead
+      const int q = c - 4, kb = 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
+      k4[q] = *reinterpret_cast<const float4*>(kss + kb);
+      c4[q] = *reinterpret_cast<const float4*>(kss + kKeys + kb);
+    }
+    st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[g], st.acc[db], 0, 0, 0);
+    if (c < 8)
+      exp_pair<kMaskCur>(u, 1, 2 * c, qsl, negm, pb, lb);
+    if (kNext && c >= 6 && c < 14) {
+      const int q = c - 6, bb = q >> 2, i = q & 3;
+      dequant4<kMaskNext>(s, bb, i, k4[q], c4[q], u, tmax, knext0 + slot_key(bb, i, half),
+                          tokens);
+    }
+    if (kNext && c == 14) {  // under the last MFMAs: tile j's sums are complete
+      st.l += la + lb;
+      raise_max(tmax, qsl, st);
+    }
+    H3_CHUNK_END();
   }
+  if (!kNext) st.l += la + lb;
 }
 
 template <bool kHeadMajor>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention(Args a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kStageBytes];
+  // Three K stages and three V^T stages, each its own array so that the compiler can tell an
+  // LDS-DMA into one stage from the reads of another.
+  __shared__ __attribute__((aligned(16))) char k0s[kKStage];
+  __shared__ __attribute__((aligned(16))) char k1s[kKStage];
+  __shared__ __attribute__((aligned(16))) char k2s[kKStage];
+  __shared__ __attribute__((aligned(16))) char v0s[kVStage];
+  __shared__ __attribute__((aligned(16))) char v1s[kVStage];
+  __shared__ __attribute__((aligned(16))) char v2s[kVStage];
 
   // XCD-aware remap: hardware hands block b to XCD b % 8; give each XCD a contiguous range of
   // (head, query block) work so its resident blocks share one head's K/V stream in L2.
@@ -268,7 +413,7 @@ void k_attention(Args a) {
   const uint32_t kv_head = head_y % a.kv_head_limit;
   const uint32_t head = kv_head % a.head_limit;
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;      // query within the wave's tile
   const int half = lane >> 5;   // which 16 key-bytes / key slots this lane holds
@@ -278,6 +423,17 @@ void k_attention(Args a) {
   const uint32_t q_tile_c = q_tile < tiles32 ? q_tile : tiles32 - 1;
   const uint32_t q = q_tile_c * kQueriesPerWave + n;
   const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
+
+  const Stager sg = make_stager<kHeadMajor>(a, wave, lane);
+  const uint32_t n_tiles = (a.tokens + kKeys - 1) / kKeys;
+  const uint32_t full = a.tokens / kKeys;  // tiles with no key past the sequence
+
+  // ---- prologue: K(0..2) and V(0..1) in flight, scales of K(0), K(1) stored, K(2)'s held
+  float ks0 = stage_k<kHeadMajor>(a, sg, kv_head, 0, k0s);
+  float ks1 = stage_k<kHeadMajor>(a, sg, kv_head, kKeys, k1s);
+  float ks_held = stage_k<kHeadMajor>(a, sg, kv_head, 2 * kKeys, k2s);
+  stage_v(a, sg, kv_head, 0, v0s);
+  stage_v(a, sg, kv_head, kKeys, v1s);
 
   // Q^T operand, held for the whole key loop: 4 chunks of 32 channels, 16 bytes per lane.
   v4i qop[4];
@@ -298,30 +454,59 @@ void k_attention(Args a) {
     for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
   st.m = -1.0e30f;
   st.l = 0.0f;
+  st.alpha = 1.0f;
 
-  const uint32_t full = a.tokens / kKeys;             // unmasked tiles
-  const uint32_t n_tiles = (a.tokens + kKeys - 1) / kKeys;
-  Prefetch pf;
-  if (full > 0)
-    load_tile<kHeadMajor, false>(a, kv_head, 0, pf);
+  store_scales(k0s, sg, ks0);
+  store_scales(k1s, sg, ks1);
+  step_barrier<kWaitAll>();
+  float u[2][16];
+  if (full == 0)
+    first_tile<true>(k0s, qop, qsl, st, u, n, half, a.tokens);
   else
-    load_tile<kHeadMajor, true>(a, kv_head, 0, pf);
-  store_tile(smem, pf);
-  __syncthreads();
+    first_tile<false>(k0s, qop, qsl, st, u, n, half, a.tokens);
+  step_barrier<kWaitAll>();  // K(0)'s stage is refilled by step 0
 
-  for (uint32_t kt = 0; kt < full; ++kt) {
-    const uint32_t next = kt + 1;
-    if (next < full)
-      load_tile<kHeadMajor, false>(a, kv_head, next * kKeys, pf);
-    else if (next < n_tiles)
-      load_tile<kHeadMajor, true>(a, kv_head, next * kKeys, pf);
-    tile_step<false>(smem + (kt & 1) * kStageBytes, qop, qsl, st, n, half, kt * kKeys, a.tokens);
-    if (next < n_tiles) store_tile(smem + (next & 1) * kStageBytes, pf);
-    __syncthreads();
+  // One steady step j (tile j+1 full) on compile-time stages: reads K(j+1) from kn, V(j) from
+  // vc; stages K(j+3) into kc (K(j)'s stage) and V(j+2) into vn2 (V(j-1)'s stage); stores the
+  // scales of K(j+2) (stage kn2) loaded one step earlier.
+#define H3_STEADY(kc, kn, kn2, vc, vn2)                                                       \
+  {                                                                                          \
+    const float ks_new = stage_k<kHeadMajor>(a, sg, kv_head, (j + 3) * kKeys, kc);           \
+    stage_v(a, sg, kv_head, (j + 2) * kKeys, vn2);                                           \
+    step<true, false, false>(kn, vc, qop, qsl, st, u, n, half, (j + 1) * kKeys, a.tokens);   \
+    store_scales(kn2, sg, ks_held);                                                          \
+    ks_held = ks_new;                                                                        \
+    step_barrier<kWaitPrevStep>();                                                           \
+    ++j;                                                                                     \
   }
-  if (full < n_tiles)
-    tile_step<true>(smem + (full & 1) * kStageBytes, qop, qsl, st, n, half, full * kKeys,
-                    a.tokens);
+
+  // ---- steady steps, three per iteration so every stage is a fixed array
+  const uint32_t steady = full > 0 ? full - 1 : 0;  // steps j with tile j+1 full
+  uint32_t j = 0;
+  for (; j + 3 <= steady;) {
+    H3_STEADY(k0s, k1s, k2s, v0s, v2s)
+    H3_STEADY(k1s, k2s, k0s, v1s, v0s)
+    H3_STEADY(k2s, k0s, k1s, v2s, v1s)
+  }
+  if (j < steady) H3_STEADY(k0s, k1s, k2s, v0s, v2s)
+  if (j < steady) H3_STEADY(k1s, k2s, k0s, v1s, v0s)
+#undef H3_STEADY
+
+  // ---- tail (stages chosen at run time): the step into the partial tile, then the last step
+  auto kst = [&](uint32_t t) { const uint32_t r = t % 3; return r == 0 ? k0s : r == 1 ? k1s : k2s; };
+  auto vst = [&](uint32_t t) { const uint32_t r = t % 3; return r == 0 ? v0s : r == 1 ? v1s : v2s; };
+  if (n_tiles > full && full > 0) {  // j == full - 1: tile j+1 is the partial tile
+    step<true, true, false>(kst(j + 1), vst(j), qop, qsl, st, u, n, half, (j + 1) * kKeys,
+                            a.tokens);
+    step_barrier<kWaitAll>();
+    ++j;
+  }
+  if (n_tiles > full)
+    step<false, false, true>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
+  else
+    step<false, false, false>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
+  // The last step raises no max, so no rescale is owed after its PV.
+  step_barrier<kWaitAll>();  // no staging load outlives the workgroup
 
   // ---- normalise and store rows < token_count
   const float l_tot = st.l + __shfl_xor(st.l, 32);
@@ -357,7 +542,7 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_
   a.token_count = token_count;
   a.capacity = cfg.token_capacity;
   a.q_words = cfg.q_stride / 4;
-  a.kv_words = cfg.kv_stride / 4;
+  a.kv_bytes = cfg.kv_stride;
   a.out_stride = cfg.out_stride;
   a.q_blocks = (token_count + kQueriesPerBlock - 1) / kQueriesPerBlock;
   a.heads = heads;
