@@ -28,8 +28,8 @@
 //   phase B  PV(j):  16 f16 MFMAs     with  exp/pack/sum of its last 16 slots (feeding PV(j)'s
 //                                          later MFMAs), then dequant + max of tile j+1 and the
 //                                          raise of the running max
-// so every MFMA has independent VALU work to co-issue with. LDS operands are read two MFMAs
-// ahead.
+// so every MFMA has independent VALU work to co-issue with. LDS operands are read a few MFMAs
+// ahead (H3_ATTN_PF).
 //
 // Staging: K and V^T tiles go from HBM straight into LDS with buffer_load ... lds (LDS-DMA; no
 // registers, no LDS store instructions), through rings of three stages each. Step j reads
@@ -52,15 +52,27 @@
 namespace h3 {
 namespace {
 
-constexpr int kWaves = 4;
+#ifndef H3_ATTN_WAVES
+#define H3_ATTN_WAVES 4
+#endif
+constexpr int kWaves = H3_ATTN_WAVES;  // waves per workgroup, all on one K/V stream
+constexpr int kThreads = 64 * kWaves;
 constexpr int kQueriesPerWave = 32;
-constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;  // 128
+constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;
 constexpr int kKeys = 64;                                   // keys per LDS tile
 constexpr int kRowBytes = 128;                              // unpadded, chunks swizzled
 constexpr int kKRows = kKeys * kRowBytes;                   // 8192
 constexpr int kKStage = kKRows + 2 * kKeys * 4;             // + ks[64], -M*ks[64]: 8704
 constexpr int kVStage = 128 * kRowBytes;                    // 16384
-constexpr int kLoadsPerStep = 7;                            // per wave: 2 K + 4 V^T DMA + 1 ks
+constexpr int kKLoads = 8 / kWaves;                         // 1 KiB LDS-DMA loads per wave
+constexpr int kVLoads = 16 / kWaves;
+constexpr int kSRows = kKeys / kWaves;                      // scale rows stored per wave
+constexpr int kLoadsPerStep = kKLoads + kVLoads + 1;        // + the scale load
+#ifndef H3_ATTN_PF
+#define H3_ATTN_PF 2
+#endif
+constexpr int kPf = H3_ATTN_PF;    // MFMA operands are read from LDS this many MFMAs ahead
+constexpr int kSPf = H3_ATTN_PF;   // and the key scales this many chunks ahead
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMagicBits = 0x4B400000;  // float 12582912 = 1.5 * 2^23
 constexpr float kMagic = 12582912.0f;
@@ -104,10 +116,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
 
 // Per-thread constants of the staging loads.
 struct Stager {
-  uint32_t koff[2];  // byte offset inside a K tile of this lane's 16 bytes, per DMA load
-  uint32_t voff[4];  // byte offset inside a V^T tile (from the head block base + 2*k0)
+  uint32_t koff[kKLoads];  // byte offset inside a K tile of this lane's 16 bytes, per DMA load
+  uint32_t voff[kVLoads];  // byte offset inside a V^T tile (from the head block base + 2*k0)
   uint32_t soff;     // ks element offset (bytes) of this lane's scale row
-  uint32_t srow;     // MFMA row whose scales this lane stores (lanes 0..15 of each wave)
+  uint32_t srow;     // MFMA row whose scales this lane stores (lanes below kSRows)
   int wave;
 };
 
@@ -117,19 +129,19 @@ __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane)
   Stager s;
   s.wave = wave;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const uint32_t o = wave * 2048 + t * 1024 + 16 * lane;
+  for (int t = 0; t < kKLoads; ++t) {
+    const uint32_t o = (wave * kKLoads + t) * 1024 + 16 * lane;
     const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
     const uint32_t key = swap23(row);
     s.koff[t] = (kHeadMajor ? key * 128 : key * a.kv_bytes) + 16 * chunk;
   }
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t o = wave * 4096 + t * 1024 + 16 * lane;
+  for (int t = 0; t < kVLoads; ++t) {
+    const uint32_t o = (wave * kVLoads + t) * 1024 + 16 * lane;
     const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
     s.voff[t] = row * a.capacity * 2 + 16 * chunk;
   }
-  s.srow = 16 * wave + (lane & 15);
+  s.srow = kSRows * wave + (lane & (kSRows - 1));
   const uint32_t skey = swap23(s.srow);
   s.soff = kHeadMajor ? skey * 4 : skey * a.kv_head_limit * 4;
   return s;
@@ -158,9 +170,9 @@ __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32
   }
   const __amdgpu_buffer_rsrc_t rk = rsrc(base, bytes);
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < kKLoads; ++t)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rk, (lds_void*)(kst + sg.wave * 2048 + t * 1024), 16, sg.koff[t], 0, 0, 0);
+        rk, (lds_void*)(kst + (sg.wave * kKLoads + t) * 1024), 16, sg.koff[t], 0, 0, 0);
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(sbase, sbytes),
                                                                          sg.soff, 0, 0));
 }
@@ -174,14 +186,14 @@ __device__ __forceinline__ void stage_v(const Args& a, const Stager& sg, uint32_
   const char* base = reinterpret_cast<const char*>(a.vt) + ((size_t)kv_head * blk + k0) * 2;
   const __amdgpu_buffer_rsrc_t rv = rsrc(base, k0 < blk ? (blk - k0) * 2 : 0u);
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < kVLoads; ++t)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rv, (lds_void*)(vst + sg.wave * 4096 + t * 1024), 16, sg.voff[t], 0, 0, 0);
+        rv, (lds_void*)(vst + (sg.wave * kVLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
 }
 
 // Scales of a staged K tile: ks and -1.5*2^23*ks at its MFMA-row index.
 __device__ __forceinline__ void store_scales(char* kst, const Stager& sg, float ks) {
-  if ((threadIdx.x & 63) < 16) {
+  if ((threadIdx.x & 63) < kSRows) {
     float* sc = reinterpret_cast<float*>(kst + kKRows);
     sc[sg.srow] = ks;
     sc[kKeys + sg.srow] = -(kMagic * ks);
@@ -340,18 +352,19 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
 
   // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
   if (kNext) {
-    kop[0] = *reinterpret_cast<const v4i*>(krow + chunk_off(0, half, sw));
-    kop[1] = *reinterpret_cast<const v4i*>(krow + 32 * kRowBytes + chunk_off(0, half, sw));
+#pragma unroll
+    for (int w = 0; w < kPf; ++w)
+      kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
   }
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int bb = c & 1, dc = c >> 1;
-    if (kNext && c + 2 < 8) {
-      const int w = c + 2;
+    if (kNext && c + kPf < 8) {
+      const int w = c + kPf;
       kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
     }
-    if (c >= 6) {
-      const int w = c - 6;
+    if (c >= 8 - kPf) {
+      const int w = c - (8 - kPf);
       vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
     if (kNext)
@@ -365,12 +378,12 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     const int g = c >> 2, db = c & 3;
-    if (c + 2 < 16) {
-      const int w = c + 2;
+    if (c + kPf < 16) {
+      const int w = c + kPf;
       vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
-    if (kNext && c >= 4 && c < 12) {  // scales of dequant quarter c-4, two chunks ahead
-      const int q = c - 4, kb = 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
+    if (kNext && c >= 6 - kSPf && c < 14 - kSPf) {  // scales of dequant quarter q, kSPf ahead
+      const int q = c - (6 - kSPf), kb = 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
       k4[q] = *reinterpret_cast<const float4*>(kss + kb);
       c4[q] = *reinterpret_cast<const float4*>(kss + kKeys + kb);
     }
@@ -392,7 +405,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
 }
 
 template <bool kHeadMajor>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention(Args a) {
   // Three K stages and three V^T stages, each its own array so that the compiler can tell an
   // LDS-DMA into one stage from the reads of another.
@@ -552,9 +565,9 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_
   a.per_xcd = (a.total + 7) / 8;
   dim3 grid(a.per_xcd * 8);
   if (head_major)
-    hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(k_attention<true>, grid, dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(k_attention<false>, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
