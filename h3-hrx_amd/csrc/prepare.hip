@@ -14,13 +14,55 @@ namespace {
 
 constexpr int kRowsPerBlock = 8;  // 256 threads = 8 half-waves = 8 (token, head) rows
 
-// Butterfly partner exchange inside a 32-lane half-wave.
-__device__ __forceinline__ float xor32(float v, int mask) { return __shfl_xor(v, mask, 32); }
+// Butterfly partner exchange inside a 32-lane half-wave, on the vector pipe: lane masks 1, 2 and
+// 8 are one DPP move (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:8), mask 4 is two
+// (row_half_mirror then quad_perm [3,2,1,0]); mask 16 is v_permlane16_swap, which yields the
+// values of both members of each lane pair at once (the lane with bit 4 clear first).
+__device__ __forceinline__ float dpp(float v, int ctrl) {
+  switch (ctrl) {  // the control must be an immediate
+    case 0xB1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+    case 0x4E: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+    case 0x141: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));
+    case 0x1B: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x1B, 0xF, 0xF, true));
+    default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+  }
+}
+__device__ __forceinline__ float xor_partner(float v, int k) {  // k in {1, 2, 4, 8}
+  if (k == 1) return dpp(v, 0xB1);
+  if (k == 2) return dpp(v, 0x4E);
+  if (k == 4) return dpp(dpp(v, 0x141), 0x1B);
+  return dpp(v, 0x128);
+}
+__device__ __forceinline__ void pair16(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+// Sum and max over the 32 lanes of a half-wave in the order k = 1, 2, 4, 8, 16 (sum) and any
+// order (max); every lane gets the result.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int k = 1; k < 16; k <<= 1) v = v + xor_partner(v, k);
+  float lo, hi;
+  pair16(v, lo, hi);
+  return lo + hi;
+}
+__device__ __forceinline__ float half_max(float v) {
+  float lo, hi;
+  pair16(v, lo, hi);
+  v = fmaxf(lo, hi);
+#pragma unroll
+  for (int k = 8; k >= 1; k >>= 1) v = fmaxf(v, xor_partner(v, k));
+  return v;
+}
 
 // The unnormalised Sylvester Hadamard H_128 over the 32 lanes of a half-wave, lane l holding
 // elements 4l..4l+3, in the reference's fp32 order (kernels/prepare_qk_i8.loom:84-156):
 // an in-lane stage over element bits 0-1, then lane butterflies k = 1, 2, 4, 8, 16 where the
 // lane with bit k clear keeps s + partner and the lane with bit k set keeps partner - s.
+// Each lane stage computes fma(s, sign, p) with sign = +1 (bit clear: s + p) or -1 (bit set:
+// p - s): one correctly rounded addition either way, so the bits are those of the reference.
 __device__ __forceinline__ v4f hadamard128(v4f y, int lane) {
   float ab_p = y[0] + y[1], ab_m = y[0] - y[1];
   float cd_p = y[2] + y[3], cd_m = y[2] - y[3];
@@ -30,13 +72,17 @@ __device__ __forceinline__ v4f hadamard128(v4f y, int lane) {
   s[2] = ab_p - cd_p;
   s[3] = ab_m - cd_m;
 #pragma unroll
-  for (int k = 1; k < 32; k <<= 1) {
-    const bool hi = (lane & k) != 0;
+  for (int k = 1; k < 16; k <<= 1) {
+    const float sign = (lane & k) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float p = xor32(s[j], k);
-      s[j] = hi ? (p - s[j]) : (s[j] + p);
-    }
+    for (int j = 0; j < 4; ++j) s[j] = __builtin_fmaf(s[j], sign, xor_partner(s[j], k));
+  }
+  const float sign16 = (lane & 16) ? -1.0f : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float lo, hi;
+    pair16(s[j], lo, hi);  // bit clear: lo + hi = s + p; bit set: lo - hi = p - s
+    s[j] = __builtin_fmaf(hi, sign16, lo);
   }
   return s;
 }
@@ -46,8 +92,7 @@ __device__ __forceinline__ v4f hadamard128(v4f y, int lane) {
 // packed low byte first. Returns the packed word of this lane; *scale gets amax/127 * extra.
 __device__ __forceinline__ uint32_t quantize_row(v4f r, float extra, float* scale) {
   float m = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
-#pragma unroll
-  for (int k = 16; k >= 1; k >>= 1) m = fmaxf(m, xor32(m, k));
+  m = half_max(m);
   float amax = fmaxf(m, 1.0000000000000001e-30f);
   float sc = amax / 127.0f;
   float inv = 127.0f / amax;
@@ -74,16 +119,28 @@ __device__ __forceinline__ uint2 load4(const void* base, size_t elem_index) {
 // The maths is the reference's (kernels/prepare_qk_rope_i8hm.loom:110-130,
 // kernels/rope_qknorm_f16.loom); the device code is shared by every kernel that needs it, so
 // fused and separate routes produce identical bits.
-__device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* weight,
-                                                const float* cos_row, const float* sin_row,
-                                                float eps) {
+// The table values one lane needs for its four channels: norm weights, cos and sin.
+struct RopeLane {
+  float4 w, c, s;
+};
+
+__device__ __forceinline__ RopeLane rope_lane(int lane, const float* weight, const float* cos_row,
+                                              const float* sin_row) {
+  const int pairlane = lane < 12 ? lane : (lane < 24 ? lane - 12 : 0);
+  RopeLane t;
+  t.w = *reinterpret_cast<const float4*>(weight + 4 * lane);
+  t.c = *reinterpret_cast<const float4*>(cos_row + 4 * pairlane);
+  t.s = *reinterpret_cast<const float4*>(sin_row + 4 * pairlane);
+  return t;
+}
+
+__device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const RopeLane& tab, float eps) {
   float part = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
-#pragma unroll
-  for (int k = 1; k < 32; k <<= 1) part = part + xor32(part, k);
+  part = half_sum(part);
   float ms = part * 0.0078125f;
   float me = ms + eps;
   float r = 1.0f / __builtin_sqrtf(me);
-  const float4 w = *reinterpret_cast<const float4*>(weight + 4 * lane);
+  const float4 w = tab.w;
   v4f xn;
   xn[0] = (v[0] * r) * w.x;
   xn[1] = (v[1] * r) * w.y;
@@ -91,13 +148,11 @@ __device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* we
   xn[3] = (v[3] * r) * w.w;
   const bool lo = lane < 12, pair = lane < 24;
   const int partner = lo ? lane + 12 : (pair ? lane - 12 : lane);
-  const int pairlane = lo ? lane : (pair ? lane - 12 : 0);
   v4f px;
 #pragma unroll
   for (int j = 0; j < 4; ++j) px[j] = __shfl(xn[j], partner, 32);
-  const float4 c = *reinterpret_cast<const float4*>(cos_row + 4 * pairlane);
-  const float4 s = *reinterpret_cast<const float4*>(sin_row + 4 * pairlane);
-  const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
+  const float cc[4] = {tab.c.x, tab.c.y, tab.c.z, tab.c.w};
+  const float ss[4] = {tab.s.x, tab.s.y, tab.s.z, tab.s.w};
   v4f out;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -108,6 +163,12 @@ __device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* we
     out[j] = (float)(_Float16)o;
   }
   return out;
+}
+
+__device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* weight,
+                                                const float* cos_row, const float* sin_row,
+                                                float eps) {
+  return rmsnorm_rope_f16(v, lane, rope_lane(lane, weight, cos_row, sin_row), eps);
 }
 
 // ---------------------------------------------------------------- quantizer kernels
@@ -145,33 +206,39 @@ __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
 
 // RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
 // (kernels/prepare_qk_rope_i8hm.loom:94-239; mean == nullptr is the reference's unsmoothed
-// kernel, a mean is this build's fused K-smoothing second pass).
+// kernel, a mean is this build's fused K-smoothing second pass). One half-wave owns one token and
+// walks its heads: the token's RoPE tables are read once (not once per head), its heads' inputs
+// are one contiguous run of the fused row, and the eight half-waves of a workgroup write eight
+// consecutive head-major rows (1 KiB) per head.
 __global__ __launch_bounds__(256) void k_prepare_qk_rope(
     const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const float* __restrict__ mean, int32_t* __restrict__ codes,
     float* __restrict__ scales, uint32_t tokens, uint32_t row_stride, uint32_t head_offset,
     uint32_t heads, uint32_t capacity, float extra, float eps, uint32_t elem) {
-  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  const uint32_t t = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
   const int lane = threadIdx.x & 31;
-  if (row >= tokens * heads) return;
-  const uint32_t t = row % tokens;
-  const uint32_t h = row / tokens;
-  const uint32_t col = head_offset + 128u * h + 4u * lane;
-  v4f v = widen4(load4(x, (size_t)t * row_stride + col), elem);
-  v4f y = rmsnorm_rope_f16(v, lane, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48, eps);
-  if (mean) {
-    const float4 m = *reinterpret_cast<const float4*>(mean + 128u * h + 4u * lane);
-    y[0] = y[0] - m.x;
-    y[1] = y[1] - m.y;
-    y[2] = y[2] - m.z;
-    y[3] = y[3] - m.w;
+  if (t >= tokens) return;
+  const RopeLane tab = rope_lane(lane, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48);
+  const size_t row0 = (size_t)t * row_stride + head_offset + 4u * lane;
+  uint2 next = load4(x, row0);
+  for (uint32_t h = 0; h < heads; ++h) {
+    const v4f v = widen4(next, elem);
+    if (h + 1 < heads) next = load4(x, row0 + 128u * (h + 1));  // one head ahead
+    v4f y = rmsnorm_rope_f16(v, lane, tab, eps);
+    if (mean) {
+      const float4 m = *reinterpret_cast<const float4*>(mean + 128u * h + 4u * lane);
+      y[0] = y[0] - m.x;
+      y[1] = y[1] - m.y;
+      y[2] = y[2] - m.z;
+      y[3] = y[3] - m.w;
+    }
+    v4f r = hadamard128(y, lane);
+    float scale;
+    uint32_t word = quantize_row(r, extra, &scale);
+    size_t out_row = (size_t)h * capacity + t;
+    codes[out_row * 32 + lane] = (int32_t)word;
+    if (lane == 0) scales[out_row] = scale;
   }
-  v4f r = hadamard128(y, lane);
-  float scale;
-  uint32_t word = quantize_row(r, extra, &scale);
-  size_t out_row = (size_t)h * capacity + t;
-  codes[out_row * 32 + lane] = (int32_t)word;
-  if (lane == 0) scales[out_row] = scale;
 }
 
 // RMSNorm + RoPE of Q and K heads to f16, V optionally copied (kernels/rope_qknorm_f16.loom).
@@ -364,8 +431,7 @@ hipError_t launch_prepare_qk_rope_mean(const h3_prepare_cfg& cfg, uint32_t token
                                        const float* weight, const float* cos_t,
                                        const float* sin_t, const float* mean, int32_t* codes,
                                        float* scales, hipStream_t stream) {
-  const uint32_t rows = tokens * cfg.heads;
-  hipLaunchKernelGGL(k_prepare_qk_rope, dim3(div_up(rows, kRowsPerBlock)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(k_prepare_qk_rope, dim3(div_up(tokens, kRowsPerBlock)), dim3(256), 0, stream,
                      x, weight, cos_t, sin_t, mean, codes, scales, tokens, cfg.row_stride,
                      cfg.head_offset, cfg.heads, cfg.token_capacity, cfg.extra_scale, cfg.eps,
                      cfg.elem);
