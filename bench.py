@@ -69,9 +69,17 @@ def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
     threads = min(threads, 16)
     rng = np.random.default_rng(1)
     rows = np.sort(rng.choice(tokens, size=rows_per_head, replace=False)).astype(np.int32)
-    per_row_s, fixed_s, _ = O.cpu_baseline(q16, k16, v16, tokens, heads, rows, threads)
-    call_s = fixed_s + per_row_s * tokens / rows_per_head
+    sample_s, fixed_s, _ = O.cpu_baseline(q16, k16, v16, tokens, heads, rows, threads)
+    call_s = fixed_s + sample_s * tokens / rows_per_head
     ops = 4.0 * tokens * tokens * heads * 128
+    # single core, on the first s1 tokens of the same data (both the per-call operand pass and
+    # the per-row attention cost are linear in the sequence length, so both scale by tokens/s1)
+    s1 = min(tokens, 8192)
+    rows1 = np.sort(rng.choice(s1, size=2, replace=False)).astype(np.int32)
+    sample1, fixed1, _ = O.cpu_baseline(np.ascontiguousarray(q16[:s1]), np.ascontiguousarray(k16[:s1]),
+                                         np.ascontiguousarray(v16[:s1]), s1, heads, rows1, 1)
+    scale1 = tokens / s1
+    call1_s = fixed1 * scale1 + sample1 * scale1 * tokens / 2
     return {
         "value": ops / call_s / 1e12,
         "unit": "TOPS",
@@ -79,8 +87,16 @@ def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
         "cores": threads,
         "kind": "port",
         "sample": (f"{rows_per_head} query rows x {heads} heads of S={tokens} (f64 attention, "
-                   f"{per_row_s:.2f} s) plus the per-call K operand/mean/V^T pass "
-                   f"({fixed_s:.2f} s) measured; ms_per_call extrapolated linearly in rows"),
+                   f"{sample_s:.2f} s) plus the per-call K operand/mean/V^T pass "
+                   f"({fixed_s:.2f} s) measured on {threads} threads; ms_per_call extrapolated "
+                   f"linearly in rows"),
+        "single_core": {
+            "value": ops / call1_s / 1e12,
+            "ms_per_call": call1_s * 1e3,
+            "sample": (f"1 thread, 2 query rows x {heads} heads and the operand pass on the first "
+                       f"{s1} tokens ({sample1:.2f} s + {fixed1:.2f} s), scaled by S/{s1} "
+                       f"(linear per row and per pass) and rows"),
+        },
     }
 
 
@@ -103,10 +119,10 @@ def copy_calibration(torch) -> None:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-rows", type=int, default=8, help="query rows per head for the CPU leg")
+    ap.add_argument("--cpu-rows", type=int, default=32, help="query rows per head for the CPU leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (the HBM-counter calibration)")
@@ -180,6 +196,7 @@ def main() -> None:
     ms_step = wall * 1e3 / args.steps
     att_ms = [a.elapsed_time(b) for a, b in att_events]
     att_avg = sum(att_ms) / len(att_ms)
+    att_q = np.percentile(np.array(att_ms), [25, 50, 75])
     ops = 4.0 * tokens * tokens * heads * 128  # QK + PV multiply-adds x2 (benches/kernels.rs:570)
     value = ops / (ms_step * 1e-3) / 1e12
     achieved = ops / (att_avg * 1e-3) / 1e12
@@ -210,6 +227,8 @@ def main() -> None:
                     "+ attention_i8qkhm",
         },
         "attention_ms": round(att_avg, 4),
+        "attention_ms_median": round(float(att_q[1]), 4),
+        "attention_ms_iqr": [round(float(att_q[0]), 4), round(float(att_q[2]), 4)],
         "attention_tops": round(achieved, 3),
         "attention_frac_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
         "output_finite": out_ok,
