@@ -31,6 +31,9 @@ WORKLOADS = {
     # name: (tokens, heads, rope grid (t, h, w))
     "c3": (129024, 32, (32, 42, 96)),
     "c2": (31104, 32, (24, 24, 54)),
+    # config 4's self-attention: the 129,024 video tokens and 1,248 audio tokens as one sequence
+    # (the audio rows continue the grid as a 33rd frame)
+    "c4": (130272, 32, (32, 42, 96)),
     "c1": (1024, 8, (1, 32, 32)),
 }
 

@@ -134,9 +134,10 @@ def test_token_count_below_tokens_writes_only_those_rows(dev):
     assert np.all(np.abs(got[rows] - want) <= 1e-3 + 2e-3 * np.abs(want))
 
 
-@pytest.mark.parametrize("tokens,heads", [(31104, 32), (129024, 32)])
+@pytest.mark.parametrize("tokens,heads", [(31104, 32), (129024, 32), (130272, 32)])
 def test_baseline_shapes_on_sampled_rows(dev, tokens, heads):
-    """BASELINE configs 2 and 3 at full size: every query row is computed by the kernel, a
+    """BASELINE configs 2, 3 and 4 (the joint 129,024 + 1,248-token sequence) at full size: every
+    query row is computed by the kernel, a
     sample of rows (first, last, tile edges, random) is checked against the f64 oracle to the
     north star's tolerance."""
     import torch
