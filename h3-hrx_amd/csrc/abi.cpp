@@ -349,6 +349,43 @@ int h3_transpose_qkv_v_f16(const h3_transpose_cfg* cfg, uint32_t launch_rows, ui
                           reinterpret_cast<hipStream_t>(stream), true);
 }
 
+int h3_gemm_i8_qkv_256(const h3_gemm_cfg* cfg, uint32_t tokens, h3_view a, h3_view w,
+                       h3_view w_scale, h3_view a_scale, h3_view out, h3_stream stream) {
+  const char* stage = "gemm_i8_qkv_256";
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  // kernels/gemm_packed_256.loom:3432-3440
+  if (!in_range(cfg->k_size, 64, 65536, 64))
+    return set_error(H3_ERR_CONFIG, "%s: k_size %u outside [64, 65536] step 64", stage,
+                     cfg->k_size);
+  if (!in_range(cfg->n_size, 384, 65536, 384))
+    return set_error(H3_ERR_CONFIG, "%s: n_size %u outside [384, 65536] step 384", stage,
+                     cfg->n_size);
+  if (!in_range(cfg->k_stride, 64, 65536, 64) || cfg->k_stride < cfg->k_size)
+    return set_error(H3_ERR_CONFIG, "%s: k_stride %u outside [k_size=%u, 65536] step 64", stage,
+                     cfg->k_stride, cfg->k_size);
+  if (!in_range(cfg->m_group, 1, 4))
+    return set_error(H3_ERR_CONFIG, "%s: m_group %u outside [1, 4]", stage, cfg->m_group);
+  if (!in_range(tokens, 1, 16777216))
+    return set_error(H3_ERR_ARGUMENT, "%s: tokens %u outside [1, 16777216]", stage, tokens);
+  // src/dispatch.rs:1025-1045: the V^T tail is padded to the 256-row capacity.
+  const size_t t = tokens, n = cfg->n_size, cap = (t + 255) / 256 * 256;
+  h3_view views[5] = {a, w, w_scale, a_scale, out};
+  size_t need[5] = {t * cfg->k_stride, n * cfg->k_stride, n * 4, t * 4,
+                    (t * n + (cap - t) * (n / 3)) * 2};
+  int st = check_bindings(stage, views, need, 5);
+  if (st) return st;
+  if (reinterpret_cast<uintptr_t>(out.ptr) % 8 != 0)
+    return set_error(H3_ERR_ARGUMENT, "%s: out is not 8-byte aligned", stage);
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_gemm_i8_qkv(tokens, cfg->n_size, cfg->k_size, cfg->k_stride,
+                                            static_cast<const int8_t*>(a.ptr),
+                                            static_cast<const int8_t*>(w.ptr),
+                                            static_cast<const float*>(w_scale.ptr),
+                                            static_cast<const float*>(a_scale.ptr),
+                                            static_cast<uint16_t*>(out.ptr),
+                                            reinterpret_cast<hipStream_t>(stream)));
+}
+
 int h3_attention_i8qkhm(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_stream stream) {

@@ -78,6 +78,15 @@ class AttentionCfg(ctypes.Structure):
     ]
 
 
+class GemmCfg(ctypes.Structure):
+    _fields_ = [
+        ("k_size", ctypes.c_uint32),
+        ("n_size", ctypes.c_uint32),
+        ("k_stride", ctypes.c_uint32),
+        ("m_group", ctypes.c_uint32),
+    ]
+
+
 class StackDims(ctypes.Structure):
     _fields_ = [
         ("heads", ctypes.c_uint32),
@@ -119,6 +128,11 @@ SIGNATURES = {
         ctypes.c_int),
     "h3_attention_i8qk": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View, _S],
+        ctypes.c_int),
+    "h3_gemm_i8_qkv_256": (
+        [_P(GemmCfg), ctypes.c_uint32, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_rope_dit_tables": (
+        [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
         ctypes.c_int),
     "h3_capacity": ([ctypes.c_uint32, ctypes.c_int], ctypes.c_uint32),
     "h3_stack_build": ([_P(StackDims), ctypes.c_void_p], ctypes.c_int),
@@ -261,6 +275,34 @@ def attention_i8qk(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, 
                    stream=None) -> None:
     check(lib().h3_attention_i8qk(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
                                   view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
+
+
+def gemm_i8_qkv_256(cfg: GemmCfg, tokens: int, a, w, w_scale, a_scale, out, stream=None) -> None:
+    check(lib().h3_gemm_i8_qkv_256(ctypes.byref(cfg), tokens, view(a), view(w), view(w_scale),
+                                   view(a_scale), view(out), stream_ptr(stream)))
+
+
+def compact_qkv_elements(tokens: int, n: int) -> int:
+    """f16 elements of the compact QKV output (src/dispatch.rs:1038-1043)."""
+    cap = -(-tokens // 256) * 256
+    return tokens * n + (cap - tokens) * (n // 3)
+
+
+def rope_dit_tables(pos, inv_freq):
+    """rope::dit on the host: pos [rows][3] float64, inv_freq [16] float32 (numpy arrays);
+    returns (cos, sin) float32 [rows][48]."""
+    import numpy as np
+
+    pos = np.ascontiguousarray(pos, np.float64).reshape(-1)
+    inv = np.ascontiguousarray(inv_freq, np.float32)
+    if inv.size != 16 or pos.size % 3:
+        raise ValueError("pos must hold [rows][3] coordinates and inv_freq 16 frequencies")
+    rows = pos.size // 3
+    cos = np.empty((rows, 48), np.float32)
+    sin = np.empty((rows, 48), np.float32)
+    check(lib().h3_rope_dit_tables(pos.ctypes.data, rows, inv.ctypes.data, cos.ctypes.data,
+                                   sin.ctypes.data))
+    return cos, sin
 
 
 def capacity(tokens: int, causal: bool = False) -> int:

@@ -155,6 +155,43 @@ int h3_transpose_f16(const h3_transpose_cfg *cfg, uint32_t launch_rows, uint32_t
 int h3_transpose_qkv_v_f16(const h3_transpose_cfg *cfg, uint32_t launch_rows, uint32_t rows,
                            h3_view x, h3_view out, h3_stream stream);
 
+/* ------------------------------------------------------------------ producers of the operands */
+
+/* Config of h3.gemm_i8_qkv_256 (kernels/gemm_packed_256.loom:3432-3440; src/dispatch.rs:758-790):
+ *   k_size    multiple of 64 in [64, 65536]: reduction length
+ *   n_size    multiple of 384 in [384, 65536]: output channels (Q, K, V thirds)
+ *   k_stride  multiple of 64 in [64, 65536], >= k_size: bytes per operand row
+ *   m_group   [1, 4]: the reference's raster grouping; accepted and validated, the raster here
+ *             is fixed by the kernel. */
+typedef struct {
+  uint32_t k_size;
+  uint32_t n_size;
+  uint32_t k_stride;
+  uint32_t m_group;
+} h3_gemm_cfg;
+
+/* h3_gemm_i8_qkv_256 (kernels/gemm_packed_256.loom:3429-3471, the packed_256 template at
+ * 14-412; bindings src/dispatch.rs:1025-1045): the compact INT8 QKV projection.
+ *   acc = sum_k a[m][k] * w[n][k] (int8, exact int32);
+ *   v = ((float)acc * w_scale[n]) * a_scale[m] + 0.0, clamped to +-65472 when finite;
+ *   n < 2N/3: out[m][n] f16 with row pitch 2N/3 (Q and K rows);
+ *   n >= 2N/3: V^T, out[M*2N/3 + (n - 2N/3)*cap + m] f16, cap = ceil(M/256)*256, zero for
+ *   M <= m < cap.
+ *   a [tokens][k_stride] int8, w [n_size][k_stride] int8, w_scale [n_size] f32,
+ *   a_scale [tokens] f32, out (tokens*n_size + (cap - tokens)*n_size/3) f16 (8-byte aligned).
+ *   tokens in [1, 16777216]. */
+int h3_gemm_i8_qkv_256(const h3_gemm_cfg *cfg, uint32_t tokens, h3_view a, h3_view w,
+                       h3_view w_scale, h3_view a_scale, h3_view out, h3_stream stream);
+
+/* rope::dit (src/rope.rs:11-37), on the host: the DiT's cos/sin tables [rows][48] f32 for
+ * h3_prepare_qk_rope_i8hm and h3_rope_qknorm_f16. For row r and axis a in 0..2, with
+ * p = (float)pos[3r + a] and angle = p * inv_freq[j] in f32 (j in 0..15):
+ * cos_t[48r + 16a + j] = cosf(angle), sin_t[...] = sinf(angle).
+ * pos [rows][3] f64, inv_freq [16] f32, cos_t/sin_t [rows][48] f32: HOST pointers. No device
+ * work; safe to call without a GPU. */
+int h3_rope_dit_tables(const double *pos, size_t rows, const float *inv_freq, float *cos_t,
+                       float *sin_t);
+
 /* ------------------------------------------------------------------ attention */
 
 /* Config of h3.attention_i8qk_* / attention_i8qkhm_mha8_k64_lds_f16_wmma

@@ -462,3 +462,37 @@ double h3o_cpu_baseline(const uint16_t *q, const uint16_t *k, const uint16_t *v,
   free(kmean); free(zmean); free(kc); free(qc); free(ks); free(qs); free(vt);
   return t1 - tm;
 }
+
+/* kernels/gemm_packed_256.loom:370-397 (the f32 epilogue of one output) in the scalar form of
+ * tests/kernels.rs:4436-4441: (dot as f32 * ws) * as + 0, clamped to +-65472 when finite. */
+static uint16_t gemm_finish(int32_t dot, float ws, float as) {
+  float raw = (float)dot * ws;
+  raw = raw * as;
+  raw = raw + 0.0f;
+  if (isfinite(raw)) raw = raw < -65472.0f ? -65472.0f : (raw > 65472.0f ? 65472.0f : raw);
+  return h3o_float_to_half(raw);
+}
+
+void h3o_gemm_i8_qkv(const int8_t *a, const int8_t *w, const float *ws, const float *as, int m,
+                     int n, int k, int k_stride, uint16_t *out, int threads) {
+  const int qk = 2 * (n / 3);
+  const size_t cap = ((size_t)m + 255) / 256 * 256;
+  uint16_t *vt = out + (size_t)m * qk;
+  if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int r = 0; r < m; ++r) {
+    const int8_t *ar = a + (size_t)r * k_stride;
+    for (int col = 0; col < n; ++col) {
+      const int8_t *wr = w + (size_t)col * k_stride;
+      int32_t dot = 0;
+      for (int i = 0; i < k; ++i) dot += (int32_t)ar[i] * (int32_t)wr[i];
+      const uint16_t h = gemm_finish(dot, ws[col], as[r]);
+      if (col < qk)
+        out[(size_t)r * qk + col] = h;
+      else
+        vt[(size_t)(col - qk) * cap + r] = h;
+    }
+  }
+  for (int c = 0; c < n / 3; ++c)
+    for (size_t r = (size_t)m; r < cap; ++r) vt[(size_t)c * cap + r] = 0;
+}

@@ -24,6 +24,13 @@
  *                           to the reference's f64 oracle (tests/kernels.rs:1146-1180) within
  *                           2e-2 abs + 2e-2 rel, and by the identity-rotation special case.
  *   h3o_transpose_f16       kernels/transpose_f16.loom: bit permutation plus zero tail.
+ *   h3o_gemm_i8_qkv         the compact INT8 QKV projection, kernels/gemm_packed_256.loom:
+ *                           14-412 as h3_gemm_i8_qkv_256 (3429-3471), in the scalar form of the
+ *                           reference test tests/kernels.rs:4392-4460. Pinned by that test's
+ *                           closed-form inputs and assertions (non-finite weight scales, a 100x
+ *                           scale that saturates to 65472, zero V padding), by exact int64 dot
+ *                           products, and by an independent numpy restatement (float32 ops,
+ *                           astype(float16)) in tests/test_oracle_gemm.py.
  *   h3o_attention_f64       the attention the operands define, tests/kernels.rs:1891-1913 and
  *                           2084-2111: softmax_j(sum(qc*kc) * qs * ks) . V in f64. Pinned by
  *                           closed forms: uniform keys give the mean of V, a single dominant key
@@ -110,6 +117,14 @@ void h3o_unpack_codes(const int32_t *words, size_t n_rows, int8_t *codes);
 double h3o_cpu_baseline(const uint16_t *q, const uint16_t *k, const uint16_t *v, int tokens,
                         int heads, const int *rows, int n_rows, int threads, double *out,
                         double *fixed_seconds);
+
+/* Compact INT8 QKV projection (kernels/gemm_packed_256.loom:14-412, 3429-3471;
+ * tests/kernels.rs:4392-4460): a [m][k_stride] int8, w [n][k_stride] int8 (first k bytes of each
+ * row used), ws [n], as [m] f32; out f16 bits, m*n + (cap-m)*n/3 elements, cap = ceil(m/256)*256:
+ * Q/K rows [m][2n/3], then V^T [n/3][cap] with zero columns m..cap-1.
+ * threads: OpenMP threads (<= 0: all). */
+void h3o_gemm_i8_qkv(const int8_t *a, const int8_t *w, const float *ws, const float *as, int m,
+                     int n, int k, int k_stride, uint16_t *out, int threads);
 
 int h3o_max_threads(void);
 

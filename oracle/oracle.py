@@ -73,6 +73,8 @@ def lib():
         L.h3o_cpu_baseline.argtypes = [u16, u16, u16, c_int, c_int, _P(np.int32, flags="C"),
                                        c_int, c_int, f64, ctypes.POINTER(c_double)]
         L.h3o_cpu_baseline.restype = c_double
+        L.h3o_gemm_i8_qkv.argtypes = [i8, i8, f32, f32, c_int, c_int, c_int, c_int, u16, c_int]
+        L.h3o_gemm_i8_qkv.restype = None
         L.h3o_max_threads.argtypes = []
         L.h3o_max_threads.restype = c_int
         _lib = L
@@ -217,3 +219,18 @@ def cpu_baseline(q_bits, k_bits, v_bits, tokens, heads, rows, threads=0):
 
 def max_threads() -> int:
     return int(lib().h3o_max_threads())
+
+
+def gemm_i8_qkv(a: np.ndarray, w: np.ndarray, ws: np.ndarray, as_: np.ndarray, k: int,
+                threads: int = 0) -> np.ndarray:
+    """Compact INT8 QKV projection; a [m][k_stride] int8, w [n][k_stride] int8. Returns the f16
+    bits of the whole output: m*n + (cap - m)*n/3 elements (Q/K rows, then V^T)."""
+    a = np.ascontiguousarray(a, np.int8)
+    w = np.ascontiguousarray(w, np.int8)
+    m, k_stride = a.shape
+    n = w.shape[0]
+    cap = -(-m // 256) * 256
+    out = np.zeros(m * n + (cap - m) * (n // 3), np.uint16)
+    lib().h3o_gemm_i8_qkv(a.reshape(-1), w.reshape(-1), np.ascontiguousarray(ws, np.float32),
+                          np.ascontiguousarray(as_, np.float32), m, n, k, k_stride, out, threads)
+    return out

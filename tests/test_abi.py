@@ -157,3 +157,38 @@ def test_python_layer_raises_with_status():
     with pytest.raises(H.H3Error) as e:
         H.check(H.lib().h3_colmean_f32(128, 0, 10, fake(1), fake(1), None))
     assert e.value.status == H.H3_ERR_CONFIG
+
+
+def call_gemm(cfg, tokens, sizes):
+    return H.lib().h3_gemm_i8_qkv_256(ctypes.byref(cfg), tokens, *[fake(n) for n in sizes], None)
+
+
+def test_gemm_bindings_follow_the_reference_extents():
+    """src/dispatch.rs:1025-1045: a t*k_stride, w n*k_stride, scales, and the compact output
+    t*n + (ceil(t/256)*256 - t)*n/3 f16 elements."""
+    t, k, n = 300, 128, 768
+    cfg = H.GemmCfg(k, n, k, 2)
+    need = [t * k, n * k, n * 4, t * 4, (t * n + (512 - t) * (n // 3)) * 2]
+    for i in range(5):
+        sizes = list(need)
+        sizes[i] -= 1
+        st = call_gemm(cfg, t, sizes)
+        assert st == H.H3_ERR_BINDING and H.last_error() == (
+            f"gemm_i8_qkv_256: binding {i} is {sizes[i]} bytes, the kernel addresses {need[i]}")
+
+
+@pytest.mark.parametrize("field,value", [("k_size", 96), ("k_size", 0), ("n_size", 512),
+                                         ("n_size", 65664), ("k_stride", 64), ("m_group", 0),
+                                         ("m_group", 5)])
+def test_gemm_config_outside_declared_ranges_is_refused(field, value):
+    cfg = H.GemmCfg(128, 768, 128, 1)
+    setattr(cfg, field, value)
+    assert call_gemm(cfg, 16, [1 << 40] * 5) == H.H3_ERR_CONFIG, H.last_error()
+
+
+def test_gemm_rejects_misaligned_output_and_bad_token_counts():
+    cfg = H.GemmCfg(128, 768, 128, 1)
+    lib = H.lib()
+    views = [fake(1 << 40)] * 4 + [H.raw_view(0x1004, 1 << 40)]
+    assert lib.h3_gemm_i8_qkv_256(ctypes.byref(cfg), 16, *views, None) == H.H3_ERR_ARGUMENT
+    assert call_gemm(cfg, 0, [1 << 40] * 5) == H.H3_ERR_ARGUMENT
