@@ -190,6 +190,48 @@ int h3_stack_attend_fused(h3_stack* s, uint32_t t, h3_view fused, h3_view qnorm,
   return stack_attention(s, t, out, stream);
 }
 
+int h3_stack_attend_compact(h3_stack* s, uint32_t t, h3_view compact, h3_view qnorm,
+                            h3_view knorm, h3_view cos_t, h3_view sin_t, h3_view out,
+                            h3_stream stream) {
+  if (!s) return set_error(H3_ERR_ARGUMENT, "attention: null stack");
+  // src/stack.rs:634-642: the compact route needs the fused operands and a capacity equal to
+  // the 256-row cover the projection writes V^T with.
+  const uint32_t tokens = s->d.tokens;
+  if (!s->fused || s->capacity != (tokens + 255) / 256 * 256)
+    return set_error(H3_ERR_ARGUMENT,
+                     "compact operands need the fused route and capacity == ceil(tokens/256)*256 "
+                     "(capacity %u, tokens %u)", s->capacity, tokens);
+  // V^T sits after the Q/K rows of the stack's token count (src/stack.rs:1034-1040), where the
+  // projection of those tokens wrote it.
+  if (t != tokens)
+    return set_error(H3_ERR_ARGUMENT, "compact operands: t %u must equal the stack's tokens %u", t,
+                     tokens);
+  const size_t rows = t, inner = (size_t)s->d.heads * 128;
+  const size_t vt_offset = rows * 2 * inner * 2, vt_bytes = inner * s->capacity * 2;
+  const char* stage = "fused attention operands";
+  int st;
+  if ((st = require(stage, 0, compact, vt_offset + vt_bytes)) ||
+      (st = require("attention", 5, out, rows * inner * 2)))
+    return st;
+  // src/stack.rs:643-648: Q/K rows of 2*inner elements, f16 (the projection's output)
+  h3_prepare_cfg pq = s->prep_q, pk = s->prep_k;
+  pq.row_stride = pk.row_stride = (uint32_t)(2 * inner);
+  pq.elem = pk.elem = H3_ELEM_F16;
+  h3_view qk = {compact.ptr, vt_offset};
+  if ((st = h3_prepare_qk_rope_i8hm(&pq, t, qk, qnorm, cos_t, sin_t, s->qi, s->qs, stream)))
+    return st;
+  if (s->smooth)
+    st = h3_prepare_k_rope_smooth_i8hm(&pk, t, qk, knorm, cos_t, sin_t, s->kmean, s->ki, s->ks,
+                                       stream);
+  else
+    st = h3_prepare_qk_rope_i8hm(&pk, t, qk, knorm, cos_t, sin_t, s->ki, s->ks, stream);
+  if (st) return st;
+  // No transpose: the projection already wrote V^T (src/stack.rs:1596-1598).
+  const h3_view vt = {static_cast<char*>(compact.ptr) + vt_offset, vt_bytes};
+  return h3_attention_i8qkhm(&s->attention, t, s->d.heads, s->qi, s->qs, s->ki, s->ks, vt, out,
+                             stream);
+}
+
 int h3_stack_attend(h3_stack* s, uint32_t t, h3_view q, h3_view k, h3_view v, h3_view out,
                     h3_stream stream) {
   if (!s) return set_error(H3_ERR_ARGUMENT, "attention: null stack");

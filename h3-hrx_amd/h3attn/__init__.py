@@ -140,6 +140,8 @@ SIGNATURES = {
     "h3_stack_capacity": ([ctypes.c_void_p], ctypes.c_uint32),
     "h3_stack_attend_fused": (
         [ctypes.c_void_p, ctypes.c_uint32, View, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_stack_attend_compact": (
+        [ctypes.c_void_p, ctypes.c_uint32, View, View, View, View, View, View, _S], ctypes.c_int),
     "h3_stack_attend": ([ctypes.c_void_p, ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
     "h3_stack_operands": ([ctypes.c_void_p, _P(IntQk)], ctypes.c_int),
 }
@@ -336,6 +338,11 @@ class Stack:
     def attend_fused(self, t, fused, qnorm, knorm, cos_t, sin_t, out, stream=None) -> None:
         check(lib().h3_stack_attend_fused(self.handle, t, view(fused), view(qnorm), view(knorm),
                                           view(cos_t), view(sin_t), view(out), stream_ptr(stream)))
+
+    def attend_compact(self, t, compact, qnorm, knorm, cos_t, sin_t, out, stream=None) -> None:
+        check(lib().h3_stack_attend_compact(self.handle, t, view(compact), view(qnorm),
+                                            view(knorm), view(cos_t), view(sin_t), view(out),
+                                            stream_ptr(stream)))
 
     def attend(self, t, q, k, v, out, stream=None) -> None:
         check(lib().h3_stack_attend(self.handle, t, view(q), view(k), view(v), view(out),

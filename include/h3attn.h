@@ -263,6 +263,16 @@ int h3_stack_attend_fused(h3_stack *stack, uint32_t t, h3_view fused, h3_view qn
                           h3_view knorm, h3_view cos_t, h3_view sin_t, h3_view out,
                           h3_stream stream);
 
+/* Stack::prepare_fused_operands on the compact route (src/stack.rs:634-661, 1034-1040,
+ * 1561-1600) followed by attention: `compact` is the output of h3_gemm_i8_qkv_256 for the
+ * stack's token count, i.e. Q/K rows [t][2*heads*128] f16 then V^T [heads*128][capacity]. Q and
+ * K are prepared from the rows (row stride 2*inner); V^T is read in place, no transpose. Needs
+ * the fused route, capacity == ceil(tokens/256)*256 (the reference's condition for this route)
+ * and t == the stack's tokens. */
+int h3_stack_attend_compact(h3_stack *stack, uint32_t t, h3_view compact, h3_view qnorm,
+                            h3_view knorm, h3_view cos_t, h3_view sin_t, h3_view out,
+                            h3_stream stream);
+
 /* Stack::attend (src/stack.rs:1669-1839) on post-RoPE f16 q, k, v [t][heads*128]
  * (the unfused route): [colmean(K) when smoothing] -> prep_q || prep_k || transpose(V) ->
  * attention. */
