@@ -21,7 +21,8 @@ CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 OUT = HERE / "libh3attn.so"
 OBJ = HERE / "_build"
-SOURCES = ["prepare.hip", "attention.hip", "gemm.hip", "abi.cpp", "stack.cpp", "tables.cpp"]
+SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "gemm.hip", "abi.cpp", "stack.cpp",
+           "tables.cpp"]
 ARCH = "gfx950"
 
 

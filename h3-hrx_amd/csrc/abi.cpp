@@ -349,6 +349,38 @@ int h3_transpose_qkv_v_f16(const h3_transpose_cfg* cfg, uint32_t launch_rows, ui
                           reinterpret_cast<hipStream_t>(stream), true);
 }
 
+int h3_prepare_plain_i8(const h3_prepare_plain_cfg* cfg, uint32_t tokens, h3_view x,
+                        h3_view codes, h3_view scales, h3_stream stream) {
+  const char* stage = "prepare_plain_i8";
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  // kernels/prepare_i8_family.loom:202-206
+  if (!in_range(cfg->width, 256, 32768, 256))
+    return set_error(H3_ERR_CONFIG, "%s: width %u outside [256, 32768] step 256", stage,
+                     cfg->width);
+  if (!in_range(cfg->lanes, 32, 1024, 32))
+    return set_error(H3_ERR_CONFIG, "%s: lanes %u outside [32, 1024] step 32", stage, cfg->lanes);
+  if (!in_range(cfg->out_stride, 256, 65536, 64) || cfg->out_stride < cfg->width)
+    return set_error(H3_ERR_CONFIG, "%s: out_stride %u outside [width=%u, 65536] step 64", stage,
+                     cfg->out_stride, cfg->width);
+  if (cfg->elem != H3_ELEM_F16 && cfg->elem != H3_ELEM_BF16 && cfg->elem != H3_ELEM_F32)
+    return set_error(H3_ERR_CONFIG, "%s: unknown element format %u", stage, cfg->elem);
+  if (!in_range(tokens, 1, 1048576))
+    return set_error(H3_ERR_ARGUMENT, "%s: tokens %u outside [1, 1048576]", stage, tokens);
+  const size_t esize = cfg->elem == H3_ELEM_F32 ? 4 : 2;
+  h3_view views[3] = {x, codes, scales};
+  size_t need[3] = {(size_t)tokens * cfg->width * esize, (size_t)tokens * cfg->out_stride,
+                    (size_t)tokens * 4};
+  int st = check_bindings(stage, views, need, 3);
+  if (st) return st;
+  if (reinterpret_cast<uintptr_t>(x.ptr) % 16 || reinterpret_cast<uintptr_t>(codes.ptr) % 16)
+    return set_error(H3_ERR_ARGUMENT, "%s: x and codes must be 16-byte aligned", stage);
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_prepare_plain(cfg->width, cfg->out_stride, cfg->elem, tokens,
+                                              x.ptr, static_cast<uint8_t*>(codes.ptr),
+                                              static_cast<float*>(scales.ptr),
+                                              reinterpret_cast<hipStream_t>(stream)));
+}
+
 int h3_gemm_i8_qkv_256(const h3_gemm_cfg* cfg, uint32_t tokens, h3_view a, h3_view w,
                        h3_view w_scale, h3_view a_scale, h3_view out, h3_stream stream) {
   const char* stage = "gemm_i8_qkv_256";

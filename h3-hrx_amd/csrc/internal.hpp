@@ -65,6 +65,9 @@ hipError_t launch_transpose(uint32_t width, uint32_t row_capacity, uint32_t row_
 hipError_t launch_gemm_i8_qkv(uint32_t m, uint32_t n, uint32_t k, uint32_t k_stride,
                               const int8_t* a, const int8_t* w, const float* ws, const float* as,
                               uint16_t* out, hipStream_t stream);
+hipError_t launch_prepare_plain(uint32_t width, uint32_t out_stride, uint32_t elem,
+                                uint32_t tokens, const void* x, uint8_t* codes, float* scales,
+                                hipStream_t stream);
 hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out,

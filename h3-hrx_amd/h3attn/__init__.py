@@ -20,7 +20,7 @@ _HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = _HERE.parent / "libh3attn.so"
 
 H3_OK, H3_ERR_BINDING, H3_ERR_CONFIG, H3_ERR_ARGUMENT, H3_ERR_LAUNCH, H3_ERR_NO_DEVICE = range(6)
-H3_ELEM_F16, H3_ELEM_BF16 = 0, 1
+H3_ELEM_F16, H3_ELEM_BF16, H3_ELEM_F32 = 0, 1, 2
 STATUS_NAMES = {0: "ok", 1: "binding", 2: "config", 3: "argument", 4: "launch", 5: "no device"}
 
 
@@ -87,6 +87,15 @@ class GemmCfg(ctypes.Structure):
     ]
 
 
+class PreparePlainCfg(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_uint32),
+        ("lanes", ctypes.c_uint32),
+        ("out_stride", ctypes.c_uint32),
+        ("elem", ctypes.c_uint32),
+    ]
+
+
 class StackDims(ctypes.Structure):
     _fields_ = [
         ("heads", ctypes.c_uint32),
@@ -129,6 +138,8 @@ SIGNATURES = {
     "h3_attention_i8qk": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View, _S],
         ctypes.c_int),
+    "h3_prepare_plain_i8": (
+        [_P(PreparePlainCfg), ctypes.c_uint32, View, View, View, _S], ctypes.c_int),
     "h3_gemm_i8_qkv_256": (
         [_P(GemmCfg), ctypes.c_uint32, View, View, View, View, View, _S], ctypes.c_int),
     "h3_rope_dit_tables": (
@@ -277,6 +288,11 @@ def attention_i8qk(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, 
                    stream=None) -> None:
     check(lib().h3_attention_i8qk(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
                                   view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
+
+
+def prepare_plain_i8(cfg: PreparePlainCfg, tokens: int, x, codes, scales, stream=None) -> None:
+    check(lib().h3_prepare_plain_i8(ctypes.byref(cfg), tokens, view(x), view(codes), view(scales),
+                                    stream_ptr(stream)))
 
 
 def gemm_i8_qkv_256(cfg: GemmCfg, tokens: int, a, w, w_scale, a_scale, out, stream=None) -> None:

@@ -52,7 +52,7 @@ enum {
   H3_ERR_NO_DEVICE = 5 /* no usable gfx950 device */
 };
 
-enum { H3_ELEM_F16 = 0, H3_ELEM_BF16 = 1 };
+enum { H3_ELEM_F16 = 0, H3_ELEM_BF16 = 1, H3_ELEM_F32 = 2 /* h3_prepare_plain_i8 only */ };
 
 /* Message of the last failing call on this thread ("" after success). */
 const char *h3_last_error(void);
@@ -182,6 +182,33 @@ typedef struct {
  *   tokens in [1, 16777216]. */
 int h3_gemm_i8_qkv_256(const h3_gemm_cfg *cfg, uint32_t tokens, h3_view a, h3_view w,
                        h3_view w_scale, h3_view a_scale, h3_view out, h3_stream stream);
+
+/* Config of h3.prepare_plain_i8 / prepare_plain_f32_i8
+ * (kernels/prepare_i8_family.loom:202-206, 598-602; src/dispatch.rs:570-600):
+ *   width       multiple of 256 in [256, 32768]: channels per token row
+ *   lanes       multiple of 32 in [32, 1024]: the reference's launch width; accepted and
+ *               validated, the launch shape here is fixed by the kernel
+ *   out_stride  multiple of 64 in [256, 65536], >= width: bytes per code row (the GEMM's
+ *               k_stride)
+ *   elem        H3_ELEM_F16 (prepare_plain_i8), H3_ELEM_F32 (prepare_plain_f32_i8) or
+ *               H3_ELEM_BF16 (an extension) */
+typedef struct {
+  uint32_t width;
+  uint32_t lanes;
+  uint32_t out_stride;
+  uint32_t elem;
+} h3_prepare_plain_cfg;
+
+/* h3_prepare_plain_i8 (kernels/prepare_i8_family.loom:200-294, f32 input 598-689): the INT8
+ * GEMM A operand. Per token row: each 256-channel group rotated by H4 (x) H4 (x) H4 (x) H4 with
+ * H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] (radix-4 stages of strides 1, 4, 16, 64 in
+ * the reference's fp32 order), amax over the row (non-finite counts as inf),
+ * s = max(amax/16, 1e-30)/127, codes = clamp(rne(y*(1/16)/s), +-127), zero codes when s is not
+ * finite.
+ *   x [tokens][width] (elem), codes [tokens][out_stride] int8 (bytes >= width untouched),
+ *   scales [tokens] f32. x and codes 16-byte aligned. tokens in [1, 1048576]. */
+int h3_prepare_plain_i8(const h3_prepare_plain_cfg *cfg, uint32_t tokens, h3_view x,
+                        h3_view codes, h3_view scales, h3_stream stream);
 
 /* rope::dit (src/rope.rs:11-37), on the host: the DiT's cos/sin tables [rows][48] f32 for
  * h3_prepare_qk_rope_i8hm and h3_rope_qknorm_f16. For row r and axis a in 0..2, with

@@ -496,3 +496,64 @@ void h3o_gemm_i8_qkv(const int8_t *a, const int8_t *w, const float *ws, const fl
   for (int c = 0; c < n / 3; ++c)
     for (size_t r = (size_t)m; r < cap; ++r) vt[(size_t)c * cap + r] = 0;
 }
+
+/* One radix-4 stage of the group-256 rotation on digit `d` (index bits 2d, 2d+1) of a 256-group,
+ * in the reference's operation order (kernels/prepare_i8_family.loom:26-43, 93-110):
+ *   s01 = x0+x1, s23 = x2+x3, d01 = x0-x1, d23 = x2-x3;
+ *   y0 = s01+d23, y1 = s01-d23, y2 = d01+s23, y3 = s23-d01.
+ * The stages at strides 4 and 16 exchange operands between lanes (48-51, 62-71) but evaluate the
+ * same four expressions (additions commute exactly in IEEE arithmetic). */
+static void plain_radix4(float *g, int d) {
+  const int stride = 1 << (2 * d);
+  for (int base = 0; base < 256; ++base) {
+    if ((base >> (2 * d)) & 3) continue;
+    float *p0 = g + base, *p1 = p0 + stride, *p2 = p1 + stride, *p3 = p2 + stride;
+    const float x0 = *p0, x1 = *p1, x2 = *p2, x3 = *p3;
+    const float s01 = x0 + x1, s23 = x2 + x3, d01 = x0 - x1, d23 = x2 - x3;
+    *p0 = s01 + d23;
+    *p1 = s01 - d23;
+    *p2 = d01 + s23;
+    *p3 = s23 - d01;
+  }
+}
+
+void h3o_prepare_plain_i8(const void *x, int fmt, int tokens, int width, int out_stride,
+                          int8_t *codes, float *scales) {
+  float *row = (float *)malloc(sizeof(float) * (size_t)width);
+  for (int t = 0; t < tokens; ++t) {
+    for (int c = 0; c < width; ++c) {
+      float v;
+      if (fmt == 2) {
+        v = ((const float *)x)[(size_t)t * width + c] + 0.0f; /* loom:641 addf zero */
+      } else {
+        const uint16_t b = ((const uint16_t *)x)[(size_t)t * width + c];
+        v = fmt == H3O_BF16 ? h3o_bf16_to_float(b) : h3o_half_to_float(b);
+      }
+      row[c] = v * 1.0f; /* prescale 1.0 (loom:280) */
+    }
+    float amax = 0.0f;
+    for (int g = 0; g < width; g += 256) {
+      for (int d = 0; d < 4; ++d) plain_radix4(row + g, d);
+      for (int i = 0; i < 256; ++i) { /* loom:126-149: non-finite counts as inf */
+        const float a = fabsf(row[g + i]);
+        const float checked = a < INFINITY ? a : INFINITY;
+        amax = fmaxf(amax, checked);
+      }
+    }
+    /* loom:155-163 */
+    const float row_max = amax * 0.0625f;
+    const float safe = fmaxf(row_max, 1.0000000000000001e-30f);
+    const float s = safe / 127.0f;
+    const float inv_s = 0.0625f / s;
+    const int valid = s < INFINITY;
+    for (int c = 0; c < width; ++c) {
+      float q = valid ? row[c] * inv_s : 0.0f;
+      q = nearbyintf(q); /* roundeven in the default rounding mode */
+      q = fmaxf(q, -127.0f);
+      q = fminf(q, 127.0f);
+      codes[(size_t)t * out_stride + c] = (int8_t)(int)q;
+    }
+    scales[t] = s;
+  }
+  free(row);
+}

@@ -31,6 +31,19 @@
  *                           scale that saturates to 65472, zero V padding), by exact int64 dot
  *                           products, and by an independent numpy restatement (float32 ops,
  *                           astype(float16)) in tests/test_oracle_gemm.py.
+ *   h3o_prepare_plain_i8    the GEMM-operand quantizer prepare_plain_i8 / prepare_plain_f32_i8
+ *                           (kernels/prepare_i8_family.loom:4-72, 80-193, 200-294, 598-689):
+ *                           per 256-group, four radix-4 stages (strides 1, 4, 16, 64) in the
+ *                           reference's fp32 operation order, absmax with non-finite -> inf,
+ *                           s = max(amax/16, 1e-30)/127, q = clamp(rne(x*(1/16)/s)). Pinned by
+ *                           the reference test f32_preparation_matches_dense_hadamard_and_marks_
+ *                           invalid_rows (tests/kernels.rs:4587-4760: codes within 1 of the
+ *                           dense product, scale within 0.01, non-finite rows -> zero codes and
+ *                           a non-finite scale) on its inputs, by exactness against the dense
+ *                           Kronecker product on integer inputs whose sums are exact in fp32,
+ *                           and by an independent numpy restatement. The rounding order of the
+ *                           butterflies follows the .loom text; no reference vector pins it
+ *                           beyond those checks.
  *   h3o_attention_f64       the attention the operands define, tests/kernels.rs:1891-1913 and
  *                           2084-2111: softmax_j(sum(qc*kc) * qs * ks) . V in f64. Pinned by
  *                           closed forms: uniform keys give the mean of V, a single dominant key
@@ -125,6 +138,12 @@ double h3o_cpu_baseline(const uint16_t *q, const uint16_t *k, const uint16_t *v,
  * threads: OpenMP threads (<= 0: all). */
 void h3o_gemm_i8_qkv(const int8_t *a, const int8_t *w, const float *ws, const float *as, int m,
                      int n, int k, int k_stride, uint16_t *out, int threads);
+
+/* prepare_plain_i8 (fmt H3O_F16 / H3O_BF16, 16-bit x) and prepare_plain_f32_i8 (fmt 2, f32 x):
+ * x [tokens][width]; codes int8 [tokens][out_stride] (first width bytes written); scales
+ * [tokens] f32. */
+void h3o_prepare_plain_i8(const void *x, int fmt, int tokens, int width, int out_stride,
+                          int8_t *codes, float *scales);
 
 int h3o_max_threads(void);
 

@@ -75,6 +75,8 @@ def lib():
         L.h3o_cpu_baseline.restype = c_double
         L.h3o_gemm_i8_qkv.argtypes = [i8, i8, f32, f32, c_int, c_int, c_int, c_int, u16, c_int]
         L.h3o_gemm_i8_qkv.restype = None
+        L.h3o_prepare_plain_i8.argtypes = [ctypes.c_void_p, c_int, c_int, c_int, c_int, i8, f32]
+        L.h3o_prepare_plain_i8.restype = None
         L.h3o_max_threads.argtypes = []
         L.h3o_max_threads.restype = c_int
         _lib = L
@@ -234,3 +236,18 @@ def gemm_i8_qkv(a: np.ndarray, w: np.ndarray, ws: np.ndarray, as_: np.ndarray, k
     lib().h3o_gemm_i8_qkv(a.reshape(-1), w.reshape(-1), np.ascontiguousarray(ws, np.float32),
                           np.ascontiguousarray(as_, np.float32), m, n, k, k_stride, out, threads)
     return out
+
+
+F32 = 2
+
+
+def prepare_plain_i8(x: np.ndarray, fmt: int, out_stride: int):
+    """prepare_plain_i8 (fmt F16/BF16: x holds 16-bit patterns) or prepare_plain_f32_i8 (fmt F32:
+    x float32), x [tokens][width]. Returns (codes int8 [tokens][out_stride], scales f32)."""
+    x = np.ascontiguousarray(x, np.float32 if fmt == F32 else np.uint16)
+    tokens, width = x.shape
+    codes = np.zeros((tokens, out_stride), np.int8)
+    scales = np.zeros(tokens, np.float32)
+    lib().h3o_prepare_plain_i8(x.ctypes.data, fmt, tokens, width, out_stride, codes.reshape(-1),
+                               scales)
+    return codes, scales

@@ -192,3 +192,28 @@ def test_gemm_rejects_misaligned_output_and_bad_token_counts():
     views = [fake(1 << 40)] * 4 + [H.raw_view(0x1004, 1 << 40)]
     assert lib.h3_gemm_i8_qkv_256(ctypes.byref(cfg), 16, *views, None) == H.H3_ERR_ARGUMENT
     assert call_gemm(cfg, 0, [1 << 40] * 5) == H.H3_ERR_ARGUMENT
+
+
+def call_plain(cfg, tokens, sizes, x_ptr=0x1000):
+    views = [H.raw_view(x_ptr, sizes[0])] + [fake(n) for n in sizes[1:]]
+    return H.lib().h3_prepare_plain_i8(ctypes.byref(cfg), tokens, *views, None)
+
+
+def test_prepare_plain_bindings_and_configs():
+    t = 7
+    cfg = H.PreparePlainCfg(4096, 448, 4160, H.H3_ELEM_F16)
+    need = [t * 4096 * 2, t * 4160, t * 4]
+    for i in range(3):
+        sizes = list(need)
+        sizes[i] -= 1
+        assert call_plain(cfg, t, sizes) == H.H3_ERR_BINDING and f"binding {i}" in H.last_error()
+    f32 = H.PreparePlainCfg(4096, 448, 4160, H.H3_ELEM_F32)
+    sizes = [t * 4096 * 4 - 1, t * 4160, t * 4]
+    assert call_plain(f32, t, sizes) == H.H3_ERR_BINDING
+    for field, value in [("width", 100), ("width", 33024), ("lanes", 16), ("lanes", 48),
+                         ("out_stride", 4032), ("out_stride", 4100), ("elem", 3)]:
+        bad = H.PreparePlainCfg(4096, 448, 4160, H.H3_ELEM_F16)
+        setattr(bad, field, value)
+        assert call_plain(bad, t, [1 << 40] * 3) == H.H3_ERR_CONFIG, (field, value)
+    assert call_plain(cfg, t, [1 << 40] * 3, x_ptr=0x1008) == H.H3_ERR_ARGUMENT
+    assert call_plain(cfg, 0, [1 << 40] * 3) == H.H3_ERR_ARGUMENT
