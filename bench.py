@@ -39,15 +39,67 @@ WORKLOADS = {
 
 
 def rope_tables(torch, dev, tokens, grid):
-    """3D RoPE cos/sin [tokens][48]: axes (t, h, w) x 16 frequencies, angle = f32(pos) *
-    inv_freq[j] (src/rope.rs:11-37, src/layout.rs:64-72), with a synthetic inv_freq
-    10000^(-j/16) since the checkpoint's table is not available."""
+    """3D RoPE cos/sin [tokens][48] from the library's host producer of the reference's DiT
+    tables (h3_rope_dit_tables = rope::dit, src/rope.rs:11-37): positions (t, h, w) of the
+    latent grid in row order, with a synthetic inv_freq 10000^(-j/16) since the checkpoint's
+    table is not available."""
+    import numpy as np
+
+    import h3attn as H
+
     t_n, h_n, w_n = grid
-    i = torch.arange(tokens, device=dev, dtype=torch.int64)
-    pos = torch.stack([i // (h_n * w_n), (i // w_n) % h_n, i % w_n], dim=1).to(torch.float32)
-    inv = torch.pow(torch.tensor(10000.0, device=dev), -torch.arange(16, device=dev) / 16.0)
-    ang = (pos[:, :, None] * inv[None, None, :].to(torch.float32)).reshape(tokens, 48)
-    return torch.cos(ang).contiguous(), torch.sin(ang).contiguous()
+    i = np.arange(tokens, dtype=np.int64)
+    pos = np.stack([i // (h_n * w_n), (i // w_n) % h_n, i % w_n], axis=1).astype(np.float64)
+    inv = np.array([np.float32(10000.0) ** (-np.float32(j) / np.float32(16.0)) for j in range(16)],
+                   np.float32)
+    cos, sin = H.rope_dit_tables(pos, inv)
+    return torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+
+
+def time_launches(torch, fn, reps):
+    """Average milliseconds of `fn` over `reps` launches, with HIP events on torch's current
+    stream (the stream the library enqueues on)."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def adjacent_kernels(torch, H, dev, tokens, width, out):
+    """The kernels either side of the path at the same shape, timed on their own (they are not
+    part of the step): the compact INT8 QKV projection that produces Q/K rows and V^T
+    (h3_gemm_i8_qkv_256, hidden 4096 -> 3*width, synthetic int8 operands) and the INT8
+    preparation of the attention output for the out-projection (h3_prepare_plain_i8)."""
+    res = {}
+    k, n = 4096, 3 * width
+    g = torch.Generator(device=dev).manual_seed(7)
+    a = torch.randint(-128, 128, (tokens, k), dtype=torch.int8, device=dev, generator=g)
+    w = torch.randint(-128, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+    ws = torch.rand(n, device=dev, generator=g) * 1e-4
+    as_ = torch.rand(tokens, device=dev, generator=g) * 1e-2
+    compact = torch.empty(H.compact_qkv_elements(tokens, n), dtype=torch.int16, device=dev)
+    gcfg = H.GemmCfg(k, n, k, 1)
+    ms = time_launches(torch, lambda: H.gemm_i8_qkv_256(gcfg, tokens, a, w, ws, as_, compact), 5)
+    tops = 2.0 * tokens * n * k / (ms * 1e-3) / 1e12
+    res["gemm_i8_qkv_256"] = {"shape": f"M={tokens} K={k} N={n}", "ms": round(ms, 4),
+                              "tops": round(tops, 1),
+                              "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4)}
+    del a, w, compact
+    codes = torch.empty((tokens, width), dtype=torch.int8, device=dev)
+    scales = torch.empty(tokens, dtype=torch.float32, device=dev)
+    pcfg = H.PreparePlainCfg(width, 448, width, H.H3_ELEM_F16)
+    ms = time_launches(torch, lambda: H.prepare_plain_i8(pcfg, tokens, out, codes, scales), 20)
+    nbytes = tokens * (width * 2 + width + 4)
+    res["prepare_plain_i8"] = {"shape": f"tokens={tokens} width={width} f16",
+                               "us": round(ms * 1e3, 1),
+                               "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                               "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 8e12, 4)}
+    return res
 
 
 def traffic_from_profiles(workload: str):
@@ -127,6 +179,8 @@ def main() -> None:
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-rows", type=int, default=32, help="query rows per head for the CPU leg")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-adjacent", action="store_true",
+                    help="skip timing the QKV projection and the output quantizer")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (the HBM-counter calibration)")
     args = ap.parse_args()
@@ -244,6 +298,9 @@ def main() -> None:
             "traffic": traffic_from_profiles(args.workload),
         },
     }
+    if not args.no_adjacent:
+        print("# adjacent kernels...", file=sys.stderr, flush=True)
+        line["adjacent_kernels"] = adjacent_kernels(torch, H, dev, tokens, width, out)
     if not args.no_cpu:
         print("# cpu baseline...", file=sys.stderr, flush=True)
         q16 = fused_bf16[:, :width].to(torch.float16).cpu().numpy().view(np.uint16)
