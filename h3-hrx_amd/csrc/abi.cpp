@@ -122,9 +122,14 @@ int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
   return check_bindings(stage, views, need, 4);
 }
 
+// Operand layouts of the attention kernels (attention.hip's modes).
+enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2 };
+
 int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
                      uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
-                     h3_view out, hipStream_t stream, bool head_major) {
+                     h3_view out, hipStream_t stream, int mode) {
+  const bool head_major = mode == kModeHeadI8;
+  const size_t code_div = mode == kModeTokenI4 ? 2 : 1;  // int4: half a byte per channel
   if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
   // kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17
   if (!in_range(cfg->q_stride, 128, 32768, 128))
@@ -164,9 +169,9 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
     need[2] = kv_head_limit * cap * 128;
     need[3] = kv_head_limit * cap * 4;
   } else {
-    need[0] = cap * cfg->q_stride;
+    need[0] = cap * cfg->q_stride / code_div;
     need[1] = cap * head_limit * 4;
-    need[2] = cap * cfg->kv_stride;
+    need[2] = cap * cfg->kv_stride / code_div;
     need[3] = cap * kv_head_limit * 4;
   }
   need[4] = (size_t)cfg->kv_stride * cap * 2;
@@ -175,7 +180,7 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   int st = check_bindings(stage, views, need, 6);
   if (st) return st;
   if ((st = device_ready(stage))) return st;
-  return launched(stage, launch_attention(*cfg, head_major, token_count, heads,
+  return launched(stage, launch_attention(*cfg, mode, token_count, heads,
                                           static_cast<const int32_t*>(qi.ptr),
                                           static_cast<const float*>(qs.ptr),
                                           static_cast<const int32_t*>(ki.ptr),
@@ -233,6 +238,25 @@ int h3_prepare_qk_i8hm(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x, h3
                        h3_view codes, h3_view scales, h3_stream stream) {
   return prepare_common("prepare_qk_i8hm", cfg, tokens, x, mean, codes, scales,
                         reinterpret_cast<hipStream_t>(stream), true);
+}
+
+int h3_prepare_qk_i4(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x, h3_view mean,
+                     h3_view codes, h3_view scales, h3_stream stream) {
+  const char* stage = "prepare_qk_i4";
+  // kernels/prepare_qk_i4.loom:11-17 (token-major; token_capacity is not read)
+  int st = check_prepare_cfg(stage, cfg, tokens, false);
+  if (st) return st;
+  const size_t rows_out = (size_t)tokens * cfg->heads;
+  h3_view views[4] = {x, mean, codes, scales};
+  size_t need[4] = {(size_t)tokens * cfg->row_stride * 2, mean.ptr ? (size_t)cfg->row_stride * 4 : 0,
+                    rows_out * 64, rows_out * 4};
+  if ((st = check_bindings(stage, views, need, 4))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_prepare_qk_i4(*cfg, tokens, x.ptr,
+                                              static_cast<const float*>(mean.ptr),
+                                              static_cast<int32_t*>(codes.ptr),
+                                              static_cast<float*>(scales.ptr),
+                                              reinterpret_cast<hipStream_t>(stream)));
 }
 
 int h3_prepare_qk_rope_i8hm(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x,
@@ -422,14 +446,21 @@ int h3_attention_i8qkhm(const h3_attention_cfg* cfg, uint32_t token_count, uint3
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_stream stream) {
   return attention_common("attention_i8qkhm", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
-                          reinterpret_cast<hipStream_t>(stream), true);
+                          reinterpret_cast<hipStream_t>(stream), kModeHeadI8);
 }
 
 int h3_attention_i8qk(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                       h3_stream stream) {
   return attention_common("attention_i8qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
-                          reinterpret_cast<hipStream_t>(stream), false);
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI8);
+}
+
+int h3_attention_i4qk(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                      h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                      h3_stream stream) {
+  return attention_common("attention_i4qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI4);
 }
 
 }  // extern "C"

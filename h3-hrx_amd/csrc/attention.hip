@@ -67,7 +67,17 @@ constexpr int kVStage = 128 * kRowBytes;                    // 16384
 constexpr int kKLoads = 8 / kWaves;                         // 1 KiB LDS-DMA loads per wave
 constexpr int kVLoads = 16 / kWaves;
 constexpr int kSRows = kKeys / kWaves;                      // scale rows stored per wave
-constexpr int kLoadsPerStep = kKLoads + kVLoads + 1;        // + the scale load
+// Operand layouts: int8 codes token-major (attention_i8qk_*) or head-major (attention_i8qkhm_*),
+// and int4 codes token-major (attention_i4qk_*, eight codes per word, low nibble first).
+enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2 };
+constexpr int kI4RowBytes = 64;                             // int4 K tile rows in LDS
+constexpr int kKRowsOf(int mode) { return mode == kTokenI4 ? kKeys * kI4RowBytes : kKRows; }
+constexpr int kKLoadsOf(int mode) { return mode == kTokenI4 ? 4 / kWaves : kKLoads; }
+// s_waitcnt fields (gfx9 layout): vmcnt <= the loads one step issues (K tile, V^T tile, the
+// scale load), lgkmcnt 0, expcnt untouched; or vmcnt 0.
+constexpr int kWaitPrevStepOf(int mode) {
+  return (kKLoadsOf(mode) + kVLoads + 1) | (7 << 4) | (0 << 8);
+}
 #ifndef H3_ATTN_PF
 #define H3_ATTN_PF 2
 #endif
@@ -78,8 +88,6 @@ constexpr int kMagicBits = 0x4B400000;  // float 12582912 = 1.5 * 2^23
 constexpr float kMagic = 12582912.0f;
 constexpr float kRescaleSlack = 8.0f;   // raise the running max only past 2^8 growth
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
-// s_waitcnt: vmcnt <= kLoadsPerStep, lgkmcnt 0, expcnt untouched (gfx9 field layout)
-constexpr int kWaitPrevStep = kLoadsPerStep | (7 << 4) | (0 << 8);
 constexpr int kWaitAll = 0 | (7 << 4) | (0 << 8);
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -94,8 +102,8 @@ struct Args {
   uint32_t tokens;
   uint32_t token_count;
   uint32_t capacity;
-  uint32_t q_words;   // q_stride / 4 (token-major row pitch of qi, in words)
-  uint32_t kv_bytes;  // kv_stride (token-major row pitch of ki, in bytes)
+  uint32_t q_row;     // token-major row pitch of qi in bytes (q_stride, or q_stride/2 for int4)
+  uint32_t kv_bytes;  // token-major row pitch of ki in bytes (kv_stride, or kv_stride/2)
   uint32_t out_stride;
   uint32_t q_blocks;  // ceil(token_count / 128)
   uint32_t heads;     // workload heads (grid y of the reference)
@@ -123,17 +131,29 @@ struct Stager {
   int wave;
 };
 
-// LDS byte o of a K/V^T stage holds row o/128, logical chunk ((o/16)%8) ^ ((row/2)%8).
-template <bool kHeadMajor>
+// LDS byte o of a K/V^T stage holds row o/128, logical chunk ((o/16)%8) ^ ((row/2)%8). An int4
+// K stage has 64-byte rows: byte o holds row o/64, logical chunk ((o/16)%4) ^ ((row/4)%4), so the
+// sixteen rows a quarter-wave reads with one 16-byte load each fall on distinct banks.
+template <int kMode>
 __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane) {
+  constexpr bool kHeadMajor = kMode == kHeadI8;
   Stager s;
   s.wave = wave;
+  if constexpr (kMode == kTokenI4) {
 #pragma unroll
-  for (int t = 0; t < kKLoads; ++t) {
-    const uint32_t o = (wave * kKLoads + t) * 1024 + 16 * lane;
-    const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
-    const uint32_t key = swap23(row);
-    s.koff[t] = (kHeadMajor ? key * 128 : key * a.kv_bytes) + 16 * chunk;
+    for (int t = 0; t < kKLoadsOf(kMode); ++t) {
+      const uint32_t o = (wave * kKLoadsOf(kMode) + t) * 1024 + 16 * lane;
+      const uint32_t row = o >> 6, chunk = ((o >> 4) & 3) ^ ((row >> 2) & 3);
+      s.koff[t] = swap23(row) * a.kv_bytes + 16 * chunk;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < kKLoads; ++t) {
+      const uint32_t o = (wave * kKLoads + t) * 1024 + 16 * lane;
+      const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
+      const uint32_t key = swap23(row);
+      s.koff[t] = (kHeadMajor ? key * 128 : key * a.kv_bytes) + 16 * chunk;
+    }
   }
 #pragma unroll
   for (int t = 0; t < kVLoads; ++t) {
@@ -149,9 +169,11 @@ __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane)
 
 // LDS-DMA of K tile k0 (rows past the sequence load as zero) into stage `kst`, and the load of
 // its scales into a register.
-template <bool kHeadMajor>
+template <int kMode>
 __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32_t kv_head,
                                          uint32_t k0, char* kst) {
+  constexpr bool kHeadMajor = kMode == kHeadI8;
+  constexpr uint32_t kCodeBytes = kMode == kTokenI4 ? 64 : 128;  // code bytes per (key, head)
   const uint32_t live = a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
   const char* base;
   uint32_t bytes;
@@ -163,16 +185,16 @@ __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32
     sbase = a.ks + (size_t)kv_head * a.capacity + k0;
     sbytes = live * 4;
   } else {
-    base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * 128;
-    bytes = live ? (live - 1) * a.kv_bytes + 128 : 0;
+    base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * kCodeBytes;
+    bytes = live ? (live - 1) * a.kv_bytes + kCodeBytes : 0;
     sbase = a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
     sbytes = live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0;
   }
   const __amdgpu_buffer_rsrc_t rk = rsrc(base, bytes);
 #pragma unroll
-  for (int t = 0; t < kKLoads; ++t)
+  for (int t = 0; t < kKLoadsOf(kMode); ++t)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rk, (lds_void*)(kst + (sg.wave * kKLoads + t) * 1024), 16, sg.koff[t], 0, 0, 0);
+        rk, (lds_void*)(kst + (sg.wave * kKLoadsOf(kMode) + t) * 1024), 16, sg.koff[t], 0, 0, 0);
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(sbase, sbytes),
                                                                          sg.soff, 0, 0));
 }
@@ -192,9 +214,10 @@ __device__ __forceinline__ void stage_v(const Args& a, const Stager& sg, uint32_
 }
 
 // Scales of a staged K tile: ks and -1.5*2^23*ks at its MFMA-row index.
+template <int kMode>
 __device__ __forceinline__ void store_scales(char* kst, const Stager& sg, float ks) {
   if ((threadIdx.x & 63) < kSRows) {
-    float* sc = reinterpret_cast<float*>(kst + kKRows);
+    float* sc = reinterpret_cast<float*>(kst + kKRowsOf(kMode));
     sc[sg.srow] = ks;
     sc[kKeys + sg.srow] = -(kMagic * ks);
   }
@@ -289,8 +312,28 @@ __device__ __forceinline__ uint32_t chunk_off(int x, int half, uint32_t sw) {
   return 16 * ((2 * x + half) ^ sw);
 }
 
+// int4 operands: eight 4-bit codes of a word become int8 lanes holding 16x the code,
+// ((w << 4) & 0xF0F0F0F0) for the low nibbles and (w & 0xF0F0F0F0) for the high ones, so the
+// int8 MFMA computes 256x the int4 dot product exactly (|256 S| < 2^21). The same byte order is
+// used for Q and K, so the permutation of dimensions it implies cancels in the dot product.
+// The 16 bytes at int4 row offset 16(2p + half) hold the operands of MFMA chunks 2p and 2p + 1.
+__device__ __forceinline__ v4i widen_i4(uint32_t x0, uint32_t x1) {
+  const v4i r = {(int)((x0 << 4) & 0xF0F0F0F0u), (int)(x0 & 0xF0F0F0F0u),
+                 (int)((x1 << 4) & 0xF0F0F0F0u), (int)(x1 & 0xF0F0F0F0u)};
+  return r;
+}
+// K operands of MFMA chunks (bb, 2p) and (bb, 2p + 1) from an int4 stage (64-byte rows, chunks
+// swizzled by (row/4)%4; row 32bb + n, with (n/4)%4 = g).
+__device__ __forceinline__ void k_pair_i4(const char* kst, int n, int half, uint32_t g, int bb,
+                                          int p, v4i& even, v4i& odd) {
+  const uint4 w = *reinterpret_cast<const uint4*>(kst + (32 * bb + n) * kI4RowBytes +
+                                                  16 * ((2 * p + half) ^ g));
+  even = widen_i4(w.x, w.y);
+  odd = widen_i4(w.z, w.w);
+}
+
 // The first tile's QK and dequant (no softmax work to overlap yet).
-template <bool kMasked>
+template <int kMode, bool kMasked>
 __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4], float qsl,
                                            State& st, float (&u)[2][16], int n, int half,
                                            uint32_t tokens) {
@@ -299,13 +342,26 @@ __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4],
                       kMagicBits, kMagicBits, kMagicBits, kMagicBits};
   const uint32_t sw = (n >> 1) & 7;
   const char* krow = kst + n * kRowBytes;
-  const float* kss = reinterpret_cast<const float*>(kst + kKRows);
+  const float* kss = reinterpret_cast<const float*>(kst + kKRowsOf(kMode));
   v16i s[2];
+  if constexpr (kMode == kTokenI4) {
+    v4i kop[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const int bb = c & 1, dc = c >> 1;
-    const v4i kop = *reinterpret_cast<const v4i*>(krow + bb * 32 * kRowBytes + chunk_off(dc, half, sw));
-    s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
+    for (int q = 0; q < 4; ++q)
+      k_pair_i4(kst, n, half, (n >> 2) & 3, q & 1, q >> 1, kop[4 * (q >> 1) + (q & 1)],
+                kop[4 * (q >> 1) + 2 + (q & 1)]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int bb = c & 1, dc = c >> 1;
+      s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int bb = c & 1, dc = c >> 1;
+      const v4i kop = *reinterpret_cast<const v4i*>(krow + bb * 32 * kRowBytes + chunk_off(dc, half, sw));
+      s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
+    }
   }
   float tmax = -INFINITY;
 #pragma unroll
@@ -323,7 +379,7 @@ __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4],
 //   kst    LDS stage of K(j+1) (unused when !kNext), vst  LDS stage of V(j)
 //   u      in: tile j's dequantized scores; out: tile j+1's
 //   knext0 first key of tile j+1
-template <bool kNext, bool kMaskNext, bool kMaskCur>
+template <int kMode, bool kNext, bool kMaskNext, bool kMaskCur>
 __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i (&qop)[4],
                                      float qsl, State& st, float (&u)[2][16], int n, int half,
                                      uint32_t knext0, uint32_t tokens) {
@@ -342,7 +398,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   const uint32_t sw = (n >> 1) & 7;
   const char* krow = kst + n * kRowBytes;  // + 32*bb rows + chunk_off(dc)
   const char* vrow = vst + n * kRowBytes;  // + 32*db rows + chunk_off(g)
-  const float* kss = reinterpret_cast<const float*>(kst + kKRows);
+  const float* kss = reinterpret_cast<const float*>(kst + kKRowsOf(kMode));
   v16i s[2];
   v8h pb[4];
   v4i kop[8];
@@ -351,15 +407,26 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   float la = 0.0f, lb = 0.0f;
 
   // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
+  constexpr bool kI4 = kMode == kTokenI4;
   if (kNext) {
+    if constexpr (kI4) {  // chunks 0..3 now, 4..7 two MFMAs ahead of their use
+      k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 0, kop[0], kop[2]);
+      k_pair_i4(kst, n, half, (n >> 2) & 3, 1, 0, kop[1], kop[3]);
+    } else {
 #pragma unroll
-    for (int w = 0; w < kPf; ++w)
-      kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
+      for (int w = 0; w < kPf; ++w)
+        kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
+    }
   }
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int bb = c & 1, dc = c >> 1;
-    if (kNext && c + kPf < 8) {
+    if constexpr (kI4) {
+      if (kNext && c == 2) {
+        k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 1, kop[4], kop[6]);
+        k_pair_i4(kst, n, half, (n >> 2) & 3, 1, 1, kop[5], kop[7]);
+      }
+    } else if (kNext && c + kPf < 8) {
       const int w = c + kPf;
       kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
     }
@@ -404,9 +471,11 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   if (!kNext) st.l += la + lb;
 }
 
-template <bool kHeadMajor>
+template <int kMode>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention(Args a) {
+  constexpr bool kHeadMajor = kMode == kHeadI8;
+  constexpr int kWaitPrevStep = kWaitPrevStepOf(kMode);
   // Three K stages and three V^T stages, each its own array so that the compiler can tell an
   // LDS-DMA into one stage from the reads of another.
   __shared__ __attribute__((aligned(16))) char k0s[kKStage];
@@ -437,28 +506,37 @@ void k_attention(Args a) {
   const uint32_t q = q_tile_c * kQueriesPerWave + n;
   const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
 
-  const Stager sg = make_stager<kHeadMajor>(a, wave, lane);
+  const Stager sg = make_stager<kMode>(a, wave, lane);
   const uint32_t n_tiles = (a.tokens + kKeys - 1) / kKeys;
   const uint32_t full = a.tokens / kKeys;  // tiles with no key past the sequence
 
   // ---- prologue: K(0..2) and V(0..1) in flight, scales of K(0), K(1) stored, K(2)'s held
-  float ks0 = stage_k<kHeadMajor>(a, sg, kv_head, 0, k0s);
-  float ks1 = stage_k<kHeadMajor>(a, sg, kv_head, kKeys, k1s);
-  float ks_held = stage_k<kHeadMajor>(a, sg, kv_head, 2 * kKeys, k2s);
+  float ks0 = stage_k<kMode>(a, sg, kv_head, 0, k0s);
+  float ks1 = stage_k<kMode>(a, sg, kv_head, kKeys, k1s);
+  float ks_held = stage_k<kMode>(a, sg, kv_head, 2 * kKeys, k2s);
   stage_v(a, sg, kv_head, 0, v0s);
   stage_v(a, sg, kv_head, kKeys, v1s);
 
   // Q^T operand, held for the whole key loop: 4 chunks of 32 channels, 16 bytes per lane.
   v4i qop[4];
-  {
+  if constexpr (kMode == kTokenI4) {  // 64 code bytes per (token, head), widened like K
+    const char* src = reinterpret_cast<const char*>(a.qi) + (size_t)q_read * a.q_row + head * 64;
+    const uint4 w0 = *reinterpret_cast<const uint4*>(src + 16 * half);
+    const uint4 w1 = *reinterpret_cast<const uint4*>(src + 16 * (2 + half));
+    qop[0] = widen_i4(w0.x, w0.y);
+    qop[1] = widen_i4(w0.z, w0.w);
+    qop[2] = widen_i4(w1.x, w1.y);
+    qop[3] = widen_i4(w1.z, w1.w);
+  } else {
     const int32_t* src = kHeadMajor ? a.qi + ((size_t)head * a.capacity + q_read) * 32
-                                    : a.qi + (size_t)q_read * a.q_words + head * 32;
+                                    : a.qi + (size_t)q_read * (a.q_row / 4) + head * 32;
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) qop[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
   }
   const float qsv = kHeadMajor ? a.qs[(size_t)head * a.capacity + q_read]
                                : a.qs[(size_t)q_read * a.head_limit + head];
-  const float qsl = qsv * kLog2e;
+  // log2 units; int4 scores arrive 256x (the widened codes are 16x each)
+  const float qsl = kMode == kTokenI4 ? qsv * kLog2e * (1.0f / 256.0f) : qsv * kLog2e;
 
   State st;
 #pragma unroll
@@ -469,14 +547,14 @@ void k_attention(Args a) {
   st.l = 0.0f;
   st.alpha = 1.0f;
 
-  store_scales(k0s, sg, ks0);
-  store_scales(k1s, sg, ks1);
+  store_scales<kMode>(k0s, sg, ks0);
+  store_scales<kMode>(k1s, sg, ks1);
   step_barrier<kWaitAll>();
   float u[2][16];
   if (full == 0)
-    first_tile<true>(k0s, qop, qsl, st, u, n, half, a.tokens);
+    first_tile<kMode, true>(k0s, qop, qsl, st, u, n, half, a.tokens);
   else
-    first_tile<false>(k0s, qop, qsl, st, u, n, half, a.tokens);
+    first_tile<kMode, false>(k0s, qop, qsl, st, u, n, half, a.tokens);
   step_barrier<kWaitAll>();  // K(0)'s stage is refilled by step 0
 
   // One steady step j (tile j+1 full) on compile-time stages: reads K(j+1) from kn, V(j) from
@@ -484,10 +562,11 @@ void k_attention(Args a) {
   // scales of K(j+2) (stage kn2) loaded one step earlier.
 #define H3_STEADY(kc, kn, kn2, vc, vn2)                                                       \
   {                                                                                          \
-    const float ks_new = stage_k<kHeadMajor>(a, sg, kv_head, (j + 3) * kKeys, kc);           \
+    const float ks_new = stage_k<kMode>(a, sg, kv_head, (j + 3) * kKeys, kc);                \
     stage_v(a, sg, kv_head, (j + 2) * kKeys, vn2);                                           \
-    step<true, false, false>(kn, vc, qop, qsl, st, u, n, half, (j + 1) * kKeys, a.tokens);   \
-    store_scales(kn2, sg, ks_held);                                                          \
+    step<kMode, true, false, false>(kn, vc, qop, qsl, st, u, n, half, (j + 1) * kKeys,       \
+                                    a.tokens);                                               \
+    store_scales<kMode>(kn2, sg, ks_held);                                                   \
     ks_held = ks_new;                                                                        \
     step_barrier<kWaitPrevStep>();                                                           \
     ++j;                                                                                     \
@@ -509,15 +588,15 @@ void k_attention(Args a) {
   auto kst = [&](uint32_t t) { const uint32_t r = t % 3; return r == 0 ? k0s : r == 1 ? k1s : k2s; };
   auto vst = [&](uint32_t t) { const uint32_t r = t % 3; return r == 0 ? v0s : r == 1 ? v1s : v2s; };
   if (n_tiles > full && full > 0) {  // j == full - 1: tile j+1 is the partial tile
-    step<true, true, false>(kst(j + 1), vst(j), qop, qsl, st, u, n, half, (j + 1) * kKeys,
-                            a.tokens);
+    step<kMode, true, true, false>(kst(j + 1), vst(j), qop, qsl, st, u, n, half, (j + 1) * kKeys,
+                                   a.tokens);
     step_barrier<kWaitAll>();
     ++j;
   }
   if (n_tiles > full)
-    step<false, false, true>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
+    step<kMode, false, false, true>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
   else
-    step<false, false, false>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
+    step<kMode, false, false, false>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
   // The last step raises no max, so no rescale is owed after its PV.
   step_barrier<kWaitAll>();  // no staging load outlives the workgroup
 
@@ -540,7 +619,7 @@ void k_attention(Args a) {
 
 }  // namespace
 
-hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_t token_count,
+hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out,
                             hipStream_t stream) {
@@ -554,8 +633,8 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_
   a.tokens = cfg.tokens;
   a.token_count = token_count;
   a.capacity = cfg.token_capacity;
-  a.q_words = cfg.q_stride / 4;
-  a.kv_bytes = cfg.kv_stride;
+  a.q_row = mode == kTokenI4 ? cfg.q_stride / 2 : cfg.q_stride;
+  a.kv_bytes = mode == kTokenI4 ? cfg.kv_stride / 2 : cfg.kv_stride;
   a.out_stride = cfg.out_stride;
   a.q_blocks = (token_count + kQueriesPerBlock - 1) / kQueriesPerBlock;
   a.heads = heads;
@@ -564,10 +643,12 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_
   a.total = a.q_blocks * heads;
   a.per_xcd = (a.total + 7) / 8;
   dim3 grid(a.per_xcd * 8);
-  if (head_major)
-    hipLaunchKernelGGL(k_attention<true>, grid, dim3(kThreads), 0, stream, a);
+  if (mode == kHeadI8)
+    hipLaunchKernelGGL(k_attention<kHeadI8>, grid, dim3(kThreads), 0, stream, a);
+  else if (mode == kTokenI4)
+    hipLaunchKernelGGL(k_attention<kTokenI4>, grid, dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(k_attention<false>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -43,6 +43,9 @@ int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2,
 hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int head_major,
                              const void* x, const float* mean, int32_t* codes, float* scales,
                              hipStream_t stream);
+hipError_t launch_prepare_qk_i4(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                                const float* mean, int32_t* codes, float* scales,
+                                hipStream_t stream);
 hipError_t launch_prepare_qk_rope(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
                                   const float* weight, const float* cos_t, const float* sin_t,
                                   int32_t* codes, float* scales, hipStream_t stream);
@@ -68,7 +71,8 @@ hipError_t launch_gemm_i8_qkv(uint32_t m, uint32_t n, uint32_t k, uint32_t k_str
 hipError_t launch_prepare_plain(uint32_t width, uint32_t out_stride, uint32_t elem,
                                 uint32_t tokens, const void* x, uint8_t* codes, float* scales,
                                 hipStream_t stream);
-hipError_t launch_attention(const h3_attention_cfg& cfg, int head_major, uint32_t token_count,
+// mode: 0 int8 token-major, 1 int8 head-major, 2 int4 token-major
+hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out,
                             hipStream_t stream);

@@ -107,6 +107,25 @@ __device__ __forceinline__ uint32_t quantize_row(v4f r, float extra, float* scal
   return word;
 }
 
+// The int4 form (kernels/prepare_qk_i4.loom:174-214): amax/7 scales, codes clamp(rne(r*7/amax),
+// +-7) as nibbles; returns this lane's four codes in the low 16 bits (low nibble first).
+__device__ __forceinline__ uint32_t quantize_row_i4(v4f r, float extra, float* scale) {
+  float m = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
+  m = half_max(m);
+  float amax = fmaxf(m, 1.0000000000000001e-30f);
+  float sc = amax / 7.0f;
+  float inv = 7.0f / amax;
+  uint32_t bits = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float q = __builtin_rintf(r[j] * inv);
+    q = fminf(fmaxf(q, -7.0f), 7.0f);
+    bits |= ((uint32_t)(int)q & 0xfu) << (4 * j);
+  }
+  *scale = sc * extra;
+  return bits;
+}
+
 __device__ __forceinline__ uint2 load4(const void* base, size_t elem_index) {
   return *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + elem_index);
 }
@@ -202,6 +221,36 @@ __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
   size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
   codes[out_row * 32 + lane] = (int32_t)word;
   if (lane == 0) scales[out_row] = scale;
+}
+
+// int4 operands, token-major (kernels/prepare_qk_i4.loom): the same rotation, 16 bits of codes
+// per lane; the even lane of each pair writes the word of both (codes [tokens][heads*16] i32).
+__global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ x,
+                                                       const float* __restrict__ mean,
+                                                       int32_t* __restrict__ codes,
+                                                       float* __restrict__ scales,
+                                                       uint32_t tokens, uint32_t row_stride,
+                                                       uint32_t head_offset, uint32_t heads,
+                                                       float extra, uint32_t elem) {
+  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  if (row >= tokens * heads) return;
+  const uint32_t t = row / heads, h = row % heads;
+  const uint32_t col = head_offset + 128u * h + 4u * lane;
+  v4f y = widen4(load4(x, (size_t)t * row_stride + col), elem);
+  if (mean) {
+    const float4 m = *reinterpret_cast<const float4*>(mean + col);
+    y[0] = y[0] - m.x;
+    y[1] = y[1] - m.y;
+    y[2] = y[2] - m.z;
+    y[3] = y[3] - m.w;
+  }
+  v4f r = hadamard128(y, lane);
+  float scale;
+  const uint32_t bits = quantize_row_i4(r, extra, &scale);
+  const uint32_t odd = (uint32_t)__builtin_amdgcn_mov_dpp((int)bits, 0xB1, 0xF, 0xF, true);
+  if ((lane & 1) == 0) codes[(size_t)row * 16 + lane / 2] = (int32_t)(bits | (odd << 16));
+  if (lane == 0) scales[row] = scale;
 }
 
 // RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
@@ -417,6 +466,16 @@ hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int hea
     hipLaunchKernelGGL(k_prepare_qk<false>, grid, dim3(256), 0, stream, x, mean, codes, scales,
                        tokens, cfg.row_stride, cfg.head_offset, cfg.heads, 0u, cfg.extra_scale,
                        cfg.elem);
+  return hipGetLastError();
+}
+
+hipError_t launch_prepare_qk_i4(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
+                                const float* mean, int32_t* codes, float* scales,
+                                hipStream_t stream) {
+  const uint32_t rows = tokens * cfg.heads;
+  hipLaunchKernelGGL(k_prepare_qk_i4, dim3((rows + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256),
+                     0, stream, x, mean, codes, scales, tokens, cfg.row_stride, cfg.head_offset,
+                     cfg.heads, cfg.extra_scale, cfg.elem);
   return hipGetLastError();
 }
 

@@ -122,6 +122,7 @@ SIGNATURES = {
     "h3_version": ([], ctypes.c_char_p),
     "h3_prepare_qk_i8": ([_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
     "h3_prepare_qk_i8hm": ([_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
+    "h3_prepare_qk_i4": ([_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, _S], ctypes.c_int),
     "h3_prepare_qk_rope_i8hm": (
         [_P(PrepareCfg), ctypes.c_uint32, View, View, View, View, View, View, _S], ctypes.c_int),
     "h3_prepare_k_rope_smooth_i8hm": (
@@ -144,6 +145,9 @@ SIGNATURES = {
         [_P(GemmCfg), ctypes.c_uint32, View, View, View, View, View, _S], ctypes.c_int),
     "h3_rope_dit_tables": (
         [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int),
+    "h3_attention_i4qk": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View, _S],
         ctypes.c_int),
     "h3_capacity": ([ctypes.c_uint32, ctypes.c_int], ctypes.c_uint32),
     "h3_stack_build": ([_P(StackDims), ctypes.c_void_p], ctypes.c_int),
@@ -242,6 +246,11 @@ def prepare_qk_i8hm(cfg: PrepareCfg, tokens: int, x, mean, codes, scales, stream
                                    view(scales), stream_ptr(stream)))
 
 
+def prepare_qk_i4(cfg: PrepareCfg, tokens: int, x, mean, codes, scales, stream=None) -> None:
+    check(lib().h3_prepare_qk_i4(ctypes.byref(cfg), tokens, view(x), view(mean), view(codes),
+                                 view(scales), stream_ptr(stream)))
+
+
 def prepare_qk_rope_i8hm(cfg: PrepareCfg, tokens: int, x, weight, cos_t, sin_t, codes, scales,
                          stream=None) -> None:
     check(lib().h3_prepare_qk_rope_i8hm(ctypes.byref(cfg), tokens, view(x), view(weight),
@@ -321,6 +330,12 @@ def rope_dit_tables(pos, inv_freq):
     check(lib().h3_rope_dit_tables(pos.ctypes.data, rows, inv.ctypes.data, cos.ctypes.data,
                                    sin.ctypes.data))
     return cos, sin
+
+
+def attention_i4qk(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                   stream=None) -> None:
+    check(lib().h3_attention_i4qk(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                  view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
 
 
 def capacity(tokens: int, causal: bool = False) -> int:

@@ -95,6 +95,14 @@ int h3_prepare_qk_i8(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x, h3_v
 int h3_prepare_qk_i8hm(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x, h3_view mean,
                        h3_view codes, h3_view scales, h3_stream stream);
 
+/* h3_prepare_qk_i4 (kernels/prepare_qk_i4.loom:1-244): the int4 operands of attention_i4qk*,
+ * token-major. The same rotation; amax = max(max|r|, 1e-30); scale = amax/7 * extra_scale;
+ * codes = clamp(rne(r*7/amax), +-7), eight 4-bit codes per i32 word, low nibble first.
+ *   x [tokens][row_stride] 16-bit, mean [row_stride] f32 (may be null) -> codes
+ *   [tokens][heads*16] i32, scales [tokens][heads] f32. token_capacity is not read. */
+int h3_prepare_qk_i4(const h3_prepare_cfg *cfg, uint32_t tokens, h3_view x, h3_view mean,
+                     h3_view codes, h3_view scales, h3_stream stream);
+
 /* h3_prepare_qk_rope_i8hm (kernels/prepare_qk_rope_i8hm.loom:19-243): per-head RMSNorm
  * (weight[128], eps), rotate-half RoPE on channels < 96 (pairs c <-> c+48, tables cos/sin
  * [tokens][48] f32), f16 rounding, then the quantizer with zero mean; head-major output.
@@ -252,6 +260,16 @@ int h3_attention_i8qkhm(const h3_attention_cfg *cfg, uint32_t token_count, uint3
  * same attention over token-major operands: qi [capacity][q_stride/4] i32, qs [capacity][heads],
  * ki [capacity][kv_stride/4], ks [capacity][heads]. */
 int h3_attention_i8qk(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                      h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                      h3_stream stream);
+
+/* h3_attention_i4qk (kernels/attention_i4qk_family.loom: attention_i4qk_mha_lds_f16_wmma and
+ * attention_i4qk_mha8_lds_f16_wmma; kernels/attention_i4qkl_mha8_lds_f16_wmma.loom for long
+ * sequences, src/stack.rs:712-722): the same attention over int4 operands from
+ * h3_prepare_qk_i4: qi [capacity][q_stride/2] bytes and ki [capacity][kv_stride/2] bytes (eight
+ * 4-bit codes per word, low nibble first), qs/ks [capacity][heads] f32. The reference's three
+ * launch shapes are one kernel here. */
+int h3_attention_i4qk(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                       h3_stream stream);
 

@@ -557,3 +557,42 @@ void h3o_prepare_plain_i8(const void *x, int fmt, int tokens, int width, int out
   }
   free(row);
 }
+
+/* int4 variant of the quantizer (kernels/prepare_qk_i4.loom:73-214): the same H_128 butterfly,
+ * amax = max(max|r|, 1e-30), sc = amax/7, inv = 7/amax, q = clamp(rne(r*inv), +-7), code e in
+ * nibble e%8 of word e/8 (low nibble first), scale = sc * extra. Token-major only
+ * (loom:7-8): codes [tokens][heads*16] i32, scales [tokens][heads]. */
+void h3o_quantize_row_i4(const float *y, float extra, int32_t *words, float *scale) {
+  float r[128];
+  h3o_hadamard128_f32(y, r);
+  float amax = 0.0f;
+  for (int e = 0; e < 128; ++e) amax = fmaxf(amax, fabsf(r[e]));
+  amax = fmaxf(amax, 1.0000000000000001e-30f);
+  const float sc = amax / 7.0f;
+  const float inv = 7.0f / amax;
+  for (int w = 0; w < 16; ++w) words[w] = 0;
+  for (int e = 0; e < 128; ++e) {
+    float q = rintf(r[e] * inv);
+    q = fminf(fmaxf(q, -7.0f), 7.0f);
+    words[e / 8] = (int32_t)((uint32_t)words[e / 8] | (((uint32_t)(int32_t)q & 15u) << (4 * (e % 8))));
+  }
+  *scale = sc * extra;
+}
+
+void h3o_prepare_qk_i4_f32(const uint16_t *x, int fmt, const float *mean, int tokens,
+                           int row_stride, int head_offset, int heads, float extra,
+                           int32_t *codes, float *scales) {
+  float y[128];
+  for (int t = 0; t < tokens; ++t) {
+    for (int h = 0; h < heads; ++h) {
+      const int col0 = head_offset + 128 * h;
+      for (int c = 0; c < 128; ++c) {
+        const float v = widen(x[(size_t)t * row_stride + col0 + c], fmt);
+        const float m = mean ? mean[col0 + c] : 0.0f;
+        y[c] = v - m;
+      }
+      h3o_quantize_row_i4(y, extra, codes + ((size_t)t * heads + h) * 16,
+                          scales + (size_t)t * heads + h);
+    }
+  }
+}

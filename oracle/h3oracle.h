@@ -16,6 +16,13 @@
  *                           Sylvester product where fp32 sums are exact; and by an independent
  *                           numpy restatement (tests/test_oracle.py).
  *   h3o_prepared_qk_f64     restatement of the reference test oracle tests/kernels.rs:1704-1741.
+ *   h3o_prepare_qk_i4_f32   kernels/prepare_qk_i4.loom:73-214: the pinned H_128 above with
+ *                           amax/7 scales and nibble packing. The reference holds no int4
+ *                           quantizer test; pinned by known answers (a one-hot row gives +-7
+ *                           in the Sylvester sign pattern, packed low nibble first as the
+ *                           reference's own attention test packs codes, tests/kernels.rs:2366-
+ *                           2375), by an independent numpy quantisation of the pinned rotation,
+ *                           and by consistency with the int8 quantizer's rotation.
  *   h3o_colmean_f32         kernels/colmean_f32.loom (in-file 30-40): sequential fp32 sum.
  *                           Pinned by exact integer-valued sums and by numpy cumulative float32.
  *   h3o_rope_qknorm_f16     this build's RMSNorm + rotate-half RoPE in a fixed fp32 order
@@ -79,6 +86,13 @@ float h3o_config_f32(double v);
 void h3o_prepare_qk_f32(const uint16_t *x, int fmt, const float *mean, int tokens, int row_stride,
                         int head_offset, int heads, float extra, int head_major, int capacity,
                         int32_t *codes, float *scales);
+
+/* int4 quantizer (kernels/prepare_qk_i4.loom:73-214), token-major: codes [tokens][heads*16]
+ * i32 (eight 4-bit codes per word, low nibble first), scales [tokens][heads] = amax/7 * extra. */
+void h3o_prepare_qk_i4_f32(const uint16_t *x, int fmt, const float *mean, int tokens,
+                           int row_stride, int head_offset, int heads, float extra,
+                           int32_t *codes, float *scales);
+void h3o_quantize_row_i4(const float *y, float extra, int32_t *words, float *scale);
 
 /* One head row: y[128] f32 (already mean-subtracted) -> 32 packed words + scale. */
 void h3o_quantize_row(const float *y, float extra, int32_t *words, float *scale);

@@ -77,6 +77,9 @@ def lib():
         L.h3o_gemm_i8_qkv.restype = None
         L.h3o_prepare_plain_i8.argtypes = [ctypes.c_void_p, c_int, c_int, c_int, c_int, i8, f32]
         L.h3o_prepare_plain_i8.restype = None
+        L.h3o_prepare_qk_i4_f32.argtypes = [u16, c_int, ctypes.c_void_p, c_int, c_int, c_int, c_int,
+                                            c_float, i32, f32]
+        L.h3o_prepare_qk_i4_f32.restype = None
         L.h3o_max_threads.argtypes = []
         L.h3o_max_threads.restype = c_int
         _lib = L
@@ -251,3 +254,24 @@ def prepare_plain_i8(x: np.ndarray, fmt: int, out_stride: int):
     lib().h3o_prepare_plain_i8(x.ctypes.data, fmt, tokens, width, out_stride, codes.reshape(-1),
                                scales)
     return codes, scales
+
+
+def prepare_qk_i4(x_bits: np.ndarray, fmt: int, mean, tokens: int, row_stride: int,
+                  head_offset: int, heads: int, extra: float):
+    """int4 quantizer, token-major; returns (codes i32 [tokens][heads*16], scales f32)."""
+    codes = np.zeros((tokens, heads * 16), np.int32)
+    scales = np.zeros((tokens, heads), np.float32)
+    m = None if mean is None else np.ascontiguousarray(mean, np.float32)
+    lib().h3o_prepare_qk_i4_f32(np.ascontiguousarray(x_bits, np.uint16), fmt,
+                                None if m is None else m.ctypes.data, tokens, row_stride,
+                                head_offset, heads, extra, codes, scales)
+    return codes, scales
+
+
+def unpack_i4(words: np.ndarray) -> np.ndarray:
+    """Words of eight 4-bit codes (low nibble first) -> int8 codes, last axis x8."""
+    w = np.ascontiguousarray(words, np.int32).view(np.uint32)
+    sh = (np.arange(8, dtype=np.uint32) * 4)
+    nib = ((w[..., None] >> sh) & 15).astype(np.int8)
+    nib = np.where(nib >= 8, nib - 16, nib).astype(np.int8)
+    return nib.reshape(*w.shape[:-1], w.shape[-1] * 8)

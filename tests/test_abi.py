@@ -217,3 +217,26 @@ def test_prepare_plain_bindings_and_configs():
         assert call_plain(bad, t, [1 << 40] * 3) == H.H3_ERR_CONFIG, (field, value)
     assert call_plain(cfg, t, [1 << 40] * 3, x_ptr=0x1008) == H.H3_ERR_ARGUMENT
     assert call_plain(cfg, 0, [1 << 40] * 3) == H.H3_ERR_ARGUMENT
+
+
+def test_int4_bindings_are_half_the_int8_extents():
+    """prepare_qk_i4 writes 64 code bytes per (token, head); attention_i4qk reads capacity rows
+    of q_stride/2 and kv_stride/2 code bytes (src/stack.rs:846, 1725-1750)."""
+    lib = H.lib()
+    cfg = H.PrepareCfg(512, 0, 4, 1.0, 64, 1e-5, H.H3_ELEM_F16)
+    t = 37
+    need = [t * 512 * 2, 2048, t * 4 * 64, t * 4 * 4]
+    sizes = list(need)
+    sizes[2] -= 1
+    st = lib.h3_prepare_qk_i4(ctypes.byref(cfg), t, *[fake(n) for n in sizes], None)
+    assert st == H.H3_ERR_BINDING and H.last_error() == (
+        f"prepare_qk_i4: binding 2 is {need[2] - 1} bytes, the kernel addresses {need[2]}")
+    acfg = att_cfg(97, 128, 4)
+    stride = 4 * 128
+    need = [128 * stride // 2, 128 * 4 * 4, 128 * stride // 2, 128 * 4 * 4, stride * 128 * 2,
+            97 * stride * 2]
+    for i in (0, 2):
+        sizes = list(need)
+        sizes[i] -= 1
+        st = lib.h3_attention_i4qk(ctypes.byref(acfg), 97, 4, *[fake(n) for n in sizes], None)
+        assert st == H.H3_ERR_BINDING and f"binding {i} " in H.last_error()
