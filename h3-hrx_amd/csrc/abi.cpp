@@ -123,13 +123,13 @@ int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
 }
 
 // Operand layouts of the attention kernels (attention.hip's modes).
-enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2 };
+enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2, kModeTokenI4Skip = 3 };
 
 int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
                      uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
-                     h3_view out, hipStream_t stream, int mode) {
+                     h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f) {
   const bool head_major = mode == kModeHeadI8;
-  const size_t code_div = mode == kModeTokenI4 ? 2 : 1;  // int4: half a byte per channel
+  const size_t code_div = mode >= kModeTokenI4 ? 2 : 1;  // int4: half a byte per channel
   if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
   // kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17
   if (!in_range(cfg->q_stride, 128, 32768, 128))
@@ -180,7 +180,7 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   int st = check_bindings(stage, views, need, 6);
   if (st) return st;
   if ((st = device_ready(stage))) return st;
-  return launched(stage, launch_attention(*cfg, mode, token_count, heads,
+  return launched(stage, launch_attention(*cfg, mode, skip_tau, token_count, heads,
                                           static_cast<const int32_t*>(qi.ptr),
                                           static_cast<const float*>(qs.ptr),
                                           static_cast<const int32_t*>(ki.ptr),
@@ -461,6 +461,20 @@ int h3_attention_i4qk(const h3_attention_cfg* cfg, uint32_t token_count, uint32_
                       h3_stream stream) {
   return attention_common("attention_i4qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI4);
+}
+
+int h3_attention_i4qks(const h3_attention_skip_cfg* cfg, uint32_t token_count, uint32_t heads,
+                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                       h3_stream stream) {
+  const char* stage = "attention_i4qks";
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  if (!(cfg->skip_tau == cfg->skip_tau) || cfg->skip_tau > 3.0e38f || cfg->skip_tau < -3.0e38f)
+    return set_error(H3_ERR_CONFIG, "%s: skip_tau must be finite", stage);
+  const h3_attention_cfg base = {cfg->q_stride, cfg->kv_stride, cfg->out_stride, cfg->tokens,
+                                 cfg->token_capacity, cfg->scale};
+  return attention_common(stage, &base, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI4Skip,
+                          cfg->skip_tau);
 }
 
 }  // extern "C"

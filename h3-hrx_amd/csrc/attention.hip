@@ -69,10 +69,12 @@ constexpr int kVLoads = 16 / kWaves;
 constexpr int kSRows = kKeys / kWaves;                      // scale rows stored per wave
 // Operand layouts: int8 codes token-major (attention_i8qk_*) or head-major (attention_i8qkhm_*),
 // and int4 codes token-major (attention_i4qk_*, eight codes per word, low nibble first).
-enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2 };
+// kTokenI4Skip is the int4 kernel with the tile skip of attention_i4qks_* (a threshold tau).
+enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2, kTokenI4Skip = 3 };
+constexpr bool isI4(int mode) { return mode == kTokenI4 || mode == kTokenI4Skip; }
 constexpr int kI4RowBytes = 64;                             // int4 K tile rows in LDS
-constexpr int kKRowsOf(int mode) { return mode == kTokenI4 ? kKeys * kI4RowBytes : kKRows; }
-constexpr int kKLoadsOf(int mode) { return mode == kTokenI4 ? 4 / kWaves : kKLoads; }
+constexpr int kKRowsOf(int mode) { return isI4(mode) ? kKeys * kI4RowBytes : kKRows; }
+constexpr int kKLoadsOf(int mode) { return isI4(mode) ? 4 / kWaves : kKLoads; }
 // s_waitcnt fields (gfx9 layout): vmcnt <= the loads one step issues (K tile, V^T tile, the
 // scale load), lgkmcnt 0, expcnt untouched; or vmcnt 0.
 constexpr int kWaitPrevStepOf(int mode) {
@@ -111,6 +113,7 @@ struct Args {
   uint32_t head_limit;
   uint32_t total;      // q_blocks * heads
   uint32_t per_xcd;    // ceil(total / 8)
+  float neg_tau;       // tile skip (kTokenI4Skip): -tau * log2(e)
 };
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
@@ -139,7 +142,7 @@ __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane)
   constexpr bool kHeadMajor = kMode == kHeadI8;
   Stager s;
   s.wave = wave;
-  if constexpr (kMode == kTokenI4) {
+  if constexpr (isI4(kMode)) {
 #pragma unroll
     for (int t = 0; t < kKLoadsOf(kMode); ++t) {
       const uint32_t o = (wave * kKLoadsOf(kMode) + t) * 1024 + 16 * lane;
@@ -173,7 +176,7 @@ template <int kMode>
 __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32_t kv_head,
                                          uint32_t k0, char* kst) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
-  constexpr uint32_t kCodeBytes = kMode == kTokenI4 ? 64 : 128;  // code bytes per (key, head)
+  constexpr uint32_t kCodeBytes = isI4(kMode) ? 64 : 128;  // code bytes per (key, head)
   const uint32_t live = a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
   const char* base;
   uint32_t bytes;
@@ -237,6 +240,7 @@ struct State {
   float m;       // running max in log2 units (u * qs * log2e)
   float l;       // this lane's partial row sum over its key slots
   float alpha;   // rescale of acc still owed for the last raise of m (1: none)
+  float gap;     // last tile's max minus the running max before it (log2 units; tile skip)
 };
 
 // Issue-order fence: the scheduler keeps each chunk's MFMA, LDS reads and VALU work together.
@@ -300,11 +304,20 @@ __device__ __forceinline__ float half_swap_max(float x) {
 __device__ __forceinline__ void raise_max(float tmax, float qsl, State& st) {
   tmax = half_swap_max(tmax);
   const float mt = tmax * qsl;
+  st.gap = mt - st.m;
   const float m_new = mt > st.m + kRescaleSlack ? mt : st.m;
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
   st.l *= alpha;
   st.alpha *= alpha;
   st.m = m_new;
+}
+
+// Tile skip decision (kernels/attention_i4qks_family.loom:318-324): the largest gap between a
+// tile's max and the running max before it over the wave's 32 queries, wave-uniform.
+__device__ __forceinline__ float wave_gap(float gap) {
+#pragma unroll
+  for (int k = 1; k < 32; k <<= 1) gap = fmaxf(gap, __shfl_xor(gap, k));
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gap)));
 }
 
 // LDS byte offset, inside a row, of logical 16-byte chunk 2x + half for rows with (row/2)%8 = sw.
@@ -344,7 +357,7 @@ __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4],
   const char* krow = kst + n * kRowBytes;
   const float* kss = reinterpret_cast<const float*>(kst + kKRowsOf(kMode));
   v16i s[2];
-  if constexpr (kMode == kTokenI4) {
+  if constexpr (isI4(kMode)) {
     v4i kop[8];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -379,10 +392,13 @@ __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4],
 //   kst    LDS stage of K(j+1) (unused when !kNext), vst  LDS stage of V(j)
 //   u      in: tile j's dequantized scores; out: tile j+1's
 //   knext0 first key of tile j+1
+//   skip   (kTokenI4Skip only, wave-uniform) tile j is skipped: no probabilities and no PV;
+//          tile j+1 is still prepared
 template <int kMode, bool kNext, bool kMaskNext, bool kMaskCur>
 __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i (&qop)[4],
                                      float qsl, State& st, float (&u)[2][16], int n, int half,
-                                     uint32_t knext0, uint32_t tokens) {
+                                     uint32_t knext0, uint32_t tokens, bool skip = false) {
+  const bool do_pv = kMode != kTokenI4Skip || !skip;
   // The rescale owed by the last raise of m, now that PV(j-1) has accumulated.
   if (__any(st.alpha != 1.0f)) {
 #pragma unroll
@@ -407,7 +423,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   float la = 0.0f, lb = 0.0f;
 
   // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
-  constexpr bool kI4 = kMode == kTokenI4;
+  constexpr bool kI4 = isI4(kMode);
   if (kNext) {
     if constexpr (kI4) {  // chunks 0..3 now, 4..7 two MFMAs ahead of their use
       k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 0, kop[0], kop[2]);
@@ -430,13 +446,13 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
       const int w = c + kPf;
       kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
     }
-    if (c >= 8 - kPf) {
+    if (do_pv && c >= 8 - kPf) {
       const int w = c - (8 - kPf);
       vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
     if (kNext)
       s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
-    exp_pair<kMaskCur>(u, 0, 2 * c, qsl, negm, pb, la);
+    if (do_pv) exp_pair<kMaskCur>(u, 0, 2 * c, qsl, negm, pb, la);
     H3_CHUNK_END();
   }
 
@@ -445,7 +461,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     const int g = c >> 2, db = c & 3;
-    if (c + kPf < 16) {
+    if (do_pv && c + kPf < 16) {
       const int w = c + kPf;
       vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
@@ -454,9 +470,10 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
       k4[q] = *reinterpret_cast<const float4*>(kss + kb);
       c4[q] = *reinterpret_cast<const float4*>(kss + kKeys + kb);
     }
-    st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[g], st.acc[db], 0, 0, 0);
-    if (c < 8)
-      exp_pair<kMaskCur>(u, 1, 2 * c, qsl, negm, pb, lb);
+    if (do_pv) {
+      st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[g], st.acc[db], 0, 0, 0);
+      if (c < 8) exp_pair<kMaskCur>(u, 1, 2 * c, qsl, negm, pb, lb);
+    }
     if (kNext && c >= 6 && c < 14) {
       const int q = c - 6, bb = q >> 2, i = q & 3;
       dequant4<kMaskNext>(s, bb, i, k4[q], c4[q], u, tmax, knext0 + slot_key(bb, i, half),
@@ -475,6 +492,7 @@ template <int kMode>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention(Args a) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
+  constexpr bool kSkip = kMode == kTokenI4Skip;
   constexpr int kWaitPrevStep = kWaitPrevStepOf(kMode);
   // Three K stages and three V^T stages, each its own array so that the compiler can tell an
   // LDS-DMA into one stage from the reads of another.
@@ -519,7 +537,7 @@ void k_attention(Args a) {
 
   // Q^T operand, held for the whole key loop: 4 chunks of 32 channels, 16 bytes per lane.
   v4i qop[4];
-  if constexpr (kMode == kTokenI4) {  // 64 code bytes per (token, head), widened like K
+  if constexpr (isI4(kMode)) {  // 64 code bytes per (token, head), widened like K
     const char* src = reinterpret_cast<const char*>(a.qi) + (size_t)q_read * a.q_row + head * 64;
     const uint4 w0 = *reinterpret_cast<const uint4*>(src + 16 * half);
     const uint4 w1 = *reinterpret_cast<const uint4*>(src + 16 * (2 + half));
@@ -536,7 +554,7 @@ void k_attention(Args a) {
   const float qsv = kHeadMajor ? a.qs[(size_t)head * a.capacity + q_read]
                                : a.qs[(size_t)q_read * a.head_limit + head];
   // log2 units; int4 scores arrive 256x (the widened codes are 16x each)
-  const float qsl = kMode == kTokenI4 ? qsv * kLog2e * (1.0f / 256.0f) : qsv * kLog2e;
+  const float qsl = isI4(kMode) ? qsv * kLog2e * (1.0f / 256.0f) : qsv * kLog2e;
 
   State st;
 #pragma unroll
@@ -556,6 +574,15 @@ void k_attention(Args a) {
   else
     first_tile<kMode, false>(k0s, qop, qsl, st, u, n, half, a.tokens);
   step_barrier<kWaitAll>();  // K(0)'s stage is refilled by step 0
+  // Tile skip: whether tile j's probabilities and PV are dropped, decided from its max once it is
+  // dequantized (the first tile always stays: the running max before it is -1e30).
+  bool skip = false;
+  if constexpr (kSkip) skip = wave_gap(st.gap) < a.neg_tau;
+#define H3_STEP(KN, KMN, KMC, KST, VST, KNEXT0)                                                \
+  {                                                                                          \
+    step<kMode, KN, KMN, KMC>(KST, VST, qop, qsl, st, u, n, half, KNEXT0, a.tokens, skip);   \
+    if (kSkip && KN) skip = wave_gap(st.gap) < a.neg_tau;                                    \
+  }
 
   // One steady step j (tile j+1 full) on compile-time stages: reads K(j+1) from kn, V(j) from
   // vc; stages K(j+3) into kc (K(j)'s stage) and V(j+2) into vn2 (V(j-1)'s stage); stores the
@@ -564,8 +591,7 @@ void k_attention(Args a) {
   {                                                                                          \
     const float ks_new = stage_k<kMode>(a, sg, kv_head, (j + 3) * kKeys, kc);                \
     stage_v(a, sg, kv_head, (j + 2) * kKeys, vn2);                                           \
-    step<kMode, true, false, false>(kn, vc, qop, qsl, st, u, n, half, (j + 1) * kKeys,       \
-                                    a.tokens);                                               \
+    H3_STEP(true, false, false, kn, vc, (j + 1) * kKeys)                                     \
     store_scales<kMode>(kn2, sg, ks_held);                                                   \
     ks_held = ks_new;                                                                        \
     step_barrier<kWaitPrevStep>();                                                           \
@@ -588,15 +614,15 @@ void k_attention(Args a) {
   auto kst = [&](uint32_t t) { const uint32_t r = t % 3; return r == 0 ? k0s : r == 1 ? k1s : k2s; };
   auto vst = [&](uint32_t t) { const uint32_t r = t % 3; return r == 0 ? v0s : r == 1 ? v1s : v2s; };
   if (n_tiles > full && full > 0) {  // j == full - 1: tile j+1 is the partial tile
-    step<kMode, true, true, false>(kst(j + 1), vst(j), qop, qsl, st, u, n, half, (j + 1) * kKeys,
-                                   a.tokens);
+    H3_STEP(true, true, false, kst(j + 1), vst(j), (j + 1) * kKeys)
     step_barrier<kWaitAll>();
     ++j;
   }
   if (n_tiles > full)
-    step<kMode, false, false, true>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
+    H3_STEP(false, false, true, nullptr, vst(j), 0)
   else
-    step<kMode, false, false, false>(nullptr, vst(j), qop, qsl, st, u, n, half, 0, a.tokens);
+    H3_STEP(false, false, false, nullptr, vst(j), 0)
+#undef H3_STEP
   // The last step raises no max, so no rescale is owed after its PV.
   step_barrier<kWaitAll>();  // no staging load outlives the workgroup
 
@@ -619,7 +645,8 @@ void k_attention(Args a) {
 
 }  // namespace
 
-hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, uint32_t token_count,
+hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
+                            uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out,
                             hipStream_t stream) {
@@ -633,8 +660,9 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, uint32_t toke
   a.tokens = cfg.tokens;
   a.token_count = token_count;
   a.capacity = cfg.token_capacity;
-  a.q_row = mode == kTokenI4 ? cfg.q_stride / 2 : cfg.q_stride;
-  a.kv_bytes = mode == kTokenI4 ? cfg.kv_stride / 2 : cfg.kv_stride;
+  a.q_row = isI4(mode) ? cfg.q_stride / 2 : cfg.q_stride;
+  a.kv_bytes = isI4(mode) ? cfg.kv_stride / 2 : cfg.kv_stride;
+  a.neg_tau = -skip_tau * kLog2e;
   a.out_stride = cfg.out_stride;
   a.q_blocks = (token_count + kQueriesPerBlock - 1) / kQueriesPerBlock;
   a.heads = heads;
@@ -647,6 +675,8 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, uint32_t toke
     hipLaunchKernelGGL(k_attention<kHeadI8>, grid, dim3(kThreads), 0, stream, a);
   else if (mode == kTokenI4)
     hipLaunchKernelGGL(k_attention<kTokenI4>, grid, dim3(kThreads), 0, stream, a);
+  else if (mode == kTokenI4Skip)
+    hipLaunchKernelGGL(k_attention<kTokenI4Skip>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();

@@ -71,8 +71,10 @@ hipError_t launch_gemm_i8_qkv(uint32_t m, uint32_t n, uint32_t k, uint32_t k_str
 hipError_t launch_prepare_plain(uint32_t width, uint32_t out_stride, uint32_t elem,
                                 uint32_t tokens, const void* x, uint8_t* codes, float* scales,
                                 hipStream_t stream);
-// mode: 0 int8 token-major, 1 int8 head-major, 2 int4 token-major
-hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, uint32_t token_count,
+// mode: 0 int8 token-major, 1 int8 head-major, 2 int4 token-major, 3 int4 with tile skip
+// (skip_tau is read in mode 3 only)
+hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
+                            uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out,
                             hipStream_t stream);

@@ -96,6 +96,18 @@ class PreparePlainCfg(ctypes.Structure):
     ]
 
 
+class AttentionSkipCfg(ctypes.Structure):
+    _fields_ = [
+        ("q_stride", ctypes.c_uint32),
+        ("kv_stride", ctypes.c_uint32),
+        ("out_stride", ctypes.c_uint32),
+        ("tokens", ctypes.c_uint32),
+        ("token_capacity", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+        ("skip_tau", ctypes.c_float),
+    ]
+
+
 class StackDims(ctypes.Structure):
     _fields_ = [
         ("heads", ctypes.c_uint32),
@@ -149,6 +161,9 @@ SIGNATURES = {
     "h3_attention_i4qk": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View, _S],
         ctypes.c_int),
+    "h3_attention_i4qks": (
+        [_P(AttentionSkipCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         _S], ctypes.c_int),
     "h3_capacity": ([ctypes.c_uint32, ctypes.c_int], ctypes.c_uint32),
     "h3_stack_build": ([_P(StackDims), ctypes.c_void_p], ctypes.c_int),
     "h3_stack_destroy": ([ctypes.c_void_p], None),
@@ -336,6 +351,12 @@ def attention_i4qk(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, 
                    stream=None) -> None:
     check(lib().h3_attention_i4qk(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
                                   view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
+
+
+def attention_i4qks(cfg: AttentionSkipCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                    stream=None) -> None:
+    check(lib().h3_attention_i4qks(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                   view(ki), view(ks), view(vt), view(out), stream_ptr(stream)))
 
 
 def capacity(tokens: int, causal: bool = False) -> int:

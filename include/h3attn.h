@@ -273,6 +273,30 @@ int h3_attention_i4qk(const h3_attention_cfg *cfg, uint32_t token_count, uint32_
                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                       h3_stream stream);
 
+/* Config of the skip twins h3.attention_i4qks_* (kernels/attention_i4qks_family.loom:
+ * 487-534): the attention config plus skip_tau (finite; the reference's Stack selects the twins
+ * for tau > 0, src/stack.rs:727-745). */
+typedef struct {
+  uint32_t q_stride;
+  uint32_t kv_stride;
+  uint32_t out_stride;
+  uint32_t tokens;
+  uint32_t token_capacity;
+  float scale;
+  float skip_tau;
+} h3_attention_skip_cfg;
+
+/* h3_attention_i4qks (kernels/attention_i4qks_family.loom, attention_i4qksl_mha8_lds_f16_wmma
+ * .loom): h3_attention_i4qk with the reference's tile skip. For each key tile and each wave of
+ * queries, gap = max over the wave's queries of (the tile's max score - the running max before
+ * the tile), in the natural-log units of the scores; a tile with gap < -skip_tau adds nothing
+ * (no probabilities, no PV; loom:318-324). Tiles here are 64 keys x 32 queries (the reference's
+ * 16 x 16), and the running max is the kernel's lazily raised one (never above the exact max),
+ * so this kernel never skips a tile the exact rule would keep at this granularity. */
+int h3_attention_i4qks(const h3_attention_skip_cfg *cfg, uint32_t token_count, uint32_t heads,
+                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                       h3_stream stream);
+
 /* ------------------------------------------------------------------ stack (host mirror) */
 
 /* Row capacity the reference allocates for a sequence of `tokens` (src/stack.rs:299-302):

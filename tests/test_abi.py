@@ -240,3 +240,19 @@ def test_int4_bindings_are_half_the_int8_extents():
         sizes[i] -= 1
         st = lib.h3_attention_i4qk(ctypes.byref(acfg), 97, 4, *[fake(n) for n in sizes], None)
         assert st == H.H3_ERR_BINDING and f"binding {i} " in H.last_error()
+
+
+def test_skip_twin_checks_tau_and_bindings():
+    lib = H.lib()
+    stride = 4 * 128
+    cfg = H.AttentionSkipCfg(stride, stride, stride, 97, 128, 1.0, float("nan"))
+    sizes = [1 << 30] * 6
+    assert lib.h3_attention_i4qks(ctypes.byref(cfg), 97, 4, *[fake(n) for n in sizes],
+                                  None) == H.H3_ERR_CONFIG
+    cfg.skip_tau = 2.0
+    need = [128 * stride // 2, 128 * 4 * 4, 128 * stride // 2, 128 * 4 * 4, stride * 128 * 2,
+            97 * stride * 2]
+    sizes = list(need)
+    sizes[5] -= 2
+    st = lib.h3_attention_i4qks(ctypes.byref(cfg), 97, 4, *[fake(n) for n in sizes], None)
+    assert st == H.H3_ERR_BINDING and H.last_error().startswith("attention_i4qks: binding 5")

@@ -11,7 +11,12 @@
     computes 256x the dot product and folds 1/256 into the query scale; the dequantisation's
     -1.5*2^23*ks term carries the same rounding error in both, relatively 256x smaller in int4,
     so the two are not bit-identical);
-  - quantizer + attention at BASELINE config 2's token count on sampled rows.
+  - quantizer + attention at BASELINE config 2's token count on sampled rows;
+  - the skip twin (h3_attention_i4qks): with the reference test's tau = 1000 it equals the
+    unskipped kernel bit for bit, with tau = 0 its output is finite (tests/kernels.rs:2420-2455),
+    and on inputs whose 64-key tiles have clearly separated scores it drops exactly the tiles
+    the rule gap < -tau names (the output equals the attention over the kept tiles and differs
+    from the full attention).
 """
 import numpy as np
 import pytest
@@ -181,3 +186,73 @@ def test_i4_path_at_config2_tokens_on_sampled_rows(dev):
     got = from_dev(out).view(np.float16).astype(np.float64).reshape(tokens, heads, 128)[rows]
     mx, mean_err = north_star_ok(got, want)
     assert mx <= 2e-2 and mean_err <= 2e-3, (mx, mean_err)
+
+
+def skip_run(dev, q, qs, k, ks, vt, tokens, cap, heads, tau):
+    import torch
+
+    stride = heads * 128
+    cfg = H.AttentionSkipCfg(stride, stride, stride, tokens, cap, 1.0, tau)
+    out = torch.zeros((tokens, stride), dtype=torch.float16, device=dev)
+    H.attention_i4qks(cfg, tokens, heads, to_dev(q, dev), to_dev(qs, dev), to_dev(k, dev),
+                      to_dev(ks, dev), to_dev(vt, dev), out)
+    torch.cuda.synchronize()
+    return from_dev(out)
+
+
+@pytest.mark.parametrize("tokens", [97, 4097])
+def test_skip_twin_with_large_tau_equals_the_unskipped_kernel(dev, tokens):
+    heads = 2
+    rng = np.random.default_rng(tokens + 11)
+    stride = heads * 128
+    cap = H.capacity(tokens)
+    q = rng.integers(-7, 8, (cap, stride)).astype(np.int8)
+    k = rng.integers(-7, 8, (cap, stride)).astype(np.int8)
+    q[tokens:] = 0
+    k[tokens:] = 0
+    qs = rng.uniform(0.005, 0.03, (cap, heads)).astype(np.float32)
+    ks = rng.uniform(0.005, 0.03, (cap, heads)).astype(np.float32)
+    v = O.f16_bits(rng.standard_normal((tokens, stride)).astype(np.float32)).reshape(tokens, stride)
+    vt = O.transpose(v, O.F16, tokens, stride, 0, stride, cap, cap)
+    print(f"skip twin tau=1000 tokens={tokens}", flush=True)
+    got = skip_run(dev, pack_i4(q), qs, pack_i4(k), ks, vt, tokens, cap, heads, 1000.0)
+    base = run_i4(dev, pack_i4(q), qs, pack_i4(k), ks, vt, tokens, cap, heads, H.attention_i4qk)
+    assert np.array_equal(got, base)
+    zero = skip_run(dev, pack_i4(q), qs, pack_i4(k), ks, vt, tokens, cap, heads, 0.0)
+    assert np.all(np.isfinite(zero.view(np.float16)))
+
+
+def test_skip_twin_drops_exactly_the_far_tiles(dev):
+    """Six 64-key tiles with uniform scores 10, 8.5, 9.8, 5, 10.2, 9 (natural units) for every
+    query; tau = 0.5 drops tiles 1, 3 and 5 (gaps -1.5, -5 and -1.2) and keeps 0, 2 and 4."""
+    heads, tokens = 1, 384
+    stride = 128
+    cap = H.capacity(tokens)
+    rng = np.random.default_rng(2)
+    c = (rng.integers(0, 2, 128) * 14 - 7).astype(np.int8)  # +-7
+    dot = float(np.dot(c.astype(np.int64), c.astype(np.int64)))  # 6272
+    q = np.zeros((cap, stride), np.int8)
+    k = np.zeros((cap, stride), np.int8)
+    q[:tokens] = c
+    k[:tokens] = c
+    scores = [10.0, 8.5, 9.8, 5.0, 10.2, 9.0]
+    qs = np.zeros((cap, 1), np.float32)
+    ks = np.zeros((cap, 1), np.float32)
+    qs[:tokens] = 1.0
+    for t, sc in enumerate(scores):
+        ks[64 * t:64 * t + 64] = np.float32(sc / dot)
+    v = O.f16_bits(rng.standard_normal((tokens, stride)).astype(np.float32)).reshape(tokens, stride)
+    vt = O.transpose(v, O.F16, tokens, stride, 0, stride, cap, cap)
+    got = skip_run(dev, pack_i4(q), qs, pack_i4(k), ks, vt, tokens, cap, heads, 0.5)
+    got = got.view(np.float16).astype(np.float64).reshape(tokens, 1, 128)
+    kept = ks.copy()
+    for t in (1, 3, 5):
+        kept[64 * t:64 * t + 64] = -np.inf
+    rows = np.array([0, 31, 32, 200, 383], np.int32)
+    qc = q.reshape(cap, 1, 128).transpose(1, 0, 2).copy()
+    kc = k.reshape(cap, 1, 128).transpose(1, 0, 2).copy()
+    want = O.attention_f64(qc, qs.T.copy(), kc, kept.T.copy(), vt, tokens, cap, 1, rows)
+    full = O.attention_f64(qc, qs.T.copy(), kc, ks.T.copy(), vt, tokens, cap, 1, rows)
+    mx, mean = north_star_ok(got[rows], want)
+    assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
+    assert np.abs(full - want).max() > 0.05  # the dropped tiles carry real weight
