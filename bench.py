@@ -70,6 +70,35 @@ def time_launches(torch, fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
+    """The INT4 QK family at the same shape (BASELINE config 5a's int4 QK, with the reference's
+    per-(token, head) absmax/7 scales): prepare_qk_i4 of Q and K from the fused rows, then
+    attention_i4qk and its skip twin at tau = 2 (natural-log units of the scores)."""
+    width = heads * 128
+    cap = H.capacity(tokens)
+    qi = torch.zeros((cap, width // 8), dtype=torch.int32, device=dev)
+    ki = torch.zeros_like(qi)
+    qs = torch.zeros((cap, heads), dtype=torch.float32, device=dev)
+    ks = torch.zeros_like(qs)
+    elem = H.H3_ELEM_BF16
+    pq = H.PrepareCfg(3 * width, 0, heads, H.EXTRA_Q, cap, 1e-5, elem)
+    pk = H.PrepareCfg(3 * width, width, heads, 1.0, cap, 1e-5, elem)
+    prep_ms = time_launches(torch, lambda: (H.prepare_qk_i4(pq, tokens, fused, None, qi, qs),
+                                            H.prepare_qk_i4(pk, tokens, fused, None, ki, ks)), 5)
+    ac = H.AttentionCfg(width, width, width, tokens, cap, 1.0)
+    ops = 4.0 * tokens * tokens * heads * 128
+    att_ms = time_launches(torch, lambda: H.attention_i4qk(ac, tokens, heads, qi, qs, ki, ks, vt,
+                                                           out), 2)
+    sc = H.AttentionSkipCfg(width, width, width, tokens, cap, 1.0, 2.0)
+    skip_ms = time_launches(torch, lambda: H.attention_i4qks(sc, tokens, heads, qi, qs, ki, ks,
+                                                             vt, out), 2)
+    return {"prepare_qk_i4_x2_ms": round(prep_ms, 4),
+            "attention_i4qk_ms": round(att_ms, 3),
+            "attention_i4qk_tops": round(ops / (att_ms * 1e-3) / 1e12, 1),
+            "attention_i4qks_tau2_ms": round(skip_ms, 3),
+            "note": "no int4 MFMA on gfx950: codes are widened to int8 in registers"}
+
+
 def adjacent_kernels(torch, H, dev, tokens, width, out):
     """The kernels either side of the path at the same shape, timed on their own (they are not
     part of the step): the compact INT8 QKV projection that produces Q/K rows and V^T
@@ -301,6 +330,9 @@ def main() -> None:
     if not args.no_adjacent:
         print("# adjacent kernels...", file=sys.stderr, flush=True)
         line["adjacent_kernels"] = adjacent_kernels(torch, H, dev, tokens, width, out)
+        print("# int4 path...", file=sys.stderr, flush=True)
+        line["adjacent_kernels"]["int4_qk"] = int4_path(torch, H, dev, tokens, heads, fused_bf16,
+                                                        vt, torch.empty_like(out))
     if not args.no_cpu:
         print("# cpu baseline...", file=sys.stderr, flush=True)
         q16 = fused_bf16[:, :width].to(torch.float16).cpu().numpy().view(np.uint16)
