@@ -51,6 +51,22 @@
  *                           and by an independent numpy restatement. The rounding order of the
  *                           butterflies follows the .loom text; no reference vector pins it
  *                           beyond those checks.
+ *   h3o_vsa_*               the VSA path (h3oracle_vsa.c): the cube plan and top-k budget of
+ *                           src/vsa.rs:54-143 and the vsa_ops / vsa_kmean kernels as literal
+ *                           restatements (route by the reference's rank count). Pinned by the
+ *                           reference's own tests: the plan tests of src/vsa.rs:145-225 (prefix
+ *                           tiles [64, 1, 6], bijection, prefix rows first), its budget cases
+ *                           topk(25) = 2, topk(35) = 4, topk(1) = 0 and its sigma-window cases,
+ *                           and the independent masked oracle of src/vsa/device.rs:513-620
+ *                           (f32 block means, scores, a sort-based top-k threshold, the neighbour
+ *                           and prefix rule, all-tie rows keeping every block), restated in numpy
+ *                           in tests/test_oracle_vsa.py; by brute-force closed forms (integer
+ *                           means, one-hot scores) and planted mistakes. h3o_vsa_coarse_f64 and
+ *                           h3o_vsa_attention_f64 are exact-arithmetic statements of what the
+ *                           reference approximates (expf<afn>, f16 probabilities): pinned by
+ *                           closed forms (uniform scores give the mean of the routed values, a
+ *                           route to one block gives that block's attention) and by the dense
+ *                           h3o_attention_f64 when every block is routed.
  *   h3o_attention_f64       the attention the operands define, tests/kernels.rs:1891-1913 and
  *                           2084-2111: softmax_j(sum(qc*kc) * qs * ks) . V in f64. Pinned by
  *                           closed forms: uniform keys give the mean of V, a single dominant key
@@ -158,6 +174,37 @@ void h3o_gemm_i8_qkv(const int8_t *a, const int8_t *w, const float *ws, const fl
  * [tokens] f32. */
 void h3o_prepare_plain_i8(const void *x, int fmt, int tokens, int width, int out_stride,
                           int8_t *codes, float *scales);
+
+/* ---- VSA (h3oracle_vsa.c; src/vsa.rs, kernels/vsa_ops.loom, vsa_kmean.loom, vsa_attention_8) */
+/* Blocks of the plan: 64-row tiles of each prefix segment plus 4x4x4 video cubes. */
+int h3o_vsa_plan_blocks(const int *seg_rows, int n_segs, int nt, int nh, int nw);
+/* src/vsa.rs:94-143. segments (row0, rows) in order; video cells (t, h, w) at rows
+ * seq_len - nt*nh*nw + (t*nh + h)*nw + w. src [64*blocks], inverse [seq_len], lengths [blocks].
+ * Returns the block count, or -1 when some row is not covered. */
+int h3o_vsa_plan(const int *seg_row0, const int *seg_rows, int n_segs, int seq_len, int nt,
+                 int nh, int nw, int32_t *src, int32_t *inverse, int32_t *lengths,
+                 int *prefix_blocks);
+int h3o_vsa_topk(double keep_percent, int nonprefix);
+int h3o_vsa_dense_reason(double start, double end, long min_tokens, long tokens, float sigma,
+                         double shift);
+void h3o_vsa_gather(const int32_t *src, int padded, int tokens, int width, const uint16_t *x,
+                    uint16_t *y);
+void h3o_vsa_scatter(const int32_t *inverse, int tokens, int width, const uint16_t *x,
+                     uint16_t *y);
+void h3o_vsa_pool(const int32_t *lengths, int blocks, int width, const uint16_t *x,
+                  float *means);
+void h3o_vsa_scores(const float *qm, const float *km, int blocks, int heads, float *scores);
+void h3o_vsa_route(const float *scores, int blocks, int heads, int prefix, int topk,
+                   int32_t *routes);
+void h3o_vsa_coarse_f64(const float *scores, const float *vm, int blocks, int heads,
+                        double *coarse);
+void h3o_vsa_gated_scatter(const int32_t *inverse, int tokens, int width, const uint16_t *fine,
+                           const uint16_t *gate, const float *coarse, uint16_t *out);
+void h3o_vsa_kmean(const float *x, int tokens, int width, float *mean);
+int h3o_vsa_attention_f64(const int8_t *qc, const float *qs, const int8_t *kc, const float *ks,
+                          const uint16_t *vt, int tokens, int capacity, int heads,
+                          const int32_t *routes, const int32_t *lengths, const int *rows,
+                          int n_rows, double *out, int threads);
 
 int h3o_max_threads(void);
 

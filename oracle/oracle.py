@@ -80,6 +80,36 @@ def lib():
         L.h3o_prepare_qk_i4_f32.argtypes = [u16, c_int, ctypes.c_void_p, c_int, c_int, c_int, c_int,
                                             c_float, i32, f32]
         L.h3o_prepare_qk_i4_f32.restype = None
+        ip = _P(np.int32, flags="C")
+        L.h3o_vsa_plan_blocks.argtypes = [ip, c_int, c_int, c_int, c_int]
+        L.h3o_vsa_plan_blocks.restype = c_int
+        L.h3o_vsa_plan.argtypes = [ip, ip, c_int, c_int, c_int, c_int, c_int, i32, i32, i32,
+                                   ctypes.POINTER(c_int)]
+        L.h3o_vsa_plan.restype = c_int
+        L.h3o_vsa_topk.argtypes = [c_double, c_int]
+        L.h3o_vsa_topk.restype = c_int
+        L.h3o_vsa_dense_reason.argtypes = [c_double, c_double, ctypes.c_long, ctypes.c_long,
+                                           c_float, c_double]
+        L.h3o_vsa_dense_reason.restype = c_int
+        L.h3o_vsa_gather.argtypes = [i32, c_int, c_int, c_int, u16, u16]
+        L.h3o_vsa_gather.restype = None
+        L.h3o_vsa_scatter.argtypes = [i32, c_int, c_int, u16, u16]
+        L.h3o_vsa_scatter.restype = None
+        L.h3o_vsa_pool.argtypes = [i32, c_int, c_int, u16, f32]
+        L.h3o_vsa_pool.restype = None
+        L.h3o_vsa_scores.argtypes = [f32, f32, c_int, c_int, f32]
+        L.h3o_vsa_scores.restype = None
+        L.h3o_vsa_route.argtypes = [f32, c_int, c_int, c_int, c_int, i32]
+        L.h3o_vsa_route.restype = None
+        L.h3o_vsa_coarse_f64.argtypes = [f32, f32, c_int, c_int, f64]
+        L.h3o_vsa_coarse_f64.restype = None
+        L.h3o_vsa_gated_scatter.argtypes = [i32, c_int, c_int, u16, u16, f32, u16]
+        L.h3o_vsa_gated_scatter.restype = None
+        L.h3o_vsa_kmean.argtypes = [f32, c_int, c_int, f32]
+        L.h3o_vsa_kmean.restype = None
+        L.h3o_vsa_attention_f64.argtypes = [i8, f32, i8, f32, u16, c_int, c_int, c_int, i32, i32,
+                                            ip, c_int, f64, c_int]
+        L.h3o_vsa_attention_f64.restype = c_int
         L.h3o_max_threads.argtypes = []
         L.h3o_max_threads.restype = c_int
         _lib = L
@@ -275,3 +305,120 @@ def unpack_i4(words: np.ndarray) -> np.ndarray:
     nib = ((w[..., None] >> sh) & 15).astype(np.int8)
     nib = np.where(nib >= 8, nib - 16, nib).astype(np.int8)
     return nib.reshape(*w.shape[:-1], w.shape[-1] * 8)
+
+
+# --------------------------------------------------------------------- VSA (h3oracle_vsa.c)
+
+DENSE_REASONS = {0: None, 1: "below_min_tokens", 2: "outside_sigma_window"}
+
+
+def vsa_plan(segments, seq_len: int, nt: int, nh: int, nw: int):
+    """src/vsa.rs:94-143. segments: [(row0, rows)] of the prefix (text, references, audio) in
+    order; the video grid nt x nh x nw ends the sequence. Returns (src, inverse, lengths,
+    prefix_blocks)."""
+    row0 = np.ascontiguousarray([s[0] for s in segments] or [0], np.int32)
+    rows = np.ascontiguousarray([s[1] for s in segments] or [0], np.int32)
+    n_segs = len(segments)
+    blocks = lib().h3o_vsa_plan_blocks(rows, n_segs, nt, nh, nw)
+    src = np.zeros(64 * blocks, np.int32)
+    inverse = np.zeros(max(seq_len, 1), np.int32)
+    lengths = np.zeros(max(blocks, 1), np.int32)
+    prefix = ctypes.c_int(0)
+    got = lib().h3o_vsa_plan(row0, rows, n_segs, seq_len, nt, nh, nw, src, inverse, lengths,
+                             ctypes.byref(prefix))
+    if got < 0:
+        raise ValueError("VSA layout must cover every live token")
+    return src, inverse[:seq_len], lengths[:blocks], prefix.value
+
+
+def vsa_topk(keep_percent: float, nonprefix: int) -> int:
+    return int(lib().h3o_vsa_topk(keep_percent, nonprefix))
+
+
+def vsa_dense_reason(start, end, min_tokens, tokens, sigma, shift):
+    return DENSE_REASONS[lib().h3o_vsa_dense_reason(start, end, min_tokens, tokens, sigma, shift)]
+
+
+def vsa_gather(src, tokens, x_bits):
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    width = x.shape[1]
+    src = np.ascontiguousarray(src, np.int32)
+    y = np.zeros((len(src), width), np.uint16)
+    lib().h3o_vsa_gather(src, len(src), tokens, width, x, y)
+    return y
+
+
+def vsa_scatter(inverse, x_bits):
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    inverse = np.ascontiguousarray(inverse, np.int32)
+    y = np.zeros((len(inverse), x.shape[1]), np.uint16)
+    lib().h3o_vsa_scatter(inverse, len(inverse), x.shape[1], x, y)
+    return y
+
+
+def vsa_pool(lengths, x_bits):
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    lengths = np.ascontiguousarray(lengths, np.int32)
+    means = np.zeros((len(lengths), x.shape[1]), np.float32)
+    lib().h3o_vsa_pool(lengths, len(lengths), x.shape[1], x, means)
+    return means
+
+
+def vsa_scores(qm, km, heads):
+    qm = np.ascontiguousarray(qm, np.float32)
+    km = np.ascontiguousarray(km, np.float32)
+    blocks = qm.shape[0]
+    out = np.zeros((heads, blocks, blocks), np.float32)
+    lib().h3o_vsa_scores(qm, km, blocks, heads, out)
+    return out
+
+
+def vsa_route(scores, prefix, topk):
+    scores = np.ascontiguousarray(scores, np.float32)
+    heads, blocks, _ = scores.shape
+    routes = np.zeros((heads, blocks, blocks), np.int32)
+    lib().h3o_vsa_route(scores, blocks, heads, prefix, topk, routes)
+    return routes
+
+
+def vsa_coarse_f64(scores, vm):
+    scores = np.ascontiguousarray(scores, np.float32)
+    vm = np.ascontiguousarray(vm, np.float32)
+    heads, blocks, _ = scores.shape
+    out = np.zeros((blocks, heads * 128), np.float64)
+    lib().h3o_vsa_coarse_f64(scores, vm, blocks, heads, out)
+    return out
+
+
+def vsa_gated_scatter(inverse, fine_bits, gate_bits, coarse):
+    inverse = np.ascontiguousarray(inverse, np.int32)
+    fine = np.ascontiguousarray(fine_bits, np.uint16)
+    gate = np.ascontiguousarray(gate_bits, np.uint16)
+    width = fine.shape[1]
+    out = np.zeros((len(inverse), width), np.uint16)
+    lib().h3o_vsa_gated_scatter(inverse, len(inverse), width, fine, gate,
+                                np.ascontiguousarray(coarse, np.float32), out)
+    return out
+
+
+def vsa_kmean(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(x.shape[1], np.float32)
+    lib().h3o_vsa_kmean(x, x.shape[0], x.shape[1], out)
+    return out
+
+
+def vsa_attention_f64(qc, qs, kc, ks, vt, tokens, cap, heads, routes, lengths, rows, threads=0):
+    """Token-major int8 codes qc/kc [cap][heads*128], scales [cap][heads], vt [heads*128][cap] f16
+    bits, routes [heads][blocks][blocks], lengths [blocks]; f64 [len(rows)][heads][128]."""
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros((len(rows), heads, 128), np.float64)
+    lib().h3o_vsa_attention_f64(np.ascontiguousarray(qc, np.int8).reshape(-1),
+                                np.ascontiguousarray(qs, np.float32).reshape(-1),
+                                np.ascontiguousarray(kc, np.int8).reshape(-1),
+                                np.ascontiguousarray(ks, np.float32).reshape(-1),
+                                np.ascontiguousarray(vt, np.uint16).reshape(-1), tokens, cap,
+                                heads, np.ascontiguousarray(routes, np.int32).reshape(-1),
+                                np.ascontiguousarray(lengths, np.int32), rows, len(rows), out,
+                                threads)
+    return out
