@@ -22,7 +22,7 @@ INCLUDE = HERE.parent / "include"
 OUT = HERE / "libh3attn.so"
 OBJ = HERE / "_build"
 SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "gemm.hip", "abi.cpp", "stack.cpp",
-           "tables.cpp"]
+           "tables.cpp", "vsa.hip", "vsa_host.cpp"]
 ARCH = "gfx950"
 
 

@@ -5,6 +5,7 @@
 // kernel's config.decl ranges bound its specialisation (kernels/*.loom). A failing check
 // returns its status, records a message for h3_last_error(), and launches nothing.
 #include <cstdarg>
+#include <initializer_list>
 #include <cstdio>
 #include <string>
 
@@ -123,13 +124,15 @@ int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
 }
 
 // Operand layouts of the attention kernels (attention.hip's modes).
-enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2, kModeTokenI4Skip = 3 };
+enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2, kModeTokenI4Skip = 3, kModeTokenI8Vsa = 4 };
 
 int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
                      uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
-                     h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f) {
+                     h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f,
+                     h3_view routes = {}, h3_view lengths = {}) {
   const bool head_major = mode == kModeHeadI8;
-  const size_t code_div = mode >= kModeTokenI4 ? 2 : 1;  // int4: half a byte per channel
+  const bool vsa = mode == kModeTokenI8Vsa;
+  const size_t code_div = (mode == kModeTokenI4 || mode == kModeTokenI4Skip) ? 2 : 1;
   if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
   // kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17
   if (!in_range(cfg->q_stride, 128, 32768, 128))
@@ -179,6 +182,27 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   h3_view views[6] = {qi, qs, ki, ks, vt, out};
   int st = check_bindings(stage, views, need, 6);
   if (st) return st;
+  if (vsa) {
+    // kernels/vsa_attention_8.loom:145-150: blocks = tokens / 64, routes [heads][blocks][blocks]
+    // i32, lengths [blocks] i32. Whole cubes only: tokens is the padded row count.
+    if (cfg->tokens % 64 != 0 || cfg->tokens / 64 > 16384)
+      return set_error(H3_ERR_CONFIG, "%s: tokens %u is not 64 * blocks with blocks <= 16384",
+                       stage, cfg->tokens);
+    const size_t blocks = cfg->tokens / 64;
+    h3_view rv[2] = {routes, lengths};
+    size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
+    if ((st = check_bindings(stage, rv, rneed, 2))) return st;
+    if ((st = device_ready(stage))) return st;
+    return launched(stage, launch_attention_vsa(*cfg, token_count, heads,
+                                                static_cast<const int32_t*>(qi.ptr),
+                                                static_cast<const float*>(qs.ptr),
+                                                static_cast<const int32_t*>(ki.ptr),
+                                                static_cast<const float*>(ks.ptr),
+                                                static_cast<const uint16_t*>(vt.ptr),
+                                                static_cast<uint16_t*>(out.ptr),
+                                                static_cast<const int32_t*>(routes.ptr),
+                                                static_cast<const int32_t*>(lengths.ptr), stream));
+  }
   if ((st = device_ready(stage))) return st;
   return launched(stage, launch_attention(*cfg, mode, skip_tau, token_count, heads,
                                           static_cast<const int32_t*>(qi.ptr),
@@ -187,6 +211,43 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
                                           static_cast<const float*>(ks.ptr),
                                           static_cast<const uint16_t*>(vt.ptr),
                                           static_cast<uint16_t*>(out.ptr), stream));
+}
+
+// kernels/vsa_ops.loom:3-9 (h3.vsa.*), plus the relations src/vsa/device.rs:63-77 builds the
+// config with: padded = 64 * blocks, width = 128 * heads, prefix <= blocks.
+int check_vsa_cfg(const char* stage, const h3_vsa_cfg* cfg) {
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  if (!in_range(cfg->tokens, 1, 1048576))
+    return set_error(H3_ERR_CONFIG, "%s: tokens %u outside [1, 1048576]", stage, cfg->tokens);
+  if (!in_range(cfg->padded, 64, 1048576, 64))
+    return set_error(H3_ERR_CONFIG, "%s: padded %u outside [64, 1048576] step 64", stage,
+                     cfg->padded);
+  if (!in_range(cfg->width, 128, 32768, 128))
+    return set_error(H3_ERR_CONFIG, "%s: width %u outside [128, 32768] step 128", stage,
+                     cfg->width);
+  if (!in_range(cfg->blocks, 1, 16384) || cfg->padded != 64 * cfg->blocks)
+    return set_error(H3_ERR_CONFIG, "%s: blocks %u outside [1, 16384] or not padded/64 (%u)",
+                     stage, cfg->blocks, cfg->padded / 64);
+  if (!in_range(cfg->heads, 1, 256) || cfg->width != 128 * cfg->heads)
+    return set_error(H3_ERR_CONFIG, "%s: heads %u outside [1, 256] or not width/128", stage,
+                     cfg->heads);
+  if (cfg->prefix > cfg->blocks)
+    return set_error(H3_ERR_CONFIG, "%s: prefix %u exceeds blocks %u", stage, cfg->prefix,
+                     cfg->blocks);
+  if (cfg->topk > 16384)
+    return set_error(H3_ERR_CONFIG, "%s: topk %u outside [0, 16384]", stage, cfg->topk);
+  return H3_OK;
+}
+
+// The row kernels move 16 bytes (eight f16 channels) per access.
+int check_aligned16(const char* stage, std::initializer_list<h3_view> views) {
+  int i = 0;
+  for (const h3_view& v : views) {
+    if (reinterpret_cast<uintptr_t>(v.ptr) % 16 != 0)
+      return set_error(H3_ERR_ARGUMENT, "%s: binding %d is not 16-byte aligned", stage, i);
+    ++i;
+  }
+  return H3_OK;
 }
 
 int transpose_common(const char* stage, const h3_transpose_cfg* cfg, uint32_t launch_rows,
@@ -475,6 +536,156 @@ int h3_attention_i4qks(const h3_attention_skip_cfg* cfg, uint32_t token_count, u
   return attention_common(stage, &base, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI4Skip,
                           cfg->skip_tau);
+}
+
+// ---------------------------------------------------------------- VSA (kernels/vsa_ops.loom)
+
+int h3_vsa_gather(const h3_vsa_cfg* cfg, h3_view src, h3_view x, h3_view y, h3_stream stream) {
+  const char* stage = "VSA gather";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t n = cfg->padded, t = cfg->tokens, w = cfg->width;
+  h3_view views[3] = {src, x, y};
+  size_t need[3] = {n * 4, t * w * 2, n * w * 2};  // src/vsa/device.rs:216-225
+  if ((st = check_bindings(stage, views, need, 3))) return st;
+  if ((st = check_aligned16(stage, {x, y}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_gather(cfg->tokens, cfg->padded, cfg->width,
+                                           static_cast<const int32_t*>(src.ptr),
+                                           static_cast<const uint16_t*>(x.ptr),
+                                           static_cast<uint16_t*>(y.ptr),
+                                           reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_scatter(const h3_vsa_cfg* cfg, h3_view inverse, h3_view x, h3_view y,
+                   h3_stream stream) {
+  const char* stage = "VSA scatter";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t n = cfg->padded, t = cfg->tokens, w = cfg->width;
+  h3_view views[3] = {inverse, x, y};
+  size_t need[3] = {t * 4, n * w * 2, t * w * 2};  // src/vsa/device.rs:436-445
+  if ((st = check_bindings(stage, views, need, 3))) return st;
+  if ((st = check_aligned16(stage, {x, y}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_scatter(cfg->tokens, cfg->padded, cfg->width,
+                                            static_cast<const int32_t*>(inverse.ptr),
+                                            static_cast<const uint16_t*>(x.ptr),
+                                            static_cast<uint16_t*>(y.ptr),
+                                            reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_pool(const h3_vsa_cfg* cfg, h3_view lengths, h3_view x, h3_view means,
+                h3_stream stream) {
+  const char* stage = "VSA pool";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t n = cfg->padded, b = cfg->blocks, w = cfg->width;
+  h3_view views[3] = {lengths, x, means};
+  size_t need[3] = {b * 4, n * w * 2, b * w * 4};  // src/vsa/device.rs:227-238
+  if ((st = check_bindings(stage, views, need, 3))) return st;
+  if ((st = check_aligned16(stage, {x, means}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_pool(cfg->blocks, cfg->width,
+                                         static_cast<const int32_t*>(lengths.ptr),
+                                         static_cast<const uint16_t*>(x.ptr),
+                                         static_cast<float*>(means.ptr),
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_scores(const h3_vsa_cfg* cfg, h3_view qm, h3_view km, h3_view scores,
+                  h3_stream stream) {
+  const char* stage = "VSA block scores";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t b = cfg->blocks, w = cfg->width, h = cfg->heads;
+  h3_view views[3] = {qm, km, scores};
+  size_t need[3] = {b * w * 4, b * w * 4, h * b * b * 4};  // src/vsa/device.rs:240-253
+  if ((st = check_bindings(stage, views, need, 3))) return st;
+  if ((st = check_aligned16(stage, {qm, km}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_scores(cfg->blocks, cfg->heads,
+                                           static_cast<const float*>(qm.ptr),
+                                           static_cast<const float*>(km.ptr),
+                                           static_cast<float*>(scores.ptr),
+                                           reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_route(const h3_vsa_cfg* cfg, h3_view scores, h3_view routes, h3_stream stream) {
+  const char* stage = "VSA route";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t b = cfg->blocks, h = cfg->heads;
+  h3_view views[2] = {scores, routes};
+  size_t need[2] = {h * b * b * 4, h * b * b * 4};  // src/vsa/device.rs:254-263
+  if ((st = check_bindings(stage, views, need, 2))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_route(cfg->blocks, cfg->heads, cfg->prefix, cfg->topk,
+                                          static_cast<const float*>(scores.ptr),
+                                          static_cast<int32_t*>(routes.ptr),
+                                          reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_coarse(const h3_vsa_cfg* cfg, h3_view scores, h3_view vm, h3_view coarse,
+                  h3_stream stream) {
+  const char* stage = "VSA coarse attention";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t b = cfg->blocks, w = cfg->width, h = cfg->heads;
+  h3_view views[3] = {scores, vm, coarse};
+  size_t need[3] = {h * b * b * 4, b * w * 4, b * w * 4};  // src/vsa/device.rs:384-398
+  if ((st = check_bindings(stage, views, need, 3))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_coarse(cfg->blocks, cfg->heads,
+                                           static_cast<const float*>(scores.ptr),
+                                           static_cast<const float*>(vm.ptr),
+                                           static_cast<float*>(coarse.ptr),
+                                           reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_gated_scatter(const h3_vsa_cfg* cfg, h3_view inverse, h3_view fine, h3_view gate,
+                         h3_view coarse, h3_view out, h3_stream stream) {
+  const char* stage = "VSA gated scatter";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t n = cfg->padded, t = cfg->tokens, b = cfg->blocks, w = cfg->width;
+  h3_view views[5] = {inverse, fine, gate, coarse, out};
+  size_t need[5] = {t * 4, n * w * 2, t * w * 2, b * w * 4, t * w * 2};  // device.rs:399-433
+  if ((st = check_bindings(stage, views, need, 5))) return st;
+  if ((st = check_aligned16(stage, {fine, gate, coarse, out}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_gated_scatter(cfg->tokens, cfg->padded, cfg->width,
+                                                  static_cast<const int32_t*>(inverse.ptr),
+                                                  static_cast<const uint16_t*>(fine.ptr),
+                                                  static_cast<const uint16_t*>(gate.ptr),
+                                                  static_cast<const float*>(coarse.ptr),
+                                                  static_cast<uint16_t*>(out.ptr),
+                                                  reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_stream stream) {
+  const char* stage = "VSA statistics";
+  // kernels/vsa_kmean.loom:5, 18
+  if (!in_range(width, 128, 65536, 128))
+    return set_error(H3_ERR_CONFIG, "%s: width %u outside [128, 65536] step 128", stage, width);
+  if (!in_range(tokens, 1, 1048576))
+    return set_error(H3_ERR_ARGUMENT, "%s: tokens %u outside [1, 1048576]", stage, tokens);
+  h3_view views[2] = {x, mean};
+  size_t need[2] = {(size_t)tokens * width * 4, (size_t)width * 4};  // device.rs:334-346
+  int st = check_bindings(stage, views, need, 2);
+  if (st) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_kmean(tokens, width, static_cast<const float*>(x.ptr),
+                                          static_cast<float*>(mean.ptr),
+                                          reinterpret_cast<hipStream_t>(stream)));
+}
+
+int h3_vsa_attention_i8(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                        h3_view routes, h3_view lengths, h3_stream stream) {
+  return attention_common("VSA attention", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI8Vsa, 0.0f, routes,
+                          lengths);
 }
 
 }  // extern "C"

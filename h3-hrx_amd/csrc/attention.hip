@@ -70,7 +70,9 @@ constexpr int kSRows = kKeys / kWaves;                      // scale rows stored
 // Operand layouts: int8 codes token-major (attention_i8qk_*) or head-major (attention_i8qkhm_*),
 // and int4 codes token-major (attention_i4qk_*, eight codes per word, low nibble first).
 // kTokenI4Skip is the int4 kernel with the tile skip of attention_i4qks_* (a threshold tau).
-enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2, kTokenI4Skip = 3 };
+// kTokenI8Vsa is the int8 token-major kernel walking only the key cubes that the VSA routes
+// keep (vsa_attention_8), see k_attention_vsa.
+enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2, kTokenI4Skip = 3, kTokenI8Vsa = 4 };
 constexpr bool isI4(int mode) { return mode == kTokenI4 || mode == kTokenI4Skip; }
 constexpr int kI4RowBytes = 64;                             // int4 K tile rows in LDS
 constexpr int kKRowsOf(int mode) { return isI4(mode) ? kKeys * kI4RowBytes : kKRows; }
@@ -114,6 +116,9 @@ struct Args {
   uint32_t total;      // q_blocks * heads
   uint32_t per_xcd;    // ceil(total / 8)
   float neg_tau;       // tile skip (kTokenI4Skip): -tau * log2(e)
+  const int32_t* routes;   // kTokenI8Vsa: [head_limit][blocks][blocks], nonzero = kept
+  const int32_t* lengths;  // kTokenI8Vsa: live keys of each 64-key cube
+  uint32_t blocks;         // kTokenI8Vsa: tokens / 64
 };
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
@@ -172,12 +177,14 @@ __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane)
 
 // LDS-DMA of K tile k0 (rows past the sequence load as zero) into stage `kst`, and the load of
 // its scales into a register.
+// live_keys >= 0 overrides the keys of the tile that are read (the rest load as zero).
 template <int kMode>
 __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32_t kv_head,
-                                         uint32_t k0, char* kst) {
+                                         uint32_t k0, char* kst, int live_keys = -1) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
   constexpr uint32_t kCodeBytes = isI4(kMode) ? 64 : 128;  // code bytes per (key, head)
-  const uint32_t live = a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
+  const uint32_t live = live_keys >= 0 ? (uint32_t)live_keys
+                        : a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
   const char* base;
   uint32_t bytes;
   const float* sbase;
@@ -223,6 +230,18 @@ __device__ __forceinline__ void store_scales(char* kst, const Stager& sg, float 
     float* sc = reinterpret_cast<float*>(kst + kKRowsOf(kMode));
     sc[sg.srow] = ks;
     sc[kKeys + sg.srow] = -(kMagic * ks);
+  }
+}
+
+// The same for a tile whose keys from `live` on are dead: their pair is (ks, -inf), so the
+// dequantized score acc*ks - inf is -inf and its probability exp2(-inf) is 0. The mask costs
+// nothing in the key loop.
+__device__ __forceinline__ void store_scales_live(char* kst, const Stager& sg, float ks,
+                                                  uint32_t live) {
+  if ((threadIdx.x & 63) < kSRows) {
+    float* sc = reinterpret_cast<float*>(kst + kKRows);
+    sc[sg.srow] = ks;
+    sc[kKeys + sg.srow] = swap23(sg.srow) < live ? -(kMagic * ks) : -INFINITY;
   }
 }
 
@@ -392,13 +411,16 @@ __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4],
 //   kst    LDS stage of K(j+1) (unused when !kNext), vst  LDS stage of V(j)
 //   u      in: tile j's dequantized scores; out: tile j+1's
 //   knext0 first key of tile j+1
-//   skip   (kTokenI4Skip only, wave-uniform) tile j is skipped: no probabilities and no PV;
-//          tile j+1 is still prepared
+//   skip   (kTokenI4Skip and kTokenI8Vsa only, wave-uniform) tile j is skipped: no
+//          probabilities and no PV; tile j+1 is still prepared
+//   qk     (kTokenI8Vsa only, wave-uniform) tile j+1 is prepared: QK, dequant and max
 template <int kMode, bool kNext, bool kMaskNext, bool kMaskCur>
 __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i (&qop)[4],
                                      float qsl, State& st, float (&u)[2][16], int n, int half,
-                                     uint32_t knext0, uint32_t tokens, bool skip = false) {
-  const bool do_pv = kMode != kTokenI4Skip || !skip;
+                                     uint32_t knext0, uint32_t tokens, bool skip = false,
+                                     bool qk = true) {
+  const bool do_pv = (kMode != kTokenI4Skip && kMode != kTokenI8Vsa) || !skip;
+  const bool do_qk = kNext && (kMode != kTokenI8Vsa || qk);
   // The rescale owed by the last raise of m, now that PV(j-1) has accumulated.
   if (__any(st.alpha != 1.0f)) {
 #pragma unroll
@@ -424,7 +446,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
 
   // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
   constexpr bool kI4 = isI4(kMode);
-  if (kNext) {
+  if (do_qk) {
     if constexpr (kI4) {  // chunks 0..3 now, 4..7 two MFMAs ahead of their use
       k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 0, kop[0], kop[2]);
       k_pair_i4(kst, n, half, (n >> 2) & 3, 1, 0, kop[1], kop[3]);
@@ -438,11 +460,11 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   for (int c = 0; c < 8; ++c) {
     const int bb = c & 1, dc = c >> 1;
     if constexpr (kI4) {
-      if (kNext && c == 2) {
+      if (do_qk && c == 2) {
         k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 1, kop[4], kop[6]);
         k_pair_i4(kst, n, half, (n >> 2) & 3, 1, 1, kop[5], kop[7]);
       }
-    } else if (kNext && c + kPf < 8) {
+    } else if (do_qk && c + kPf < 8) {
       const int w = c + kPf;
       kop[w] = *reinterpret_cast<const v4i*>(krow + (w & 1) * 32 * kRowBytes + chunk_off(w >> 1, half, sw));
     }
@@ -450,7 +472,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
       const int w = c - (8 - kPf);
       vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
-    if (kNext)
+    if (do_qk)
       s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
     if (do_pv) exp_pair<kMaskCur>(u, 0, 2 * c, qsl, negm, pb, la);
     H3_CHUNK_END();
@@ -465,7 +487,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
       const int w = c + kPf;
       vop[w] = *reinterpret_cast<const v8h*>(vrow + (w & 3) * 32 * kRowBytes + chunk_off(w >> 2, half, sw));
     }
-    if (kNext && c >= 6 - kSPf && c < 14 - kSPf) {  // scales of dequant quarter q, kSPf ahead
+    if (do_qk && c >= 6 - kSPf && c < 14 - kSPf) {  // scales of dequant quarter q, kSPf ahead
       const int q = c - (6 - kSPf), kb = 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
       k4[q] = *reinterpret_cast<const float4*>(kss + kb);
       c4[q] = *reinterpret_cast<const float4*>(kss + kKeys + kb);
@@ -474,18 +496,18 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
       st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[g], st.acc[db], 0, 0, 0);
       if (c < 8) exp_pair<kMaskCur>(u, 1, 2 * c, qsl, negm, pb, lb);
     }
-    if (kNext && c >= 6 && c < 14) {
+    if (do_qk && c >= 6 && c < 14) {
       const int q = c - 6, bb = q >> 2, i = q & 3;
       dequant4<kMaskNext>(s, bb, i, k4[q], c4[q], u, tmax, knext0 + slot_key(bb, i, half),
                           tokens);
     }
-    if (kNext && c == 14) {  // under the last MFMAs: tile j's sums are complete
+    if (do_qk && c == 14) {  // under the last MFMAs: tile j's sums are complete
       st.l += la + lb;
       raise_max(tmax, qsl, st);
     }
     H3_CHUNK_END();
   }
-  if (!kNext) st.l += la + lb;
+  if (!do_qk) st.l += la + lb;
 }
 
 template <int kMode>
@@ -643,6 +665,184 @@ void k_attention(Args a) {
   }
 }
 
+// ---------------------------------------------------------------- VSA block-sparse attention
+//
+// kernels/vsa_attention_8.loom: query cube b (64 queries in the gathered layout) attends to the
+// keys of every key cube kb with routes[head][b][kb] != 0, and within a cube only to its first
+// lengths[kb] keys. A workgroup here is two query cubes (waves 0-1: cube 2qb, waves 2-3: cube
+// 2qb + 1), and a key tile is one cube. Per run of the key loop the workgroup scans the two
+// route rows into an LDS list of the cubes that either query cube keeps (in ascending order,
+// up to kListMax of them per run), each entry carrying which of the two keeps it and its live
+// length. The pipeline of k_attention then walks that list: the K/V^T tiles of a listed cube
+// are staged for the whole workgroup, and a wave whose query cube does not keep the cube skips
+// its QK, softmax and PV (wave-uniform branches), so every wave computes exactly its own
+// routes. Dead keys are masked through their staged scale pair (store_scales_live).
+constexpr int kListMax = 1024;           // list entries per run of the key loop
+constexpr uint32_t kEntryCube = 0x3fffu;  // entry: cube (14 bits) | keep flags << 14 | live << 16
+
+__device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_attention_vsa(Args a) {
+  constexpr int kMode = kTokenI8Vsa;
+  constexpr int kWaitPrevStep = kWaitPrevStepOf(kMode);
+  __shared__ __attribute__((aligned(16))) char k0s[kKStage];
+  __shared__ __attribute__((aligned(16))) char k1s[kKStage];
+  __shared__ __attribute__((aligned(16))) char k2s[kKStage];
+  __shared__ __attribute__((aligned(16))) char v0s[kVStage];
+  __shared__ __attribute__((aligned(16))) char v1s[kVStage];
+  __shared__ __attribute__((aligned(16))) char v2s[kVStage];
+  __shared__ uint32_t list[kListMax];
+  __shared__ uint32_t wave_counts[kWaves];
+
+  const uint32_t b = blockIdx.x;
+  const uint32_t logical = (b & 7u) * a.per_xcd + (b >> 3);
+  if (logical >= a.total) return;
+  const uint32_t head_y = logical / a.q_blocks;
+  const uint32_t qb = logical % a.q_blocks;
+  const uint32_t kv_head = head_y % a.kv_head_limit;
+  const uint32_t head = kv_head % a.head_limit;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31;
+  const int half = lane >> 5;
+  const uint32_t tiles32 = (a.tokens + 31) / 32;
+  const uint32_t q_tile = qb * kWaves + wave;
+  const uint32_t q_tile_c = q_tile < tiles32 ? q_tile : tiles32 - 1;
+  const uint32_t q = q_tile_c * kQueriesPerWave + n;
+  const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
+  const uint32_t my_flag = 1u << (14 + (wave >> 1));  // keep flag of this wave's query cube
+
+  const Stager sg = make_stager<kMode>(a, wave, lane);
+  v4i qop[4];
+  {
+    const int32_t* src = a.qi + (size_t)q_read * (a.q_row / 4) + head * 32;
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) qop[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
+  }
+  const float qsl = a.qs[(size_t)q_read * a.head_limit + head] * kLog2e;
+
+  State st;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
+  st.m = -1.0e30f;
+  st.l = 0.0f;
+  st.alpha = 1.0f;
+  float u[2][16] = {};
+
+  const uint32_t cube0 = 2 * qb;
+  const bool has1 = cube0 + 1 < a.blocks;
+  const int32_t* route0 = a.routes + ((size_t)head * a.blocks + cube0) * a.blocks;
+  const int32_t* route1 = route0 + a.blocks;
+  auto cube_of = [](uint32_t e) { return e & kEntryCube; };
+  auto live_of = [](uint32_t e) { return (int)(e >> 16); };
+
+  uint32_t scan = 0;  // first key cube not yet listed
+  while (scan < a.blocks) {
+    // ---- list the kept cubes from `scan` on, kThreads cubes per pass, while they fit
+    uint32_t count = 0;
+    while (scan < a.blocks) {
+      const uint32_t kb = scan + threadIdx.x;
+      uint32_t f = 0;
+      if (kb < a.blocks) f = (route0[kb] != 0 ? 1u : 0u) | (has1 && route1[kb] != 0 ? 2u : 0u);
+      const uint64_t ball = __ballot(f != 0);
+      if (lane == 0) wave_counts[wave] = (uint32_t)__popcll(ball);
+      __syncthreads();
+      uint32_t before = 0, pass_total = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const uint32_t c = wave_counts[w];
+        before += w < wave ? c : 0u;
+        pass_total += c;
+      }
+      if (count + pass_total > (uint32_t)kListMax) {  // the same decision in every wave
+        __syncthreads();
+        break;
+      }
+      if (f) {
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
+        const int len = a.lengths[kb];
+        const uint32_t live = len < 0 ? 0u : len > kKeys ? (uint32_t)kKeys : (uint32_t)len;
+        list[count + before + rank] = kb | (f << 14) | (live << 16);
+      }
+      count += pass_total;
+      scan += kThreads;
+      __syncthreads();
+    }
+    if (count == 0) continue;
+
+    // ---- the pipeline of k_attention over list[0 .. count): tile t is cube cube_of(list[t])
+    auto entry = [&](uint32_t t) { return t < count ? rfl(list[t]) : 0u; };
+    uint32_t e0 = entry(0), e1 = entry(1), e2 = entry(2), e3 = entry(3);
+    float ks0 = stage_k<kMode>(a, sg, kv_head, cube_of(e0) * kKeys, k0s, live_of(e0));
+    float ks1 = stage_k<kMode>(a, sg, kv_head, cube_of(e1) * kKeys, k1s, live_of(e1));
+    float ks_held = stage_k<kMode>(a, sg, kv_head, cube_of(e2) * kKeys, k2s, live_of(e2));
+    stage_v(a, sg, kv_head, cube_of(e0) * kKeys, v0s);
+    stage_v(a, sg, kv_head, cube_of(e1) * kKeys, v1s);
+    store_scales_live(k0s, sg, ks0, live_of(e0));
+    store_scales_live(k1s, sg, ks1, live_of(e1));
+    step_barrier<kWaitAll>();
+    if (e0 & my_flag) first_tile<kMode, false>(k0s, qop, qsl, st, u, n, half, a.tokens);
+    step_barrier<kWaitAll>();
+
+    // One step j: K(j+3) -> kc, V(j+2) -> vn2; QK(j+1) from kn if this wave keeps cube j+1,
+    // PV(j) from vc if it keeps cube j; then the scales of K(j+2) into kn2.
+#define H3_VSA_STEP(kc, kn, kn2, vc, vn2)                                                      \
+  {                                                                                          \
+    const float ks_new = stage_k<kMode>(a, sg, kv_head, cube_of(e3) * kKeys, kc, live_of(e3)); \
+    stage_v(a, sg, kv_head, cube_of(e2) * kKeys, vn2);                                       \
+    const uint32_t e4 = entry(j + 4);                                                        \
+    step<kMode, true, false, false>(kn, vc, qop, qsl, st, u, n, half, 0, a.tokens,           \
+                                    (e0 & my_flag) == 0, (e1 & my_flag) != 0);               \
+    store_scales_live(kn2, sg, ks_held, live_of(e2));                                        \
+    ks_held = ks_new;                                                                        \
+    e0 = e1;                                                                                 \
+    e1 = e2;                                                                                 \
+    e2 = e3;                                                                                 \
+    e3 = e4;                                                                                 \
+    step_barrier<kWaitPrevStep>();                                                           \
+    ++j;                                                                                     \
+  }
+    const uint32_t steady = count - 1;
+    uint32_t j = 0;
+    for (; j + 3 <= steady;) {
+      H3_VSA_STEP(k0s, k1s, k2s, v0s, v2s)
+      H3_VSA_STEP(k1s, k2s, k0s, v1s, v0s)
+      H3_VSA_STEP(k2s, k0s, k1s, v2s, v1s)
+    }
+    if (j < steady) H3_VSA_STEP(k0s, k1s, k2s, v0s, v2s)
+    if (j < steady) H3_VSA_STEP(k1s, k2s, k0s, v1s, v0s)
+#undef H3_VSA_STEP
+    {  // the last tile's PV (stage j % 3)
+      const uint32_t r = j % 3;
+      const char* vlast = r == 0 ? v0s : r == 1 ? v1s : v2s;
+      step<kMode, false, false, false>(nullptr, vlast, qop, qsl, st, u, n, half, 0, a.tokens,
+                                       (e0 & my_flag) == 0, false);
+    }
+    step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
+  }
+
+  // ---- normalise and store rows < token_count
+  const float l_tot = st.l + __shfl_xor(st.l, 32);
+  const float inv = 1.0f / l_tot;
+  if (q_tile < tiles32 && q < a.token_count && q < a.tokens) {
+    uint16_t* dst = a.out + (size_t)q * a.out_stride + head * 128;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
+                 (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
+        *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
@@ -679,6 +879,37 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
     hipLaunchKernelGGL(k_attention<kTokenI4Skip>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
+                                uint32_t heads, const int32_t* qi, const float* qs,
+                                const int32_t* ki, const float* ks, const uint16_t* vt,
+                                uint16_t* out, const int32_t* routes, const int32_t* lengths,
+                                hipStream_t stream) {
+  Args a{};
+  a.qi = qi;
+  a.qs = qs;
+  a.ki = ki;
+  a.ks = ks;
+  a.vt = vt;
+  a.out = out;
+  a.tokens = cfg.tokens;
+  a.token_count = token_count;
+  a.capacity = cfg.token_capacity;
+  a.q_row = cfg.q_stride;
+  a.kv_bytes = cfg.kv_stride;
+  a.out_stride = cfg.out_stride;
+  a.q_blocks = (token_count + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  a.heads = heads;
+  a.kv_head_limit = cfg.kv_stride / 128;
+  a.head_limit = cfg.out_stride / 128;
+  a.total = a.q_blocks * heads;
+  a.per_xcd = (a.total + 7) / 8;
+  a.routes = routes;
+  a.lengths = lengths;
+  a.blocks = cfg.tokens / kKeys;
+  hipLaunchKernelGGL(k_attention_vsa, dim3(a.per_xcd * 8), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -79,4 +79,31 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             const float* ks, const uint16_t* vt, uint16_t* out,
                             hipStream_t stream);
 
+// kTokenI8Vsa: the int8 token-major attention over the cubes `routes` keeps (attention.hip)
+hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
+                                uint32_t heads, const int32_t* qi, const float* qs,
+                                const int32_t* ki, const float* ks, const uint16_t* vt,
+                                uint16_t* out, const int32_t* routes, const int32_t* lengths,
+                                hipStream_t stream);
+// VSA operations (vsa.hip)
+hipError_t launch_vsa_gather(uint32_t tokens, uint32_t padded, uint32_t width, const int32_t* src,
+                             const uint16_t* x, uint16_t* y, hipStream_t stream);
+hipError_t launch_vsa_scatter(uint32_t tokens, uint32_t padded, uint32_t width,
+                              const int32_t* inverse, const uint16_t* x, uint16_t* y,
+                              hipStream_t stream);
+hipError_t launch_vsa_pool(uint32_t blocks, uint32_t width, const int32_t* lengths,
+                           const uint16_t* x, float* means, hipStream_t stream);
+hipError_t launch_vsa_scores(uint32_t blocks, uint32_t heads, const float* qm, const float* km,
+                             float* scores, hipStream_t stream);
+hipError_t launch_vsa_route(uint32_t blocks, uint32_t heads, uint32_t prefix, uint32_t topk,
+                            const float* scores, int32_t* routes, hipStream_t stream);
+hipError_t launch_vsa_coarse(uint32_t blocks, uint32_t heads, const float* scores,
+                             const float* vm, float* coarse, hipStream_t stream);
+hipError_t launch_vsa_gated_scatter(uint32_t tokens, uint32_t padded, uint32_t width,
+                                    const int32_t* inverse, const uint16_t* fine,
+                                    const uint16_t* gate, const float* coarse, uint16_t* out,
+                                    hipStream_t stream);
+hipError_t launch_vsa_kmean(uint32_t tokens, uint32_t width, const float* x, float* mean,
+                            hipStream_t stream);
+
 }  // namespace h3

@@ -126,6 +126,40 @@ class IntQk(ctypes.Structure):
     ]
 
 
+class VsaCfg(ctypes.Structure):
+    """h3.vsa.* (kernels/vsa_ops.loom:3-9)."""
+    _fields_ = [
+        ("tokens", ctypes.c_uint32),
+        ("padded", ctypes.c_uint32),
+        ("width", ctypes.c_uint32),
+        ("blocks", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("prefix", ctypes.c_uint32),
+        ("topk", ctypes.c_uint32),
+    ]
+
+
+class VsaSegment(ctypes.Structure):
+    _fields_ = [("row0", ctypes.c_uint32), ("rows", ctypes.c_uint32)]
+
+
+class VsaOptionsC(ctypes.Structure):
+    _fields_ = [
+        ("keep_percent", ctypes.c_double),
+        ("start", ctypes.c_double),
+        ("end", ctypes.c_double),
+        ("min_tokens", ctypes.c_uint32),
+        ("dense_blocks", ctypes.POINTER(ctypes.c_uint32)),
+        ("n_dense_blocks", ctypes.c_uint32),
+    ]
+
+
+class VsaBuffers(ctypes.Structure):
+    _fields_ = [(name, View) for name in (
+        "src", "inverse", "lengths", "q", "k", "v", "qm", "km", "scores", "routes", "qi", "ki",
+        "qs", "ks", "vt", "out", "kmean")] + [("cfg", VsaCfg), ("attention", AttentionCfg)]
+
+
 # (name, argtypes) of every exported entry point; restype is int unless noted.
 _P = ctypes.POINTER
 _S = ctypes.c_void_p
@@ -164,6 +198,37 @@ SIGNATURES = {
     "h3_attention_i4qks": (
         [_P(AttentionSkipCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          _S], ctypes.c_int),
+    "h3_vsa_gather": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
+    "h3_vsa_scatter": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
+    "h3_vsa_pool": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
+    "h3_vsa_scores": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
+    "h3_vsa_route": ([_P(VsaCfg), View, View, _S], ctypes.c_int),
+    "h3_vsa_coarse": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
+    "h3_vsa_gated_scatter": ([_P(VsaCfg), View, View, View, View, View, _S], ctypes.c_int),
+    "h3_vsa_kmean": ([ctypes.c_uint32, ctypes.c_uint32, View, View, _S], ctypes.c_int),
+    "h3_vsa_attention_i8": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         View, View, _S], ctypes.c_int),
+    "h3_vsa_plan_blocks": (
+        [_P(VsaSegment), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+         _P(ctypes.c_uint32)], ctypes.c_int),
+    "h3_vsa_plan": (
+        [_P(VsaSegment), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+         ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _P(ctypes.c_uint32)],
+        ctypes.c_int),
+    "h3_vsa_validate": ([_P(VsaOptionsC), ctypes.c_uint32], ctypes.c_int),
+    "h3_vsa_topk": ([ctypes.c_double, ctypes.c_uint32], ctypes.c_uint32),
+    "h3_vsa_dense_reason": (
+        [_P(VsaOptionsC), ctypes.c_uint32, ctypes.c_float, ctypes.c_double], ctypes.c_char_p),
+    "h3_vsa_build": (
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+         ctypes.c_uint32, _P(VsaOptionsC), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p],
+        ctypes.c_int),
+    "h3_vsa_destroy": ([ctypes.c_void_p], None),
+    "h3_vsa_reset": ([ctypes.c_void_p, _S], ctypes.c_int),
+    "h3_vsa_attend": (
+        [ctypes.c_void_p, ctypes.c_uint32, View, View, View, View, View, _S], ctypes.c_int),
+    "h3_vsa_inspect": ([ctypes.c_void_p, ctypes.c_uint32, _P(VsaBuffers)], ctypes.c_int),
     "h3_capacity": ([ctypes.c_uint32, ctypes.c_int], ctypes.c_uint32),
     "h3_stack_build": ([_P(StackDims), ctypes.c_void_p], ctypes.c_int),
     "h3_stack_destroy": ([ctypes.c_void_p], None),
@@ -404,3 +469,137 @@ class Stack:
         ops = IntQk()
         check(lib().h3_stack_operands(self.handle, ctypes.byref(ops)))
         return ops
+
+
+# ------------------------------------------------------------------------- VSA (src/vsa.rs)
+
+def vsa_gather(cfg: VsaCfg, src, x, y, stream=None) -> None:
+    check(lib().h3_vsa_gather(ctypes.byref(cfg), view(src), view(x), view(y), stream_ptr(stream)))
+
+
+def vsa_scatter(cfg: VsaCfg, inverse, x, y, stream=None) -> None:
+    check(lib().h3_vsa_scatter(ctypes.byref(cfg), view(inverse), view(x), view(y),
+                               stream_ptr(stream)))
+
+
+def vsa_pool(cfg: VsaCfg, lengths, x, means, stream=None) -> None:
+    check(lib().h3_vsa_pool(ctypes.byref(cfg), view(lengths), view(x), view(means),
+                            stream_ptr(stream)))
+
+
+def vsa_scores(cfg: VsaCfg, qm, km, scores, stream=None) -> None:
+    check(lib().h3_vsa_scores(ctypes.byref(cfg), view(qm), view(km), view(scores),
+                              stream_ptr(stream)))
+
+
+def vsa_route(cfg: VsaCfg, scores, routes, stream=None) -> None:
+    check(lib().h3_vsa_route(ctypes.byref(cfg), view(scores), view(routes), stream_ptr(stream)))
+
+
+def vsa_coarse(cfg: VsaCfg, scores, vm, coarse, stream=None) -> None:
+    check(lib().h3_vsa_coarse(ctypes.byref(cfg), view(scores), view(vm), view(coarse),
+                              stream_ptr(stream)))
+
+
+def vsa_gated_scatter(cfg: VsaCfg, inverse, fine, gate, coarse, out, stream=None) -> None:
+    check(lib().h3_vsa_gated_scatter(ctypes.byref(cfg), view(inverse), view(fine), view(gate),
+                                     view(coarse), view(out), stream_ptr(stream)))
+
+
+def vsa_kmean(width: int, tokens: int, x, mean, stream=None) -> None:
+    check(lib().h3_vsa_kmean(width, tokens, view(x), view(mean), stream_ptr(stream)))
+
+
+def vsa_attention_i8(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                     routes, lengths, stream=None) -> None:
+    check(lib().h3_vsa_attention_i8(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                    view(ki), view(ks), view(vt), view(out), view(routes),
+                                    view(lengths), stream_ptr(stream)))
+
+
+class VsaOptions:
+    """VsaOptions (src/vsa.rs:11-31) with its defaults."""
+
+    def __init__(self, keep_percent=10.0, start=0.2, end=1.0, min_tokens=12288, dense_blocks=()):
+        self.keep_percent, self.start, self.end = float(keep_percent), float(start), float(end)
+        self.min_tokens = int(min_tokens)
+        self.dense_blocks = [int(b) for b in dense_blocks]
+
+    def c(self) -> VsaOptionsC:
+        arr = (ctypes.c_uint32 * max(1, len(self.dense_blocks)))(*self.dense_blocks)
+        opt = VsaOptionsC(self.keep_percent, self.start, self.end, self.min_tokens,
+                          ctypes.cast(arr, ctypes.POINTER(ctypes.c_uint32)), len(self.dense_blocks))
+        opt._keep = arr
+        return opt
+
+    def validate(self, attention_bits: int = 8) -> None:
+        check(lib().h3_vsa_validate(ctypes.byref(self.c()), attention_bits))
+
+    def topk(self, nonprefix: int) -> int:
+        return int(lib().h3_vsa_topk(self.keep_percent, nonprefix))
+
+    def dense_reason(self, tokens: int, sigma: float, shift: float):
+        r = lib().h3_vsa_dense_reason(ctypes.byref(self.c()), tokens, sigma, shift)
+        return None if r is None else r.decode()
+
+
+def vsa_plan(segments, seq_len: int, nt: int, nh: int, nw: int):
+    """Plan::new (src/vsa.rs:94-143): segments [(row0, rows)] of the prefix in order, then the
+    nt x nh x nw video grid at the end of the sequence. Returns numpy (src, inverse, lengths,
+    prefix_blocks)."""
+    import numpy as np
+
+    segs = (VsaSegment * max(1, len(segments)))(*[VsaSegment(a, b) for a, b in segments])
+    blocks = ctypes.c_uint32()
+    check(lib().h3_vsa_plan_blocks(segs, len(segments), nt, nh, nw, ctypes.byref(blocks)))
+    src = np.zeros(64 * blocks.value, np.int32)
+    inverse = np.zeros(max(1, seq_len), np.int32)
+    lengths = np.zeros(blocks.value, np.int32)
+    prefix = ctypes.c_uint32()
+    check(lib().h3_vsa_plan(segs, len(segments), seq_len, nt, nh, nw, src.ctypes.data,
+                            inverse.ctypes.data, lengths.ctypes.data, ctypes.byref(prefix)))
+    return src, inverse[:seq_len], lengths, prefix.value
+
+
+class Vsa:
+    """vsa::device::Runtime (src/vsa/device.rs) for INT8 attention: build once per plan, then
+    attend(layer, q, k, v, out, gate=None) per DiT block; reset() clears the per-layer K means."""
+
+    def __init__(self, src, inverse, lengths, prefix_blocks: int, heads: int,
+                 options: Optional[VsaOptions] = None, layers: int = 1):
+        import numpy as np
+
+        self.options = options or VsaOptions()
+        src = np.ascontiguousarray(src, np.int32)
+        inverse = np.ascontiguousarray(inverse, np.int32)
+        lengths = np.ascontiguousarray(lengths, np.int32)
+        handle = ctypes.c_void_p()
+        opt = self.options.c()
+        check(lib().h3_vsa_build(src.ctypes.data, inverse.ctypes.data, lengths.ctypes.data,
+                                 len(lengths), len(inverse), prefix_blocks, ctypes.byref(opt),
+                                 heads, layers, ctypes.byref(handle)))
+        self.handle = handle
+        self.layers = layers
+
+    def close(self) -> None:
+        if self.handle:
+            lib().h3_vsa_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self, stream=None) -> None:
+        check(lib().h3_vsa_reset(self.handle, stream_ptr(stream)))
+
+    def attend(self, layer: int, q, k, v, out, gate=None, stream=None) -> None:
+        check(lib().h3_vsa_attend(self.handle, layer, view(q), view(k), view(v), view(out),
+                                  view(gate), stream_ptr(stream)))
+
+    def buffers(self, layer: int = 0) -> VsaBuffers:
+        b = VsaBuffers()
+        check(lib().h3_vsa_inspect(self.handle, layer, ctypes.byref(b)))
+        return b

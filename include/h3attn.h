@@ -297,6 +297,148 @@ int h3_attention_i4qks(const h3_attention_skip_cfg *cfg, uint32_t token_count, u
                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                        h3_stream stream);
 
+/* ------------------------------------------------------------------ VSA (video sparse attention) */
+
+/* Config of h3.vsa.* (kernels/vsa_ops.loom:3-9), as src/vsa/device.rs:63-77 builds it:
+ *   tokens  [1, 1048576]: rows of the activations in sequence order
+ *   padded  multiple of 64 in [64, 1048576]: rows of the gathered layout, 64 * blocks
+ *   width   multiple of 128 in [128, 32768]: heads * 128
+ *   blocks  [1, 16384]: 64-row blocks of the plan (prefix tiles, then 4x4x4 video cubes)
+ *   heads   [1, 256]
+ *   prefix  [0, blocks]: the prefix blocks (text, references, audio), always attended
+ *   topk    [0, 16384]: non-prefix blocks each query block keeps beyond the forced ones
+ * The gathered layout holds block b in rows 64b..64b+63, its lengths[b] live rows first. f16
+ * activations, block means (f32) and the gated scatter's operands must be 16-byte aligned. */
+typedef struct {
+  uint32_t tokens;
+  uint32_t padded;
+  uint32_t width;
+  uint32_t blocks;
+  uint32_t heads;
+  uint32_t prefix;
+  uint32_t topk;
+} h3_vsa_cfg;
+
+/* h3_vsa_gather (vsa_ops.loom h3_vsa_gather): y[i] = x[src[i]] for 0 <= src[i] < tokens, else a
+ * zero row. src [padded] i32, x [tokens][width] f16, y [padded][width] f16. */
+int h3_vsa_gather(const h3_vsa_cfg *cfg, h3_view src, h3_view x, h3_view y, h3_stream stream);
+/* h3_vsa_scatter (vsa_ops.loom h3_vsa_scatter): y[r] = x[inverse[r]]. inverse [tokens] i32 (a
+ * value outside [0, padded) writes a zero row), x [padded][width], y [tokens][width] f16. */
+int h3_vsa_scatter(const h3_vsa_cfg *cfg, h3_view inverse, h3_view x, h3_view y,
+                   h3_stream stream);
+/* h3_vsa_pool (vsa_ops.loom h3_vsa_pool): means[b][c] = (sum_{j < lengths[b]} x[64b+j][c]) /
+ * lengths[b], a running f32 sum over the rows (bit-identical to the reference). lengths
+ * [blocks] i32 in [1, 64], x [padded][width] f16, means [blocks][width] f32. */
+int h3_vsa_pool(const h3_vsa_cfg *cfg, h3_view lengths, h3_view x, h3_view means,
+                h3_stream stream);
+/* h3_vsa_scores (vsa_ops.loom h3_vsa_scores): scores[h][q][j] = fma chain over d = 0..127 of
+ * qm[q][128h+d] * km[j][128h+d] (bit-identical). qm, km [blocks][width] f32, scores
+ * [heads][blocks][blocks] f32. */
+int h3_vsa_scores(const h3_vsa_cfg *cfg, h3_view qm, h3_view km, h3_view scores,
+                  h3_stream stream);
+/* h3_vsa_route (vsa_ops.loom h3_vsa_route): routes[h][q][j] = 1 when q < prefix, j < prefix or
+ * |q - j| <= 1; otherwise 1 when fewer than topk of the non-prefix scores of row q are strictly
+ * greater than scores[h][q][j], else 0. Exact (integer) result; computed per row by a radix
+ * select of the topk-th largest score instead of the reference's count per entry. */
+int h3_vsa_route(const h3_vsa_cfg *cfg, h3_view scores, h3_view routes, h3_stream stream);
+/* h3_vsa_coarse (vsa_ops.loom h3_vsa_coarse): coarse[q][128h+c] = sum_j softmax_j(scores[h][q]
+ * [j] / sqrt(128)) vm[j][128h+c], with the hardware exp (the reference's expf<afn>). scores
+ * [heads][blocks][blocks], vm and coarse [blocks][width] f32. */
+int h3_vsa_coarse(const h3_vsa_cfg *cfg, h3_view scores, h3_view vm, h3_view coarse,
+                  h3_stream stream);
+/* h3_vsa_gated_scatter (vsa_ops.loom h3_vsa_gated_scatter): out[r][c] = f16(fma(gate[r][c],
+ * coarse[inverse[r]/64][c], fine[inverse[r]][c])) (bit-identical). inverse [tokens], fine
+ * [padded][width] f16, gate [tokens][width] f16, coarse [blocks][width] f32, out [tokens][width]. */
+int h3_vsa_gated_scatter(const h3_vsa_cfg *cfg, h3_view inverse, h3_view fine, h3_view gate,
+                         h3_view coarse, h3_view out, h3_stream stream);
+/* h3_vsa_kmean (kernels/vsa_kmean.loom): mean[c] = (sum_t x[t][c]) / tokens, a running f32 sum
+ * (bit-identical). width multiple of 128 in [128, 65536]; x [tokens][width] f32, mean [width]. */
+int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_stream stream);
+/* h3_vsa_attention_i8 (kernels/vsa_attention_8.loom, h3_vsa_attention_8): h3_attention_i8qk over
+ * the gathered layout, where query row t (block t/64) of head h attends only to the keys
+ * 64kb + j with routes[h][t/64][kb] != 0 and j < lengths[kb]. cfg->tokens = padded (a multiple
+ * of 64, blocks = tokens/64 <= 16384), token operands as h3_attention_i8qk; routes
+ * [out_stride/128][blocks][blocks] i32, lengths [blocks] i32. qs must be positive (the quantizer's
+ * scales are). */
+int h3_vsa_attention_i8(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                        h3_view routes, h3_view lengths, h3_stream stream);
+
+/* ---- VSA host policy (src/vsa.rs), no device work */
+
+/* A prefix segment of the sequence: rows row0 .. row0+rows-1 (text, a reference, audio). */
+typedef struct {
+  uint32_t row0;
+  uint32_t rows;
+} h3_vsa_segment;
+
+/* Plan::new (src/vsa.rs:94-143) on a layout given as its prefix segments, in order, and its
+ * video grid of nt x nh x nw latent cells (nh = lat_h/2, nw = lat_w/2), which fills rows
+ * seq_len - nt*nh*nw + (t*nh + h)*nw + w. Each segment is cut into 64-row tiles (the last one
+ * padded with -1); the grid into 4x4x4 cubes in (t, h, w) order, row-major inside a cube.
+ * h3_vsa_plan_blocks gives the block count; h3_vsa_plan fills HOST arrays src [64*blocks],
+ * inverse [seq_len], lengths [blocks] and *prefix_blocks, and fails (H3_ERR_ARGUMENT) unless
+ * every row is covered exactly once (src/vsa.rs:137-140). */
+int h3_vsa_plan_blocks(const h3_vsa_segment *segments, uint32_t n_segments, uint32_t nt,
+                       uint32_t nh, uint32_t nw, uint32_t *blocks);
+int h3_vsa_plan(const h3_vsa_segment *segments, uint32_t n_segments, uint32_t seq_len,
+                uint32_t nt, uint32_t nh, uint32_t nw, int32_t *src, int32_t *inverse,
+                int32_t *lengths, uint32_t *prefix_blocks);
+
+/* VsaOptions (src/vsa.rs:11-31): keep_percent in (0, 100], 0 <= start <= end <= 1,
+ * min_tokens <= 2^20, dense_blocks: global DiT block indices (< 50) that always run dense. */
+typedef struct {
+  double keep_percent;
+  double start;
+  double end;
+  uint32_t min_tokens;
+  const uint32_t *dense_blocks;
+  uint32_t n_dense_blocks;
+} h3_vsa_options;
+
+/* VsaOptions::validate and AttentionPattern::validate (src/vsa.rs:33-52, 76-85): also refuses
+ * attention_bits == 4 ("VSA supports f16 or i8 attention, not i4"). */
+int h3_vsa_validate(const h3_vsa_options *options, uint32_t attention_bits);
+/* VsaOptions::topk (src/vsa.rs:54-59): round-half-even(keep_percent/100 * nonprefix), at least
+ * 1, at most nonprefix - 1 (0 when nonprefix <= 1). */
+uint32_t h3_vsa_topk(double keep_percent, uint32_t nonprefix);
+/* VsaOptions::dense_reason (src/vsa.rs:60-72): NULL when the step runs sparse, else
+ * "below_min_tokens" or "outside_sigma_window". */
+const char *h3_vsa_dense_reason(const h3_vsa_options *options, uint32_t tokens, float sigma,
+                                double shift);
+
+/* ---- VSA runtime (src/vsa/device.rs: Runtime::new, emit, reset) */
+
+typedef struct h3_vsa h3_vsa;
+
+/* Runtime::new (src/vsa/device.rs:49-188) for the INT8 attention (bits 8): uploads the plan
+ * (HOST arrays as h3_vsa_plan fills them), derives the h3.vsa.* and attention configs, and
+ * allocates the gathered q/k/v, block means, scores, routes, operand and output buffers and
+ * one zeroed K-mean vector per layer. The only allocating VSA call. */
+int h3_vsa_build(const int32_t *src, const int32_t *inverse, const int32_t *lengths,
+                 uint32_t blocks, uint32_t seq_len, uint32_t prefix_blocks,
+                 const h3_vsa_options *options, uint32_t heads, uint32_t layers, h3_vsa **out);
+void h3_vsa_destroy(h3_vsa *vsa);
+/* Runtime::reset (device.rs:189-196): zero every layer's K-mean vector. */
+int h3_vsa_reset(h3_vsa *vsa, h3_stream stream);
+/* Runtime::emit (device.rs:197-446) for layer `layer`: gather q, k, v [seq_len][heads*128] f16
+ * -> pool q, k -> block scores -> route -> Q operand (zero mean), K operand centred on the
+ * layer's K mean from the previous call || V transpose -> sparse attention -> the layer's K
+ * mean from this call's block means -> scatter into out [seq_len][heads*128] f16, or, with a
+ * gate [seq_len][heads*128] f16 (gate.ptr non-NULL), pool v -> coarse attention -> gated
+ * scatter. */
+int h3_vsa_attend(h3_vsa *vsa, uint32_t layer, h3_view q, h3_view k, h3_view v, h3_view out,
+                  h3_view gate, h3_stream stream);
+/* Device buffers of the runtime, for inspection: the plan, gathered q/k/v, block means,
+ * scores and routes, the INT8 operands, V^T, the gathered output, and layer `layer`'s K mean. */
+typedef struct {
+  h3_view src, inverse, lengths, q, k, v, qm, km, scores, routes, qi, ki, qs, ks, vt, out,
+      kmean;
+  h3_vsa_cfg cfg;
+  h3_attention_cfg attention;
+} h3_vsa_buffers;
+int h3_vsa_inspect(const h3_vsa *vsa, uint32_t layer, h3_vsa_buffers *out);
+
 /* ------------------------------------------------------------------ stack (host mirror) */
 
 /* Row capacity the reference allocates for a sequence of `tokens` (src/stack.rs:299-302):
