@@ -131,6 +131,64 @@ def adjacent_kernels(torch, H, dev, tokens, width, out):
     return res
 
 
+def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
+    """The VSA block-sparse path (BASELINE config 5b; src/vsa.rs, src/vsa/device.rs) at the same
+    shape: the plan of the latent grid in 4x4x4 cubes (no prefix segments), the reference's
+    default options (keep 10% of the non-prefix cubes per query cube and head, plus the
+    diagonal +-1), INT8 attention. Times the whole runtime sequence (gather, pool, scores,
+    route, operands, V^T, sparse attention, K-mean update, scatter) and the sparse attention
+    kernel alone; counts the (query, key) pairs the routes keep."""
+    import ctypes
+
+    import numpy as np
+
+    nt, nh, nw = grid
+    if nt * nh * nw != tokens:
+        return None
+    width = heads * 128
+    src, inverse, lengths, prefix = H.vsa_plan([], tokens, nt, nh, nw)
+    vsa = H.Vsa(src, inverse, lengths, prefix, heads)
+    q = fused[:, :width].to(torch.float16)
+    k = fused[:, width:2 * width].to(torch.float16)
+    v = fused[:, 2 * width:].to(torch.float16)
+    out = torch.empty((tokens, width), dtype=torch.float16, device=dev)
+    run_ms = time_launches(torch, lambda: vsa.attend(0, q, k, v, out), 3)
+    b = vsa.buffers(0)
+    att_ms = time_launches(torch, lambda: H.vsa_attention_i8(
+        b.attention, b.attention.tokens, heads, b.qi, b.qs, b.ki, b.ks, b.vt, b.out, b.routes,
+        b.lengths), 5)
+    nb = len(lengths)
+    routes = torch.empty(heads * nb * nb, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    hip = ctypes.CDLL("libamdhip64.so")
+    rc = hip.hipMemcpy(ctypes.c_void_p(routes.data_ptr()), ctypes.c_void_p(b.routes.ptr),
+                       ctypes.c_size_t(b.routes.bytes), 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy of the routes failed: {rc}")
+    r = routes.view(heads, nb, nb).to(torch.float64)
+    ln = torch.from_numpy(lengths.astype(np.float64)).to(dev)
+    useful = float(((r @ ln) * ln).sum().item())             # live (query, key) pairs kept
+    executed = float(r.sum().item()) * 64 * 64               # pairs the MFMAs run (whole cubes)
+    ops_dense = 4.0 * tokens * tokens * heads * 128
+    res = {
+        "workload": f"config 5b shape: S={tokens} H={heads}, grid {nt}x{nh}x{nw} in {nb} cubes, "
+                    "keep 10% + diagonal +-1 (reference defaults), int8 QK, f16 PV, synthetic "
+                    "N(0,1) q/k/v (K offset N(0,2))",
+        "runtime_ms": round(run_ms, 3),
+        "sparse_attention_ms": round(att_ms, 3),
+        "density_useful": round(useful / (float(tokens) * tokens * heads), 4),
+        "density_executed": round(executed / ((64.0 * nb) ** 2 * heads), 4),
+        "useful_tops": round(4.0 * 128 * useful / (att_ms * 1e-3) / 1e12, 1),
+        "executed_tops": round(4.0 * 128 * executed / (att_ms * 1e-3) / 1e12, 1),
+        "executed_frac_int8_peak": round(4.0 * 128 * executed / (att_ms * 1e-3) / 1e12
+                                         / PEAK_INT8_TOPS, 4),
+        "dense_equivalent_tops": round(ops_dense / (run_ms * 1e-3) / 1e12, 1),
+        "speedup_vs_dense_attention": round(dense_ms / run_ms, 2),
+    }
+    vsa.close()
+    return res
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per attention launch from the committed rocprofv3 PMC summary, if present."""
     p = ROOT / "profiles" / f"attention_i8qkhm_{workload}_pmc.md"
@@ -333,6 +391,9 @@ def main() -> None:
         print("# int4 path...", file=sys.stderr, flush=True)
         line["adjacent_kernels"]["int4_qk"] = int4_path(torch, H, dev, tokens, heads, fused_bf16,
                                                         vt, torch.empty_like(out))
+        print("# vsa path...", file=sys.stderr, flush=True)
+        line["adjacent_kernels"]["vsa"] = vsa_path(torch, H, dev, tokens, heads, grid, fused_bf16,
+                                                   att_avg)
     if not args.no_cpu:
         print("# cpu baseline...", file=sys.stderr, flush=True)
         q16 = fused_bf16[:, :width].to(torch.float16).cpu().numpy().view(np.uint16)

@@ -669,15 +669,17 @@ void k_attention(Args a) {
 //
 // kernels/vsa_attention_8.loom: query cube b (64 queries in the gathered layout) attends to the
 // keys of every key cube kb with routes[head][b][kb] != 0, and within a cube only to its first
-// lengths[kb] keys. A workgroup here is two query cubes (waves 0-1: cube 2qb, waves 2-3: cube
-// 2qb + 1), and a key tile is one cube. Per run of the key loop the workgroup scans the two
+// lengths[kb] keys. A workgroup here is kWaves/2 query cubes (waves 2c and 2c+1: cube
+// (kWaves/2)qb + c), and a key tile is one cube. Per run of the key loop the workgroup scans the two
 // route rows into an LDS list of the cubes that either query cube keeps (in ascending order,
-// up to kListMax of them per run), each entry carrying which of the two keeps it and its live
+// up to kListMax of them per run), each entry carrying which of them keeps it and its live
 // length. The pipeline of k_attention then walks that list: the K/V^T tiles of a listed cube
 // are staged for the whole workgroup, and a wave whose query cube does not keep the cube skips
 // its QK, softmax and PV (wave-uniform branches), so every wave computes exactly its own
 // routes. Dead keys are masked through their staged scale pair (store_scales_live).
 constexpr int kListMax = 1024;           // list entries per run of the key loop
+constexpr int kCubes = kWaves / 2;        // query cubes per workgroup (64 queries each)
+static_assert(kCubes == 1 || kCubes == 2, "a workgroup holds one or two query cubes");
 constexpr uint32_t kEntryCube = 0x3fffu;  // entry: cube (14 bits) | keep flags << 14 | live << 16
 
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -733,8 +735,8 @@ void k_attention_vsa(Args a) {
   st.alpha = 1.0f;
   float u[2][16] = {};
 
-  const uint32_t cube0 = 2 * qb;
-  const bool has1 = cube0 + 1 < a.blocks;
+  const uint32_t cube0 = kCubes * qb;
+  const bool has1 = kCubes == 2 && cube0 + 1 < a.blocks;
   const int32_t* route0 = a.routes + ((size_t)head * a.blocks + cube0) * a.blocks;
   const int32_t* route1 = route0 + a.blocks;
   auto cube_of = [](uint32_t e) { return e & kEntryCube; };
