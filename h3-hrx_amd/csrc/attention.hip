@@ -20,7 +20,7 @@
 //        in f16 and in the f32 sums); only then are the output accumulators rescaled, so in
 //        the steady state the O accumulators are touched by nothing but the MFMAs.
 //   PV   O^T (128 ch x 32 queries) += V^T . P^T on v_mfma_f32_32x32x16_f16; the row sum is
-//        accumulated from the same packed f16 probabilities with v_dot2.
+//        accumulated from the same packed f16 probabilities (a packed f16 add tree per tile).
 //
 // Software pipeline (one wave, step j): the matrix work of two tiles runs under the vector work
 // of one, in a fixed issue order:
@@ -265,10 +265,10 @@ struct State {
 // Issue-order fence: the scheduler keeps each chunk's MFMA, LDS reads and VALU work together.
 #define H3_CHUNK_END() __builtin_amdgcn_sched_barrier(0)
 
-// Probabilities of key slots r, r+1 of S^T block bb: exp2, pack to f16 (B operand of PV), sum.
+// Probabilities of key slots r, r+1 of S^T block bb: exp2, pack to f16 (B operand of PV).
 template <bool kMasked>
 __device__ __forceinline__ void exp_pair(const float (&u)[2][16], int bb, int r, float qsl,
-                                         float negm, v8h (&pb)[4], float& l) {
+                                         float negm, v8h (&pb)[4]) {
   float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r], qsl, negm));
   float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[bb][r + 1], qsl, negm));
   if (kMasked) {
@@ -276,9 +276,18 @@ __device__ __forceinline__ void exp_pair(const float (&u)[2][16], int bb, int r,
     if (u[bb][r + 1] == -INFINITY) p1 = 0.0f;
   }
   const v2h pair = {(_Float16)p0, (_Float16)p1};
-  l = __builtin_amdgcn_fdot2(pair, v2h{(_Float16)1.0f, (_Float16)1.0f}, l, false);
   pb[2 * bb + r / 8][r % 8] = pair[0];
   pb[2 * bb + r / 8][r % 8 + 1] = pair[1];
+}
+
+// This lane's sum of a tile's 32 packed f16 probabilities: a tree of packed f16 adds (15 full-rate
+// v_pk_add_f16) and one v_dot2 into f32, instead of a v_dot2 (two VALU slots each) per pair. The
+// partial sums stay below 2^13 (p <= 2^8 under the lazy max), well inside f16's range.
+__device__ __forceinline__ float tile_sum(const v8h (&pb)[4]) {
+  const v8h t8 = (pb[0] + pb[1]) + (pb[2] + pb[3]);
+  const v4h t4 = v4h{t8[0], t8[1], t8[2], t8[3]} + v4h{t8[4], t8[5], t8[6], t8[7]};
+  const v2h t2 = v2h{t4[0], t4[1]} + v2h{t4[2], t4[3]};
+  return __builtin_amdgcn_fdot2(t2, v2h{(_Float16)1.0f, (_Float16)1.0f}, 0.0f, false);
 }
 
 // max3 kept where it is written: as an opaque instruction it is neither reassociated into one
@@ -442,7 +451,6 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   v4i kop[8];
   v8h vop[16];
   float4 k4[8], c4[8];
-  float la = 0.0f, lb = 0.0f;
 
   // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
   constexpr bool kI4 = isI4(kMode);
@@ -474,7 +482,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
     }
     if (do_qk)
       s[bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[dc], dc == 0 ? magic : s[bb], 0, 0, 0);
-    if (do_pv) exp_pair<kMaskCur>(u, 0, 2 * c, qsl, negm, pb, la);
+    if (do_pv) exp_pair<kMaskCur>(u, 0, 2 * c, qsl, negm, pb);
     H3_CHUNK_END();
   }
 
@@ -494,20 +502,20 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
     }
     if (do_pv) {
       st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[g], st.acc[db], 0, 0, 0);
-      if (c < 8) exp_pair<kMaskCur>(u, 1, 2 * c, qsl, negm, pb, lb);
+      if (c < 8) exp_pair<kMaskCur>(u, 1, 2 * c, qsl, negm, pb);
     }
     if (do_qk && c >= 6 && c < 14) {
       const int q = c - 6, bb = q >> 2, i = q & 3;
       dequant4<kMaskNext>(s, bb, i, k4[q], c4[q], u, tmax, knext0 + slot_key(bb, i, half),
                           tokens);
     }
-    if (do_qk && c == 14) {  // under the last MFMAs: tile j's sums are complete
-      st.l += la + lb;
+    if (do_qk && c == 14) {  // under the last MFMAs: tile j's probabilities are complete
+      if (do_pv) st.l += tile_sum(pb);
       raise_max(tmax, qsl, st);
     }
     H3_CHUNK_END();
   }
-  if (!do_qk) st.l += la + lb;
+  if (!do_qk && do_pv) st.l += tile_sum(pb);
 }
 
 template <int kMode>
