@@ -31,8 +31,8 @@ WORKLOADS = {
     # name: (tokens, heads, rope grid (t, h, w))
     "c3": (129024, 32, (32, 42, 96)),
     "c2": (31104, 32, (24, 24, 54)),
-    # config 4's self-attention: the 129,024 video tokens and 1,248 audio tokens as one sequence
-    # (the audio rows continue the grid as a 33rd frame)
+    # config 4: the 129,024 video tokens and 1,248 audio tokens as one self-attention sequence
+    # (the audio rows continue the grid as a 33rd frame), then the text cross-attention
     "c4": (130272, 32, (32, 42, 96)),
     "c1": (1024, 8, (1, 32, 32)),
 }
@@ -129,6 +129,45 @@ def adjacent_kernels(torch, H, dev, tokens, width, out):
                                "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 8e12, 4)}
     return res
+
+
+TEXT_TOKENS, TEXT_KV_HEADS, TEXT_PAD = 512, 8, 0.2  # BASELINE config 4's text cross-attention
+
+
+class TextCross:
+    """BASELINE config 4's GQA text cross-attention (h3_attention_i8qkhm_cross, an extension):
+    the step's head-major Q operand (32 query heads) attends to 512 text tokens of 8 key/value
+    heads, N(0,1), the last 20 % of them padding (masked). The text K operand and V^T are
+    prepared by the same kernels as the self-attention's (prepare_qk_i8hm, transpose_f16)."""
+
+    def __init__(self, torch, H, dev, tokens, heads, cap, qi, qs):
+        self.H = H
+        kh, kt = TEXT_KV_HEADS, TEXT_TOKENS
+        g = torch.Generator(device=dev).manual_seed(99)
+        self.k = torch.randn((kt, kh * 128), generator=g, device=dev).half()
+        self.v = torch.randn((kt, kh * 128), generator=g, device=dev).half()
+        mask = torch.ones(kt, dtype=torch.uint8, device=dev)
+        mask[int(kt * (1 - TEXT_PAD)):] = 0
+        self.mask = mask
+        self.ki = torch.zeros(kh * kt * 32, dtype=torch.int32, device=dev)
+        self.ks = torch.zeros(kh * kt, dtype=torch.float32, device=dev)
+        self.vt = torch.zeros(kh * 128 * kt, dtype=torch.float16, device=dev)
+        self.zero = torch.zeros(kh * 128, dtype=torch.float32, device=dev)
+        self.prep = H.PrepareCfg(kh * 128, 0, kh, 1.0, kt, 1e-5, H.H3_ELEM_F16)
+        self.tcfg = H.TransposeCfg(kh * 128, kt, H.H3_ELEM_F16)
+        self.cfg = H.CrossCfg(heads, kh, tokens, cap, kt, kt, heads * 128)
+        self.qi, self.qs = qi, qs
+        self.out = torch.empty((tokens, heads * 128), dtype=torch.float16, device=dev)
+        self.ops = 4.0 * tokens * kt * heads * 128
+
+    def prepare(self):
+        H = self.H
+        H.prepare_qk_i8hm(self.prep, TEXT_TOKENS, self.k, self.zero, self.ki, self.ks)
+        H.transpose_f16(self.tcfg, TEXT_TOKENS, TEXT_TOKENS, self.v, self.vt)
+
+    def attend(self):
+        self.H.attention_i8qkhm_cross(self.cfg, self.qi, self.qs, self.ki, self.ks, self.vt,
+                                      self.mask, self.out)
 
 
 def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
@@ -314,6 +353,8 @@ def main() -> None:
     ac = H.AttentionCfg(width, width, width, tokens, cap, H.config_f32(1.0 / math.sqrt(128.0)))
 
     att_events = []
+    text = TextCross(torch, H, dev, tokens, heads, cap, qi, qs)
+    with_text = args.workload == "c4"  # config 4 = joint self-attention + text cross-attention
 
     def step(record: bool):
         H.prepare_qk_rope_i8hm(pq, tokens, fused_bf16, qnorm, cos_t, sin_t, qi, qs)
@@ -327,6 +368,9 @@ def main() -> None:
         if record:
             e1.record()
             att_events.append((e0, e1))
+        if with_text:
+            text.prepare()
+            text.attend()
 
     for _ in range(args.warmup):
         step(False)
@@ -342,7 +386,8 @@ def main() -> None:
     att_avg = sum(att_ms) / len(att_ms)
     att_q = np.percentile(np.array(att_ms), [25, 50, 75])
     ops = 4.0 * tokens * tokens * heads * 128  # QK + PV multiply-adds x2 (benches/kernels.rs:570)
-    value = ops / (ms_step * 1e-3) / 1e12
+    step_ops = ops + (text.ops if with_text else 0.0)
+    value = step_ops / (ms_step * 1e-3) / 1e12
     achieved = ops / (att_avg * 1e-3) / 1e12
     out_ok = bool(torch.isfinite(out).all().item())
 
@@ -368,7 +413,9 @@ def main() -> None:
             "head_dim": 128,
             "capacity": cap,
             "step": "prepare_qk_rope_i8hm(Q) + prepare_qk_rope_i8hm(K) + transpose_qkv_v_f16 "
-                    "+ attention_i8qkhm",
+                    "+ attention_i8qkhm" + (" + text K/V^T prep + attention_i8qkhm_cross (512 text "
+                                            "tokens, 8 KV heads, 20% padding masked)"
+                                            if with_text else ""),
         },
         "attention_ms": round(att_avg, 4),
         "attention_ms_median": round(float(att_q[1]), 4),
@@ -391,6 +438,14 @@ def main() -> None:
         print("# int4 path...", file=sys.stderr, flush=True)
         line["adjacent_kernels"]["int4_qk"] = int4_path(torch, H, dev, tokens, heads, fused_bf16,
                                                         vt, torch.empty_like(out))
+        text.prepare()
+        cross_ms = time_launches(torch, text.attend, 10)
+        line["adjacent_kernels"]["text_cross_attention"] = {
+            "shape": f"{tokens} queries x {heads} heads over {TEXT_TOKENS} text tokens x "
+                     f"{TEXT_KV_HEADS} KV heads, last {int(TEXT_PAD * 100)}% masked (config 4's text part)",
+            "ms": round(cross_ms, 4),
+            "tops": round(text.ops / (cross_ms * 1e-3) / 1e12, 1),
+            "frac_int8_peak": round(text.ops / (cross_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
         print("# vsa path...", file=sys.stderr, flush=True)
         line["adjacent_kernels"]["vsa"] = vsa_path(torch, H, dev, tokens, heads, grid, fused_bf16,
                                                    att_avg)

@@ -680,6 +680,43 @@ int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_st
                                           reinterpret_cast<hipStream_t>(stream)));
 }
 
+int h3_attention_i8qkhm_cross(const h3_cross_cfg* cfg, h3_view qi, h3_view qs, h3_view ki,
+                              h3_view ks, h3_view vt, h3_view key_mask, h3_view out,
+                              h3_stream stream) {
+  const char* stage = "cross attention";
+  if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
+  if (!in_range(cfg->q_heads, 1, 256) || !in_range(cfg->kv_heads, 1, 256) ||
+      cfg->q_heads % cfg->kv_heads != 0)
+    return set_error(H3_ERR_CONFIG, "%s: kv_heads %u must divide q_heads %u (both in [1, 256])",
+                     stage, cfg->kv_heads, cfg->q_heads);
+  if (!in_range(cfg->q_tokens, 1, 1048576) || !in_range(cfg->kv_tokens, 1, 1048576))
+    return set_error(H3_ERR_CONFIG, "%s: q_tokens %u / kv_tokens %u outside [1, 1048576]", stage,
+                     cfg->q_tokens, cfg->kv_tokens);
+  if (!in_range(cfg->q_capacity, 32, 1048576, 32) || cfg->q_capacity < cfg->q_tokens ||
+      !in_range(cfg->kv_capacity, 32, 1048576, 32) || cfg->kv_capacity < cfg->kv_tokens)
+    return set_error(H3_ERR_CONFIG,
+                     "%s: capacities %u / %u must be multiples of 32 covering the tokens", stage,
+                     cfg->q_capacity, cfg->kv_capacity);
+  if (!in_range(cfg->out_stride, 128, 32768, 128) || cfg->out_stride < 128 * cfg->q_heads)
+    return set_error(H3_ERR_CONFIG, "%s: out_stride %u outside [128 * q_heads, 32768] step 128",
+                     stage, cfg->out_stride);
+  const size_t qh = cfg->q_heads, kh = cfg->kv_heads, qc = cfg->q_capacity, kc = cfg->kv_capacity;
+  h3_view views[7] = {qi, qs, ki, ks, vt, key_mask, out};
+  size_t need[7] = {qh * qc * 128, qh * qc * 4, kh * kc * 128, kh * kc * 4, kh * 128 * kc * 2,
+                    cfg->kv_tokens, (size_t)cfg->q_tokens * cfg->out_stride * 2};
+  int st = check_bindings(stage, views, need, 7);
+  if (st) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_attention_cross(*cfg, static_cast<const int32_t*>(qi.ptr),
+                                                static_cast<const float*>(qs.ptr),
+                                                static_cast<const int32_t*>(ki.ptr),
+                                                static_cast<const float*>(ks.ptr),
+                                                static_cast<const uint16_t*>(vt.ptr),
+                                                static_cast<const uint8_t*>(key_mask.ptr),
+                                                static_cast<uint16_t*>(out.ptr),
+                                                reinterpret_cast<hipStream_t>(stream)));
+}
+
 int h3_vsa_attention_i8(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_stream stream) {

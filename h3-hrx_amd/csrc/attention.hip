@@ -116,6 +116,10 @@ struct Args {
   uint32_t total;      // q_blocks * heads
   uint32_t per_xcd;    // ceil(total / 8)
   float neg_tau;       // tile skip (kTokenI4Skip): -tau * log2(e)
+  const uint8_t* key_mask;  // k_attention_cross: [tokens], nonzero = key attended
+  uint32_t q_tokens;        // k_attention_cross: query rows (tokens counts the keys)
+  uint32_t q_capacity;      // k_attention_cross: head-major row capacity of qi / qs
+  uint32_t kv_group;        // k_attention_cross: query heads per key/value head
   const int32_t* routes;   // kTokenI8Vsa: [head_limit][blocks][blocks], nonzero = kept
   const int32_t* lengths;  // kTokenI8Vsa: live keys of each 64-key cube
   uint32_t blocks;         // kTokenI8Vsa: tokens / 64
@@ -853,6 +857,139 @@ void k_attention_vsa(Args a) {
   }
 }
 
+// ---------------------------------------------------------------- cross-attention (GQA, key mask)
+//
+// An extension with no counterpart in the reference: queries of one sequence (the video + audio
+// rows) attend to the keys of another (the text), with grouped heads (query head h reads key /
+// value head h / kv_group) and a key-padding mask (keys with key_mask == 0, and keys past the
+// key count, get probability 0). Head-major int8 operands as attention_i8qkhm, separate row
+// capacities for Q and K. The key loop is the pipeline of k_attention; every tile is masked
+// through its staged scale pairs (ks, -inf for a dead key), so no tile needs the masked step.
+
+// Whether key k0 + (this lane's scale row) is attended; read by the lanes that store scales.
+__device__ __forceinline__ bool key_live(const Args& a, const Stager& sg, uint32_t k0) {
+  const uint32_t key = k0 + swap23(sg.srow);
+  return key < a.tokens && a.key_mask[key] != 0;
+}
+
+__device__ __forceinline__ void store_scales_mask(char* kst, const Stager& sg, float ks,
+                                                  bool live) {
+  if ((threadIdx.x & 63) < kSRows) {
+    float* sc = reinterpret_cast<float*>(kst + kKRows);
+    sc[sg.srow] = ks;
+    sc[kKeys + sg.srow] = live ? -(kMagic * ks) : -INFINITY;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_attention_cross(Args a) {
+  constexpr int kMode = kHeadI8;
+  constexpr int kWaitPrevStep = kWaitPrevStepOf(kMode);
+  __shared__ __attribute__((aligned(16))) char k0s[kKStage];
+  __shared__ __attribute__((aligned(16))) char k1s[kKStage];
+  __shared__ __attribute__((aligned(16))) char k2s[kKStage];
+  __shared__ __attribute__((aligned(16))) char v0s[kVStage];
+  __shared__ __attribute__((aligned(16))) char v1s[kVStage];
+  __shared__ __attribute__((aligned(16))) char v2s[kVStage];
+
+  const uint32_t b = blockIdx.x;
+  const uint32_t logical = (b & 7u) * a.per_xcd + (b >> 3);
+  if (logical >= a.total) return;
+  const uint32_t head = logical / a.q_blocks;  // query head
+  const uint32_t qb = logical % a.q_blocks;
+  const uint32_t kv_head = head / a.kv_group;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31;
+  const int half = lane >> 5;
+  const uint32_t tiles32 = (a.q_tokens + 31) / 32;
+  const uint32_t q_tile = qb * kWaves + wave;
+  const uint32_t q_tile_c = q_tile < tiles32 ? q_tile : tiles32 - 1;
+  const uint32_t q = q_tile_c * kQueriesPerWave + n;
+  const uint32_t q_read = q < a.q_tokens ? q : a.q_tokens - 1;
+
+  const Stager sg = make_stager<kMode>(a, wave, lane);
+  const uint32_t n_tiles = (a.tokens + kKeys - 1) / kKeys;
+
+  float ks0 = stage_k<kMode>(a, sg, kv_head, 0, k0s);
+  const bool m0 = key_live(a, sg, 0);
+  float ks1 = stage_k<kMode>(a, sg, kv_head, kKeys, k1s);
+  const bool m1 = key_live(a, sg, kKeys);
+  float ks_held = stage_k<kMode>(a, sg, kv_head, 2 * kKeys, k2s);
+  bool m_held = key_live(a, sg, 2 * kKeys);
+  stage_v(a, sg, kv_head, 0, v0s);
+  stage_v(a, sg, kv_head, kKeys, v1s);
+
+  v4i qop[4];
+  {
+    const int32_t* src = a.qi + ((size_t)head * a.q_capacity + q_read) * 32;
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) qop[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
+  }
+  const float qsl = a.qs[(size_t)head * a.q_capacity + q_read] * kLog2e;
+
+  State st;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
+  st.m = -1.0e30f;
+  st.l = 0.0f;
+  st.alpha = 1.0f;
+
+  store_scales_mask(k0s, sg, ks0, m0);
+  store_scales_mask(k1s, sg, ks1, m1);
+  step_barrier<kWaitAll>();
+  float u[2][16];
+  first_tile<kMode, false>(k0s, qop, qsl, st, u, n, half, a.tokens);
+  step_barrier<kWaitAll>();
+
+#define H3_CROSS_STEP(kc, kn, kn2, vc, vn2)                                                   \
+  {                                                                                          \
+    const float ks_new = stage_k<kMode>(a, sg, kv_head, (j + 3) * kKeys, kc);                \
+    const bool m_new = key_live(a, sg, (j + 3) * kKeys);                                     \
+    stage_v(a, sg, kv_head, (j + 2) * kKeys, vn2);                                           \
+    step<kMode, true, false, false>(kn, vc, qop, qsl, st, u, n, half, 0, a.tokens);          \
+    store_scales_mask(kn2, sg, ks_held, m_held);                                             \
+    ks_held = ks_new;                                                                        \
+    m_held = m_new;                                                                          \
+    step_barrier<kWaitPrevStep>();                                                           \
+    ++j;                                                                                     \
+  }
+  const uint32_t steady = n_tiles - 1;
+  uint32_t j = 0;
+  for (; j + 3 <= steady;) {
+    H3_CROSS_STEP(k0s, k1s, k2s, v0s, v2s)
+    H3_CROSS_STEP(k1s, k2s, k0s, v1s, v0s)
+    H3_CROSS_STEP(k2s, k0s, k1s, v2s, v1s)
+  }
+  if (j < steady) H3_CROSS_STEP(k0s, k1s, k2s, v0s, v2s)
+  if (j < steady) H3_CROSS_STEP(k1s, k2s, k0s, v1s, v0s)
+#undef H3_CROSS_STEP
+  {
+    const uint32_t r = j % 3;
+    const char* vlast = r == 0 ? v0s : r == 1 ? v1s : v2s;
+    step<kMode, false, false, false>(nullptr, vlast, qop, qsl, st, u, n, half, 0, a.tokens);
+  }
+  step_barrier<kWaitAll>();
+
+  const float l_tot = st.l + __shfl_xor(st.l, 32);
+  const float inv = 1.0f / l_tot;
+  if (q_tile < tiles32 && q < a.q_tokens) {
+    uint16_t* dst = a.out + (size_t)q * a.out_stride + head * 128;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
+                 (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
+        *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
@@ -889,6 +1026,34 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
     hipLaunchKernelGGL(k_attention<kTokenI4Skip>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
+                                  const int32_t* ki, const float* ks, const uint16_t* vt,
+                                  const uint8_t* key_mask, uint16_t* out, hipStream_t stream) {
+  Args a{};
+  a.qi = qi;
+  a.qs = qs;
+  a.ki = ki;
+  a.ks = ks;
+  a.vt = vt;
+  a.out = out;
+  a.key_mask = key_mask;
+  a.tokens = cfg.kv_tokens;
+  a.capacity = cfg.kv_capacity;
+  a.q_tokens = cfg.q_tokens;
+  a.q_capacity = cfg.q_capacity;
+  a.token_count = cfg.q_tokens;
+  a.kv_group = cfg.q_heads / cfg.kv_heads;
+  a.out_stride = cfg.out_stride;
+  a.q_blocks = (cfg.q_tokens + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  a.heads = cfg.q_heads;
+  a.kv_head_limit = cfg.kv_heads;
+  a.head_limit = cfg.q_heads;
+  a.total = a.q_blocks * cfg.q_heads;
+  a.per_xcd = (a.total + 7) / 8;
+  hipLaunchKernelGGL(k_attention_cross, dim3(a.per_xcd * 8), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

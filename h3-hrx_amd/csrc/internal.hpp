@@ -79,6 +79,10 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             const float* ks, const uint16_t* vt, uint16_t* out,
                             hipStream_t stream);
 
+// Cross-attention with grouped heads and a key-padding mask (attention.hip)
+hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
+                                  const int32_t* ki, const float* ks, const uint16_t* vt,
+                                  const uint8_t* key_mask, uint16_t* out, hipStream_t stream);
 // kTokenI8Vsa: the int8 token-major attention over the cubes `routes` keeps (attention.hip)
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
                                 uint32_t heads, const int32_t* qi, const float* qs,

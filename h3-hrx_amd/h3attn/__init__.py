@@ -126,6 +126,12 @@ class IntQk(ctypes.Structure):
     ]
 
 
+class CrossCfg(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_uint32) for name in (
+        "q_heads", "kv_heads", "q_tokens", "q_capacity", "kv_tokens", "kv_capacity",
+        "out_stride")]
+
+
 class VsaCfg(ctypes.Structure):
     """h3.vsa.* (kernels/vsa_ops.loom:3-9)."""
     _fields_ = [
@@ -198,6 +204,8 @@ SIGNATURES = {
     "h3_attention_i4qks": (
         [_P(AttentionSkipCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          _S], ctypes.c_int),
+    "h3_attention_i8qkhm_cross": (
+        [_P(CrossCfg), View, View, View, View, View, View, View, _S], ctypes.c_int),
     "h3_vsa_gather": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
     "h3_vsa_scatter": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
     "h3_vsa_pool": ([_P(VsaCfg), View, View, View, _S], ctypes.c_int),
@@ -469,6 +477,13 @@ class Stack:
         ops = IntQk()
         check(lib().h3_stack_operands(self.handle, ctypes.byref(ops)))
         return ops
+
+
+def attention_i8qkhm_cross(cfg: CrossCfg, qi, qs, ki, ks, vt, key_mask, out, stream=None) -> None:
+    """Cross-attention with grouped heads and a key-padding mask (an extension)."""
+    check(lib().h3_attention_i8qkhm_cross(ctypes.byref(cfg), view(qi), view(qs), view(ki),
+                                          view(ks), view(vt), view(key_mask), view(out),
+                                          stream_ptr(stream)))
 
 
 # ------------------------------------------------------------------------- VSA (src/vsa.rs)

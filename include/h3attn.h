@@ -297,6 +297,36 @@ int h3_attention_i4qks(const h3_attention_skip_cfg *cfg, uint32_t token_count, u
                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                        h3_stream stream);
 
+/* Cross-attention with grouped heads and a key-padding mask: BASELINE config 4's text
+ * cross-attention (32 query heads over 8 key/value heads, 512 text tokens, padded positions
+ * masked). An extension: the reference has no such kernel.
+ *   q_heads   [1, 256]; kv_heads divides q_heads; query head h reads key/value head
+ *             h / (q_heads / kv_heads)
+ *   q_tokens  [1, 1048576] query rows; q_capacity multiple of 32, >= q_tokens
+ *   kv_tokens [1, 1048576] key rows;   kv_capacity multiple of 32, >= kv_tokens
+ *   out_stride multiple of 128 in [128 * q_heads, 32768] */
+typedef struct {
+  uint32_t q_heads;
+  uint32_t kv_heads;
+  uint32_t q_tokens;
+  uint32_t q_capacity;
+  uint32_t kv_tokens;
+  uint32_t kv_capacity;
+  uint32_t out_stride;
+} h3_cross_cfg;
+
+/* h3_attention_i8qkhm_cross: out[t][h*128 + c] = sum_j softmax_j(S_tj * qs_t * ks_j) vt[g*128 +
+ * c][j] over the keys j < kv_tokens with key_mask[j] != 0, g = h / (q_heads / kv_heads).
+ * Head-major operands as h3_attention_i8qkhm: qi [q_heads][q_capacity][32] i32, qs
+ * [q_heads][q_capacity] f32, ki [kv_heads][kv_capacity][32], ks [kv_heads][kv_capacity],
+ * vt [kv_heads*128][kv_capacity] f16 (columns >= kv_tokens finite), key_mask [kv_tokens] u8,
+ * out [q_tokens][out_stride] f16. A query whose keys are all masked gets a non-finite row. qs
+ * must be positive (the quantizer's are): masked keys are dropped through a -inf
+ * dequantisation offset. */
+int h3_attention_i8qkhm_cross(const h3_cross_cfg *cfg, h3_view qi, h3_view qs, h3_view ki,
+                              h3_view ks, h3_view vt, h3_view key_mask, h3_view out,
+                              h3_stream stream);
+
 /* ------------------------------------------------------------------ VSA (video sparse attention) */
 
 /* Config of h3.vsa.* (kernels/vsa_ops.loom:3-9), as src/vsa/device.rs:63-77 builds it:

@@ -596,3 +596,56 @@ void h3o_prepare_qk_i4_f32(const uint16_t *x, int fmt, const float *mean, int to
     }
   }
 }
+
+/* Cross-attention of int8 operands with grouped heads and a key mask, f64 (an extension with no
+ * reference kernel; the formula is h3o_attention_f64's over the attended keys): query row t of
+ * head h attends to the keys j < kv_tokens with mask[j] != 0 of key/value head h / group.
+ *   qc [qh][q_cap][128], qs [qh][q_cap]; kc [kh][kv_cap][128], ks [kh][kv_cap];
+ *   vt [kh*128][kv_cap] f16; out f64 [n_rows][qh][128]. */
+int h3o_cross_attention_f64(const int8_t *qc, const float *qs, const int8_t *kc, const float *ks,
+                            const uint16_t *vt, const uint8_t *mask, int q_cap, int kv_tokens,
+                            int kv_cap, int qh, int kh, const int *rows, int n_rows, double *out,
+                            int threads) {
+  const int d = 128, group = qh / kh;
+  long total = (long)n_rows * qh;
+#ifdef _OPENMP
+  if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel num_threads(threads)
+#endif
+  {
+    double *score = (double *)malloc(sizeof(double) * (size_t)(kv_tokens > 0 ? kv_tokens : 1));
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+    for (long job = 0; job < total; ++job) {
+      const int ri = (int)(job / qh), h = (int)(job % qh), g = h / group;
+      const int row = rows[ri];
+      const int8_t *q = qc + ((size_t)h * q_cap + row) * d;
+      const double qscale = (double)qs[(size_t)h * q_cap + row];
+      double top = -INFINITY;
+      for (int j = 0; j < kv_tokens; ++j) {
+        if (!mask[j]) { score[j] = -INFINITY; continue; }
+        const int8_t *k = kc + ((size_t)g * kv_cap + j) * d;
+        int32_t dot = 0;
+        for (int c = 0; c < d; ++c) dot += (int32_t)q[c] * (int32_t)k[c];
+        score[j] = (double)dot * qscale * (double)ks[(size_t)g * kv_cap + j];
+        if (score[j] > top) top = score[j];
+      }
+      double sum = 0.0;
+      for (int j = 0; j < kv_tokens; ++j) {
+        score[j] = mask[j] ? exp(score[j] - top) : 0.0;
+        sum += score[j];
+      }
+      double *o = out + ((size_t)ri * qh + h) * d;
+      for (int c = 0; c < d; ++c) {
+        const uint16_t *vrow = vt + ((size_t)g * d + c) * kv_cap;
+        double a = 0.0;
+        for (int j = 0; j < kv_tokens; ++j)
+          if (mask[j]) a += score[j] * (double)h3o_half_to_float(vrow[j]);
+        o[c] = a / sum;
+      }
+    }
+    free(score);
+  }
+  return 0;
+}

@@ -67,6 +67,11 @@
  *                           closed forms (uniform scores give the mean of the routed values, a
  *                           route to one block gives that block's attention) and by the dense
  *                           h3o_attention_f64 when every block is routed.
+ *   h3o_cross_attention_f64 the cross-attention extension (grouped heads, key mask): the formula
+ *                           of h3o_attention_f64 over the attended keys. Pinned by equality with
+ *                           h3o_attention_f64 when queries and keys are one sequence, the heads
+ *                           are not grouped and no key is masked; by the mean of the attended V
+ *                           rows for uniform scores; and by brute-force numpy on small shapes.
  *   h3o_attention_f64       the attention the operands define, tests/kernels.rs:1891-1913 and
  *                           2084-2111: softmax_j(sum(qc*kc) * qs * ks) . V in f64. Pinned by
  *                           closed forms: uniform keys give the mean of V, a single dominant key
@@ -174,6 +179,12 @@ void h3o_gemm_i8_qkv(const int8_t *a, const int8_t *w, const float *ws, const fl
  * [tokens] f32. */
 void h3o_prepare_plain_i8(const void *x, int fmt, int tokens, int width, int out_stride,
                           int8_t *codes, float *scales);
+
+/* Cross-attention with grouped heads and a key mask (this build's extension), f64. */
+int h3o_cross_attention_f64(const int8_t *qc, const float *qs, const int8_t *kc, const float *ks,
+                            const uint16_t *vt, const uint8_t *mask, int q_cap, int kv_tokens,
+                            int kv_cap, int qh, int kh, const int *rows, int n_rows, double *out,
+                            int threads);
 
 /* ---- VSA (h3oracle_vsa.c; src/vsa.rs, kernels/vsa_ops.loom, vsa_kmean.loom, vsa_attention_8) */
 /* Blocks of the plan: 64-row tiles of each prefix segment plus 4x4x4 video cubes. */

@@ -81,6 +81,10 @@ def lib():
                                             c_float, i32, f32]
         L.h3o_prepare_qk_i4_f32.restype = None
         ip = _P(np.int32, flags="C")
+        L.h3o_cross_attention_f64.argtypes = [i8, f32, i8, f32, u16, _P(np.uint8, flags="C"),
+                                              c_int, c_int, c_int, c_int, c_int, ip, c_int, f64,
+                                              c_int]
+        L.h3o_cross_attention_f64.restype = c_int
         L.h3o_vsa_plan_blocks.argtypes = [ip, c_int, c_int, c_int, c_int]
         L.h3o_vsa_plan_blocks.restype = c_int
         L.h3o_vsa_plan.argtypes = [ip, ip, c_int, c_int, c_int, c_int, c_int, i32, i32, i32,
@@ -421,4 +425,21 @@ def vsa_attention_f64(qc, qs, kc, ks, vt, tokens, cap, heads, routes, lengths, r
                                 heads, np.ascontiguousarray(routes, np.int32).reshape(-1),
                                 np.ascontiguousarray(lengths, np.int32), rows, len(rows), out,
                                 threads)
+    return out
+
+
+def cross_attention_f64(qc, qs, kc, ks, vt, mask, kv_tokens, rows, threads=0):
+    """Head-major codes qc [qh][q_cap][128], kc [kh][kv_cap][128], scales [heads][cap], vt
+    [kh*128][kv_cap] f16 bits, mask [kv_tokens] u8; f64 [len(rows)][qh][128]."""
+    qc = np.ascontiguousarray(qc, np.int8)
+    kc = np.ascontiguousarray(kc, np.int8)
+    qh, q_cap, _ = qc.shape
+    kh, kv_cap, _ = kc.shape
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros((len(rows), qh, 128), np.float64)
+    lib().h3o_cross_attention_f64(qc.reshape(-1), np.ascontiguousarray(qs, np.float32).reshape(-1),
+                                  kc.reshape(-1), np.ascontiguousarray(ks, np.float32).reshape(-1),
+                                  np.ascontiguousarray(vt, np.uint16).reshape(-1),
+                                  np.ascontiguousarray(mask, np.uint8), q_cap, kv_tokens, kv_cap,
+                                  qh, kh, rows, len(rows), out, threads)
     return out

@@ -256,3 +256,22 @@ def test_skip_twin_checks_tau_and_bindings():
     sizes[5] -= 2
     st = lib.h3_attention_i4qks(ctypes.byref(cfg), 97, 4, *[fake(n) for n in sizes], None)
     assert st == H.H3_ERR_BINDING and H.last_error().startswith("attention_i4qks: binding 5")
+
+
+def test_cross_attention_checks_groups_capacities_and_bindings():
+    L = H.lib()
+    qh, kh, qt, kt, qc, kc = 8, 2, 300, 77, 320, 96
+    need = [qh * qc * 128, qh * qc * 4, kh * kc * 128, kh * kc * 4, kh * 128 * kc * 2, kt,
+            qt * qh * 128 * 2]
+    cfg = H.CrossCfg(qh, kh, qt, qc, kt, kc, qh * 128)
+    for i in range(len(need)):
+        views = [fake(x) for x in need]
+        views[i] = fake(need[i] - 1)
+        st = L.h3_attention_i8qkhm_cross(ctypes.byref(cfg), *views, None)
+        assert st == H.H3_ERR_BINDING and f"binding {i} is" in H.last_error(), H.last_error()
+    for field, value in [("kv_heads", 3), ("q_capacity", 310), ("kv_capacity", 64),
+                         ("out_stride", 512), ("kv_tokens", 0)]:
+        bad = H.CrossCfg(qh, kh, qt, qc, kt, kc, qh * 128)
+        setattr(bad, field, value)
+        st = L.h3_attention_i8qkhm_cross(ctypes.byref(bad), *[fake(1 << 30)] * 7, None)
+        assert st == H.H3_ERR_CONFIG, (field, H.last_error())
