@@ -13,6 +13,10 @@ namespace h3 {
 namespace {
 
 constexpr int kRowsPerBlock = 8;  // 256 threads = 8 half-waves = 8 (token, head) rows
+// Rows per half-wave in the quantizers: their loads are issued together before any row is
+// processed, so each half-wave keeps kRowsAhead 256-byte rows in flight (one row is far too few
+// bytes in flight to cover HBM latency at these kernels' occupancy).
+constexpr int kRowsAhead = 4;
 
 // Butterfly partner exchange inside a 32-lane half-wave, on the vector pipe: lane masks 1, 2 and
 // 8 are one DPP move (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:8), mask 4 is two
@@ -200,27 +204,43 @@ __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
                                                     uint32_t row_stride, uint32_t head_offset,
                                                     uint32_t heads, uint32_t capacity,
                                                     float extra, uint32_t elem) {
-  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  // Half-wave g of block b takes rows b*8*kRowsAhead + 8i + g, i < kRowsAhead: for each i the
+  // block's eight half-waves cover eight consecutive rows.
+  const uint32_t first = blockIdx.x * kRowsPerBlock * kRowsAhead + (threadIdx.x >> 5);
   const int lane = threadIdx.x & 31;
-  if (row >= tokens * heads) return;
-  // head-major rows walk tokens fastest (contiguous code stores), token-major rows walk heads
-  const uint32_t t = kHeadMajor ? row % tokens : row / heads;
-  const uint32_t h = kHeadMajor ? row / tokens : row % heads;
-  const uint32_t col = head_offset + 128u * h + 4u * lane;
-  v4f y = widen4(load4(x, (size_t)t * row_stride + col), elem);
-  if (mean) {
-    const float4 m = *reinterpret_cast<const float4*>(mean + col);
-    y[0] = y[0] - m.x;
-    y[1] = y[1] - m.y;
-    y[2] = y[2] - m.z;
-    y[3] = y[3] - m.w;
+  const uint32_t total = tokens * heads;
+  uint2 in[kRowsAhead];
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t row = first + kRowsPerBlock * i;
+    if (row >= total) break;
+    // head-major rows walk tokens fastest (contiguous code stores), token-major rows walk heads
+    const uint32_t t = kHeadMajor ? row % tokens : row / heads;
+    const uint32_t h = kHeadMajor ? row / tokens : row % heads;
+    in[i] = load4(x, (size_t)t * row_stride + head_offset + 128u * h + 4u * lane);
   }
-  v4f r = hadamard128(y, lane);
-  float scale;
-  uint32_t word = quantize_row(r, extra, &scale);
-  size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
-  codes[out_row * 32 + lane] = (int32_t)word;
-  if (lane == 0) scales[out_row] = scale;
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t row = first + kRowsPerBlock * i;
+    if (row >= total) break;
+    const uint32_t t = kHeadMajor ? row % tokens : row / heads;
+    const uint32_t h = kHeadMajor ? row / tokens : row % heads;
+    const uint32_t col = head_offset + 128u * h + 4u * lane;
+    v4f y = widen4(in[i], elem);
+    if (mean) {
+      const float4 m = *reinterpret_cast<const float4*>(mean + col);
+      y[0] = y[0] - m.x;
+      y[1] = y[1] - m.y;
+      y[2] = y[2] - m.z;
+      y[3] = y[3] - m.w;
+    }
+    v4f r = hadamard128(y, lane);
+    float scale;
+    uint32_t word = quantize_row(r, extra, &scale);
+    size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
+    codes[out_row * 32 + lane] = (int32_t)word;
+    if (lane == 0) scales[out_row] = scale;
+  }
 }
 
 // int4 operands, token-major (kernels/prepare_qk_i4.loom): the same rotation, 16 bits of codes
@@ -232,25 +252,38 @@ __global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ 
                                                        uint32_t tokens, uint32_t row_stride,
                                                        uint32_t head_offset, uint32_t heads,
                                                        float extra, uint32_t elem) {
-  const uint32_t row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  const uint32_t first = blockIdx.x * kRowsPerBlock * kRowsAhead + (threadIdx.x >> 5);
   const int lane = threadIdx.x & 31;
-  if (row >= tokens * heads) return;
-  const uint32_t t = row / heads, h = row % heads;
-  const uint32_t col = head_offset + 128u * h + 4u * lane;
-  v4f y = widen4(load4(x, (size_t)t * row_stride + col), elem);
-  if (mean) {
-    const float4 m = *reinterpret_cast<const float4*>(mean + col);
-    y[0] = y[0] - m.x;
-    y[1] = y[1] - m.y;
-    y[2] = y[2] - m.z;
-    y[3] = y[3] - m.w;
+  const uint32_t total = tokens * heads;
+  uint2 in[kRowsAhead];
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t row = first + kRowsPerBlock * i;
+    if (row >= total) break;
+    const uint32_t t = row / heads, h = row % heads;
+    in[i] = load4(x, (size_t)t * row_stride + head_offset + 128u * h + 4u * lane);
   }
-  v4f r = hadamard128(y, lane);
-  float scale;
-  const uint32_t bits = quantize_row_i4(r, extra, &scale);
-  const uint32_t odd = (uint32_t)__builtin_amdgcn_mov_dpp((int)bits, 0xB1, 0xF, 0xF, true);
-  if ((lane & 1) == 0) codes[(size_t)row * 16 + lane / 2] = (int32_t)(bits | (odd << 16));
-  if (lane == 0) scales[row] = scale;
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t row = first + kRowsPerBlock * i;
+    if (row >= total) break;
+    const uint32_t h = row % heads;
+    const uint32_t col = head_offset + 128u * h + 4u * lane;
+    v4f y = widen4(in[i], elem);
+    if (mean) {
+      const float4 m = *reinterpret_cast<const float4*>(mean + col);
+      y[0] = y[0] - m.x;
+      y[1] = y[1] - m.y;
+      y[2] = y[2] - m.z;
+      y[3] = y[3] - m.w;
+    }
+    v4f r = hadamard128(y, lane);
+    float scale;
+    const uint32_t bits = quantize_row_i4(r, extra, &scale);
+    const uint32_t odd = (uint32_t)__builtin_amdgcn_mov_dpp((int)bits, 0xB1, 0xF, 0xF, true);
+    if ((lane & 1) == 0) codes[(size_t)row * 16 + lane / 2] = (int32_t)(bits | (odd << 16));
+    if (lane == 0) scales[row] = scale;
+  }
 }
 
 // RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
@@ -269,10 +302,17 @@ __global__ __launch_bounds__(256) void k_prepare_qk_rope(
   if (t >= tokens) return;
   const RopeLane tab = rope_lane(lane, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48);
   const size_t row0 = (size_t)t * row_stride + head_offset + 4u * lane;
-  uint2 next = load4(x, row0);
-  for (uint32_t h = 0; h < heads; ++h) {
-    const v4f v = widen4(next, elem);
-    if (h + 1 < heads) next = load4(x, row0 + 128u * (h + 1));  // one head ahead
+  uint2 ring[kRowsAhead];  // heads h .. h + kRowsAhead - 1 in flight
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i)
+    if ((uint32_t)i < heads) ring[i] = load4(x, row0 + 128u * i);
+  for (uint32_t h0 = 0; h0 < heads; h0 += kRowsAhead)
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t h = h0 + i;
+    if (h >= heads) break;
+    const v4f v = widen4(ring[i], elem);
+    if (h + kRowsAhead < heads) ring[i] = load4(x, row0 + 128u * (h + kRowsAhead));
     v4f y = rmsnorm_rope_f16(v, lane, tab, eps);
     if (mean) {
       const float4 m = *reinterpret_cast<const float4*>(mean + 128u * h + 4u * lane);
@@ -457,7 +497,7 @@ hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int hea
                              const void* x, const float* mean, int32_t* codes, float* scales,
                              hipStream_t stream) {
   const uint32_t rows = tokens * cfg.heads;
-  dim3 grid(div_up(rows, kRowsPerBlock));
+  dim3 grid(div_up(rows, kRowsPerBlock * kRowsAhead));
   if (head_major)
     hipLaunchKernelGGL(k_prepare_qk<true>, grid, dim3(256), 0, stream, x, mean, codes, scales,
                        tokens, cfg.row_stride, cfg.head_offset, cfg.heads, cfg.token_capacity,
@@ -473,7 +513,7 @@ hipError_t launch_prepare_qk_i4(const h3_prepare_cfg& cfg, uint32_t tokens, cons
                                 const float* mean, int32_t* codes, float* scales,
                                 hipStream_t stream) {
   const uint32_t rows = tokens * cfg.heads;
-  hipLaunchKernelGGL(k_prepare_qk_i4, dim3((rows + kRowsPerBlock - 1) / kRowsPerBlock), dim3(256),
+  hipLaunchKernelGGL(k_prepare_qk_i4, dim3(div_up(rows, kRowsPerBlock * kRowsAhead)), dim3(256),
                      0, stream, x, mean, codes, scales, tokens, cfg.row_stride, cfg.head_offset,
                      cfg.heads, cfg.extra_scale, cfg.elem);
   return hipGetLastError();
