@@ -47,6 +47,17 @@ int check_bindings(const char* stage, const h3_view* views, const size_t* need, 
   return H3_OK;
 }
 
+// The row kernels (quantizers, VSA rows) move 16 bytes (eight 16-bit channels) per access.
+int check_aligned16(const char* stage, std::initializer_list<h3_view> views) {
+  int i = 0;
+  for (const h3_view& v : views) {
+    if (reinterpret_cast<uintptr_t>(v.ptr) % 16 != 0)
+      return set_error(H3_ERR_ARGUMENT, "%s: binding %d is not 16-byte aligned", stage, i);
+    ++i;
+  }
+  return H3_OK;
+}
+
 // config.decl ... where [range(v, lo, hi), multiple_of(v, m)]: lo <= v <= hi, v % m == 0.
 bool in_range(uint32_t v, uint32_t lo, uint32_t hi, uint32_t multiple = 1) {
   return v >= lo && v <= hi && v % multiple == 0;
@@ -108,6 +119,7 @@ int prepare_common(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens
   size_t need[4] = {(size_t)tokens * cfg->row_stride * 2, mean.ptr ? (size_t)cfg->row_stride * 4 : 0,
                     rows_out * 128, rows_out * 4};
   if ((st = check_bindings(stage, views, need, 4))) return st;
+  if ((st = check_aligned16(stage, {x, mean}))) return st;
   if ((st = device_ready(stage))) return st;
   return launched(stage, launch_prepare_qk(*cfg, tokens, head_major, x.ptr,
                                            static_cast<const float*>(mean.ptr),
@@ -120,7 +132,8 @@ int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
   h3_view views[4] = {x, weight, cos_t, sin_t};
   size_t need[4] = {(size_t)tokens * cfg->row_stride * 2, 128 * 4, (size_t)tokens * 48 * 4,
                     (size_t)tokens * 48 * 4};
-  return check_bindings(stage, views, need, 4);
+  const int st = check_bindings(stage, views, need, 4);
+  return st ? st : check_aligned16(stage, {x, weight, cos_t, sin_t});
 }
 
 // Operand layouts of the attention kernels (attention.hip's modes).
@@ -239,16 +252,6 @@ int check_vsa_cfg(const char* stage, const h3_vsa_cfg* cfg) {
   return H3_OK;
 }
 
-// The row kernels move 16 bytes (eight f16 channels) per access.
-int check_aligned16(const char* stage, std::initializer_list<h3_view> views) {
-  int i = 0;
-  for (const h3_view& v : views) {
-    if (reinterpret_cast<uintptr_t>(v.ptr) % 16 != 0)
-      return set_error(H3_ERR_ARGUMENT, "%s: binding %d is not 16-byte aligned", stage, i);
-    ++i;
-  }
-  return H3_OK;
-}
 
 int transpose_common(const char* stage, const h3_transpose_cfg* cfg, uint32_t launch_rows,
                      uint32_t rows, h3_view x, h3_view out, hipStream_t stream, bool qkv) {
@@ -312,6 +315,7 @@ int h3_prepare_qk_i4(const h3_prepare_cfg* cfg, uint32_t tokens, h3_view x, h3_v
   size_t need[4] = {(size_t)tokens * cfg->row_stride * 2, mean.ptr ? (size_t)cfg->row_stride * 4 : 0,
                     rows_out * 64, rows_out * 4};
   if ((st = check_bindings(stage, views, need, 4))) return st;
+  if ((st = check_aligned16(stage, {x, mean}))) return st;
   if ((st = device_ready(stage))) return st;
   return launched(stage, launch_prepare_qk_i4(*cfg, tokens, x.ptr,
                                               static_cast<const float*>(mean.ptr),

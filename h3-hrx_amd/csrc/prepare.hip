@@ -1,8 +1,11 @@
 // Operand preparation for INT8 attention on gfx950: Hadamard-rotated per-(token, head) INT8
 // quantisation, the fused RMSNorm + RoPE variant, the f16 RoPE kernel, K column means and the
-// V transposes. All of these are HBM-bound byte work: each (token, head) row of 128 channels is
-// handled by one 32-lane half of a wave64 (four channels per lane, one 8-byte load per lane),
-// so a 256-thread workgroup covers eight rows and every global access is a full 256-byte row.
+// V transposes. All of these are HBM-bound byte work. In the quantizers each (token, head) row of
+// 128 channels is held by a 16-lane group (a DPP row; eight channels per lane, one 16-byte load
+// per lane), a 256-thread workgroup holds sixteen rows at a time and every global access is a
+// whole 256-byte row; several rows per group are loaded before any is processed, to keep enough
+// bytes in flight. The f16 RoPE kernel and the column means use 32-lane halves (four channels
+// per lane) with the same arithmetic.
 //
 // The arithmetic is built with -ffp-contract=off: every float operation below is one IEEE
 // operation in the order written, which is what makes the quantizer bit-exact with the
@@ -13,8 +16,8 @@ namespace h3 {
 namespace {
 
 constexpr int kRowsPerBlock = 8;  // 256 threads = 8 half-waves = 8 (token, head) rows
-// Rows per half-wave in the quantizers: their loads are issued together before any row is
-// processed, so each half-wave keeps kRowsAhead 256-byte rows in flight (one row is far too few
+// Rows per 16-lane group in the quantizers: their loads are issued together before any row is
+// processed, so each group keeps kRowsAhead 256-byte rows in flight (one row is far too few
 // bytes in flight to cover HBM latency at these kernels' occupancy).
 constexpr int kRowsAhead = 4;
 
@@ -43,8 +46,7 @@ __device__ __forceinline__ void pair16(float v, float& lo, float& hi) {
   lo = __uint_as_float(r[0]);
   hi = __uint_as_float(r[1]);
 }
-// Sum and max over the 32 lanes of a half-wave in the order k = 1, 2, 4, 8, 16 (sum) and any
-// order (max); every lane gets the result.
+// Sum over the 32 lanes of a half-wave in the order k = 1, 2, 4, 8, 16; every lane gets it.
 __device__ __forceinline__ float half_sum(float v) {
 #pragma unroll
   for (int k = 1; k < 16; k <<= 1) v = v + xor_partner(v, k);
@@ -52,76 +54,101 @@ __device__ __forceinline__ float half_sum(float v) {
   pair16(v, lo, hi);
   return lo + hi;
 }
-__device__ __forceinline__ float half_max(float v) {
-  float lo, hi;
-  pair16(v, lo, hi);
-  v = fmaxf(lo, hi);
+
+// ---------------------------------------------------------------- 16-lane row groups
+// The quantizers hold one 128-channel row in a 16-lane group (a DPP row), eight channels per
+// lane, read with one 16-byte load per lane. Partner exchanges k = 1, 2, 4, 8 are the DPP moves
+// of xor_partner, which stay inside a DPP row.
+__device__ __forceinline__ float row16_sum(float v) {  // order k = 1, 2, 4, 8
+#pragma unroll
+  for (int k = 1; k < 16; k <<= 1) v = v + xor_partner(v, k);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
 #pragma unroll
   for (int k = 8; k >= 1; k >>= 1) v = fmaxf(v, xor_partner(v, k));
   return v;
 }
 
-// The unnormalised Sylvester Hadamard H_128 over the 32 lanes of a half-wave, lane l holding
-// elements 4l..4l+3, in the reference's fp32 order (kernels/prepare_qk_i8.loom:84-156):
-// an in-lane stage over element bits 0-1, then lane butterflies k = 1, 2, 4, 8, 16 where the
-// lane with bit k clear keeps s + partner and the lane with bit k set keeps partner - s.
-// Each lane stage computes fma(s, sign, p) with sign = +1 (bit clear: s + p) or -1 (bit set:
-// p - s): one correctly rounded addition either way, so the bits are those of the reference.
-__device__ __forceinline__ v4f hadamard128(v4f y, int lane) {
-  float ab_p = y[0] + y[1], ab_m = y[0] - y[1];
-  float cd_p = y[2] + y[3], cd_m = y[2] - y[3];
-  v4f s;
-  s[0] = ab_p + cd_p;
-  s[1] = ab_m + cd_m;
-  s[2] = ab_p - cd_p;
-  s[3] = ab_m - cd_m;
-#pragma unroll
-  for (int k = 1; k < 16; k <<= 1) {
-    const float sign = (lane & k) ? -1.0f : 1.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = __builtin_fmaf(s[j], sign, xor_partner(s[j], k));
-  }
-  const float sign16 = (lane & 16) ? -1.0f : 1.0f;
+// Eight 16-bit activations (f16 or bf16 bit patterns) widened to f32 exactly.
+__device__ __forceinline__ void widen8(uint4 b, int elem, float (&v)[8]) {
+  const v4f lo = widen4(make_uint2(b.x, b.y), elem), hi = widen4(make_uint2(b.z, b.w), elem);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float lo, hi;
-    pair16(s[j], lo, hi);  // bit clear: lo + hi = s + p; bit set: lo - hi = p - s
-    s[j] = __builtin_fmaf(hi, sign16, lo);
+    v[j] = lo[j];
+    v[4 + j] = hi[j];
   }
-  return s;
 }
 
-// Quantise one rotated row (kernels/prepare_qk_i8.loom:157-188): amax over the half-wave,
-// sc = amax/127, inv = 127/amax (correctly rounded divisions), codes = clamp(rne(r*inv), +-127)
-// packed low byte first. Returns the packed word of this lane; *scale gets amax/127 * extra.
-__device__ __forceinline__ uint32_t quantize_row(v4f r, float extra, float* scale) {
-  float m = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
-  m = half_max(m);
-  float amax = fmaxf(m, 1.0000000000000001e-30f);
-  float sc = amax / 127.0f;
-  float inv = 127.0f / amax;
-  uint32_t word = 0;
+// The unnormalised Sylvester Hadamard H_128, lane l of a 16-lane group holding elements
+// 8l..8l+7, in the reference's fp32 order (kernels/prepare_qk_i8.loom:84-156). The reference
+// holds four elements per lane: an in-lane stage over element bits 0-1, then lane butterflies
+// over lane bits 1, 2, 4, 8, 16 (element bits 2-6), where the element with the bit clear keeps
+// s + partner and the one with the bit set keeps partner - s. Here element bit 2 lies inside
+// the lane and the same two sums are formed there; element bits 3-6 are lane bits 1, 2, 4, 8.
+// Every result is one correctly rounded addition or subtraction of the same two operands as in
+// the reference, so the bits are the reference's.
+__device__ __forceinline__ void hadamard128(float (&s)[8], int l) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int g = 0; g < 2; ++g) {
+    const float ab_p = s[4 * g] + s[4 * g + 1], ab_m = s[4 * g] - s[4 * g + 1];
+    const float cd_p = s[4 * g + 2] + s[4 * g + 3], cd_m = s[4 * g + 2] - s[4 * g + 3];
+    s[4 * g] = ab_p + cd_p;
+    s[4 * g + 1] = ab_m + cd_m;
+    s[4 * g + 2] = ab_p - cd_p;
+    s[4 * g + 3] = ab_m - cd_m;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // element bit 2: s + partner (bit clear), partner - s (set)
+    const float p = s[j] + s[j + 4], m = s[j] - s[j + 4];
+    s[j] = p;
+    s[j + 4] = m;
+  }
+#pragma unroll
+  for (int k = 1; k < 16; k <<= 1) {  // element bits 3-6; fma(s, -1, p) is p - s exactly
+    const float sign = (l & k) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = __builtin_fmaf(s[j], sign, xor_partner(s[j], k));
+  }
+}
+
+// Quantise one rotated row (kernels/prepare_qk_i8.loom:157-188): amax over the group,
+// sc = amax/127, inv = 127/amax (correctly rounded divisions), codes = clamp(rne(r*inv), +-127)
+// packed low byte first. Returns this lane's two words (elements 8l..8l+3, 8l+4..8l+7); *scale
+// gets amax/127 * extra.
+__device__ __forceinline__ uint2 quantize_row(const float (&r)[8], float extra, float* scale) {
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(r[j]));
+  m = row16_max(m);
+  const float amax = fmaxf(m, 1.0000000000000001e-30f);
+  const float sc = amax / 127.0f;
+  const float inv = 127.0f / amax;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
     float q = __builtin_rintf(r[j] * inv);
     q = fminf(fmaxf(q, -127.0f), 127.0f);
-    word |= ((uint32_t)(int)q & 0xffu) << (8 * j);
+    w[j / 4] |= ((uint32_t)(int)q & 0xffu) << (8 * (j % 4));
   }
   *scale = sc * extra;
-  return word;
+  return make_uint2(w[0], w[1]);
 }
 
 // The int4 form (kernels/prepare_qk_i4.loom:174-214): amax/7 scales, codes clamp(rne(r*7/amax),
-// +-7) as nibbles; returns this lane's four codes in the low 16 bits (low nibble first).
-__device__ __forceinline__ uint32_t quantize_row_i4(v4f r, float extra, float* scale) {
-  float m = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
-  m = half_max(m);
-  float amax = fmaxf(m, 1.0000000000000001e-30f);
-  float sc = amax / 7.0f;
-  float inv = 7.0f / amax;
+// +-7) as nibbles; returns this lane's eight codes as one word (low nibble first).
+__device__ __forceinline__ uint32_t quantize_row_i4(const float (&r)[8], float extra,
+                                                    float* scale) {
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(r[j]));
+  m = row16_max(m);
+  const float amax = fmaxf(m, 1.0000000000000001e-30f);
+  const float sc = amax / 7.0f;
+  const float inv = 7.0f / amax;
   uint32_t bits = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 8; ++j) {
     float q = __builtin_rintf(r[j] * inv);
     q = fminf(fmaxf(q, -7.0f), 7.0f);
     bits |= ((uint32_t)(int)q & 0xfu) << (4 * j);
@@ -194,8 +221,78 @@ __device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* we
   return rmsnorm_rope_f16(v, lane, rope_lane(lane, weight, cos_row, sin_row), eps);
 }
 
+// The same RMSNorm + RoPE for a row held eight channels per lane by a 16-lane group (the
+// quantizers' layout), bit for bit: the lane partial is the sum of the two four-channel partials
+// of the layout above (that layout's first butterfly step, k = 1, adds exactly those two), then
+// butterflies k = 1, 2, 4, 8 here are its k = 2, 4, 8, 16; the rotation partner is lane l +- 6.
+struct RopeLane8 {
+  float w[8], c[8], s[8];
+};
+
+__device__ __forceinline__ RopeLane8 rope_lane8(int l, const float* weight, const float* cos_row,
+                                                const float* sin_row) {
+  const int pairlane = l < 6 ? l : (l < 12 ? l - 6 : 0);
+  RopeLane8 t;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float4 w = *reinterpret_cast<const float4*>(weight + 8 * l + 4 * h);
+    const float4 c = *reinterpret_cast<const float4*>(cos_row + 8 * pairlane + 4 * h);
+    const float4 sn = *reinterpret_cast<const float4*>(sin_row + 8 * pairlane + 4 * h);
+    t.w[4 * h] = w.x; t.w[4 * h + 1] = w.y; t.w[4 * h + 2] = w.z; t.w[4 * h + 3] = w.w;
+    t.c[4 * h] = c.x; t.c[4 * h + 1] = c.y; t.c[4 * h + 2] = c.z; t.c[4 * h + 3] = c.w;
+    t.s[4 * h] = sn.x; t.s[4 * h + 1] = sn.y; t.s[4 * h + 2] = sn.z; t.s[4 * h + 3] = sn.w;
+  }
+  return t;
+}
+
+__device__ __forceinline__ void rmsnorm_rope_f16(float (&v)[8], int l, const RopeLane8& tab,
+                                                 float eps) {
+  const float p0 = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
+  const float p1 = ((v[4] * v[4] + v[5] * v[5]) + v[6] * v[6]) + v[7] * v[7];
+  const float part = row16_sum(p0 + p1);
+  const float ms = part * 0.0078125f;
+  const float me = ms + eps;
+  const float r = 1.0f / __builtin_sqrtf(me);
+  float xn[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) xn[j] = (v[j] * r) * tab.w[j];
+  const bool lo = l < 6, pair = l < 12;
+  const int partner = lo ? l + 6 : (pair ? l - 6 : l);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float px = __shfl(xn[j], partner, 16);
+    const float a = xn[j] * tab.c[j];
+    const float b = px * tab.s[j];
+    float o = lo ? (a - b) : (a + b);
+    o = pair ? o : xn[j];
+    v[j] = (float)(_Float16)o;
+  }
+}
+
 // ---------------------------------------------------------------- quantizer kernels
 
+constexpr int kGroupsPerBlock = 16;  // 256 threads = 16 row groups of 16 lanes
+
+__device__ __forceinline__ uint4 load8(const void* base, size_t elem_index) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + elem_index);
+}
+
+__device__ __forceinline__ void subtract_mean(float (&y)[8], const float* mean, uint32_t col) {
+  if (!mean) return;
+  const float4 a = *reinterpret_cast<const float4*>(mean + col);
+  const float4 b = *reinterpret_cast<const float4*>(mean + col + 4);
+  y[0] = y[0] - a.x;
+  y[1] = y[1] - a.y;
+  y[2] = y[2] - a.z;
+  y[3] = y[3] - a.w;
+  y[4] = y[4] - b.x;
+  y[5] = y[5] - b.y;
+  y[6] = y[6] - b.z;
+  y[7] = y[7] - b.w;
+}
+
+// (token, head) rows, one per 16-lane group; group g of block b takes rows
+// b*16*kRowsAhead + 16i + g, i < kRowsAhead, all loads issued before the first row is processed.
 template <bool kHeadMajor>
 __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
                                                     const float* __restrict__ mean,
@@ -204,47 +301,39 @@ __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
                                                     uint32_t row_stride, uint32_t head_offset,
                                                     uint32_t heads, uint32_t capacity,
                                                     float extra, uint32_t elem) {
-  // Half-wave g of block b takes rows b*8*kRowsAhead + 8i + g, i < kRowsAhead: for each i the
-  // block's eight half-waves cover eight consecutive rows.
-  const uint32_t first = blockIdx.x * kRowsPerBlock * kRowsAhead + (threadIdx.x >> 5);
-  const int lane = threadIdx.x & 31;
+  const uint32_t first = blockIdx.x * kGroupsPerBlock * kRowsAhead + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
   const uint32_t total = tokens * heads;
-  uint2 in[kRowsAhead];
+  uint4 in[kRowsAhead];
 #pragma unroll
   for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kRowsPerBlock * i;
+    const uint32_t row = first + kGroupsPerBlock * i;
     if (row >= total) break;
     // head-major rows walk tokens fastest (contiguous code stores), token-major rows walk heads
     const uint32_t t = kHeadMajor ? row % tokens : row / heads;
     const uint32_t h = kHeadMajor ? row / tokens : row % heads;
-    in[i] = load4(x, (size_t)t * row_stride + head_offset + 128u * h + 4u * lane);
+    in[i] = load8(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
   }
 #pragma unroll
   for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kRowsPerBlock * i;
+    const uint32_t row = first + kGroupsPerBlock * i;
     if (row >= total) break;
     const uint32_t t = kHeadMajor ? row % tokens : row / heads;
     const uint32_t h = kHeadMajor ? row / tokens : row % heads;
-    const uint32_t col = head_offset + 128u * h + 4u * lane;
-    v4f y = widen4(in[i], elem);
-    if (mean) {
-      const float4 m = *reinterpret_cast<const float4*>(mean + col);
-      y[0] = y[0] - m.x;
-      y[1] = y[1] - m.y;
-      y[2] = y[2] - m.z;
-      y[3] = y[3] - m.w;
-    }
-    v4f r = hadamard128(y, lane);
+    float y[8];
+    widen8(in[i], elem, y);
+    subtract_mean(y, mean, head_offset + 128u * h + 8u * l);
+    hadamard128(y, l);
     float scale;
-    uint32_t word = quantize_row(r, extra, &scale);
-    size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
-    codes[out_row * 32 + lane] = (int32_t)word;
-    if (lane == 0) scales[out_row] = scale;
+    const uint2 w = quantize_row(y, extra, &scale);
+    const size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
+    reinterpret_cast<uint2*>(codes + out_row * 32)[l] = w;
+    if (l == 0) scales[out_row] = scale;
   }
 }
 
-// int4 operands, token-major (kernels/prepare_qk_i4.loom): the same rotation, 16 bits of codes
-// per lane; the even lane of each pair writes the word of both (codes [tokens][heads*16] i32).
+// int4 operands, token-major (kernels/prepare_qk_i4.loom): the same rotation; a lane's eight
+// codes are one word of the row (codes [tokens][heads*16] i32).
 __global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ x,
                                                        const float* __restrict__ mean,
                                                        int32_t* __restrict__ codes,
@@ -252,81 +341,69 @@ __global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ 
                                                        uint32_t tokens, uint32_t row_stride,
                                                        uint32_t head_offset, uint32_t heads,
                                                        float extra, uint32_t elem) {
-  const uint32_t first = blockIdx.x * kRowsPerBlock * kRowsAhead + (threadIdx.x >> 5);
-  const int lane = threadIdx.x & 31;
+  const uint32_t first = blockIdx.x * kGroupsPerBlock * kRowsAhead + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
   const uint32_t total = tokens * heads;
-  uint2 in[kRowsAhead];
+  uint4 in[kRowsAhead];
 #pragma unroll
   for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kRowsPerBlock * i;
+    const uint32_t row = first + kGroupsPerBlock * i;
     if (row >= total) break;
     const uint32_t t = row / heads, h = row % heads;
-    in[i] = load4(x, (size_t)t * row_stride + head_offset + 128u * h + 4u * lane);
+    in[i] = load8(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
   }
 #pragma unroll
   for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kRowsPerBlock * i;
+    const uint32_t row = first + kGroupsPerBlock * i;
     if (row >= total) break;
     const uint32_t h = row % heads;
-    const uint32_t col = head_offset + 128u * h + 4u * lane;
-    v4f y = widen4(in[i], elem);
-    if (mean) {
-      const float4 m = *reinterpret_cast<const float4*>(mean + col);
-      y[0] = y[0] - m.x;
-      y[1] = y[1] - m.y;
-      y[2] = y[2] - m.z;
-      y[3] = y[3] - m.w;
-    }
-    v4f r = hadamard128(y, lane);
+    float y[8];
+    widen8(in[i], elem, y);
+    subtract_mean(y, mean, head_offset + 128u * h + 8u * l);
+    hadamard128(y, l);
     float scale;
-    const uint32_t bits = quantize_row_i4(r, extra, &scale);
-    const uint32_t odd = (uint32_t)__builtin_amdgcn_mov_dpp((int)bits, 0xB1, 0xF, 0xF, true);
-    if ((lane & 1) == 0) codes[(size_t)row * 16 + lane / 2] = (int32_t)(bits | (odd << 16));
-    if (lane == 0) scales[row] = scale;
+    codes[(size_t)row * 16 + l] = (int32_t)quantize_row_i4(y, extra, &scale);
+    if (l == 0) scales[row] = scale;
   }
 }
 
 // RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
 // (kernels/prepare_qk_rope_i8hm.loom:94-239; mean == nullptr is the reference's unsmoothed
-// kernel, a mean is this build's fused K-smoothing second pass). One half-wave owns one token and
-// walks its heads: the token's RoPE tables are read once (not once per head), its heads' inputs
-// are one contiguous run of the fused row, and the eight half-waves of a workgroup write eight
-// consecutive head-major rows (1 KiB) per head.
+// kernel, a mean is this build's fused K-smoothing second pass). One 16-lane group owns one token
+// and walks its heads with kRowsAhead heads in flight: the token's RoPE tables are read once
+// (not once per head), its heads' inputs are one contiguous run of the fused row, and the 16
+// groups of a workgroup write 16 consecutive head-major rows (2 KiB) per head.
 __global__ __launch_bounds__(256) void k_prepare_qk_rope(
     const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const float* __restrict__ mean, int32_t* __restrict__ codes,
     float* __restrict__ scales, uint32_t tokens, uint32_t row_stride, uint32_t head_offset,
     uint32_t heads, uint32_t capacity, float extra, float eps, uint32_t elem) {
-  const uint32_t t = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
-  const int lane = threadIdx.x & 31;
+  const uint32_t t = blockIdx.x * kGroupsPerBlock + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
   if (t >= tokens) return;
-  const RopeLane tab = rope_lane(lane, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48);
-  const size_t row0 = (size_t)t * row_stride + head_offset + 4u * lane;
-  uint2 ring[kRowsAhead];  // heads h .. h + kRowsAhead - 1 in flight
+  const RopeLane8 tab = rope_lane8(l, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48);
+  const size_t row0 = (size_t)t * row_stride + head_offset + 8u * l;
+  uint4 ring[kRowsAhead];  // heads h .. h + kRowsAhead - 1 in flight
 #pragma unroll
   for (int i = 0; i < kRowsAhead; ++i)
-    if ((uint32_t)i < heads) ring[i] = load4(x, row0 + 128u * i);
-  for (uint32_t h0 = 0; h0 < heads; h0 += kRowsAhead)
+    if ((uint32_t)i < heads) ring[i] = load8(x, row0 + 128u * i);
+  for (uint32_t h0 = 0; h0 < heads; h0 += kRowsAhead) {
 #pragma unroll
-  for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t h = h0 + i;
-    if (h >= heads) break;
-    const v4f v = widen4(ring[i], elem);
-    if (h + kRowsAhead < heads) ring[i] = load4(x, row0 + 128u * (h + kRowsAhead));
-    v4f y = rmsnorm_rope_f16(v, lane, tab, eps);
-    if (mean) {
-      const float4 m = *reinterpret_cast<const float4*>(mean + 128u * h + 4u * lane);
-      y[0] = y[0] - m.x;
-      y[1] = y[1] - m.y;
-      y[2] = y[2] - m.z;
-      y[3] = y[3] - m.w;
+    for (int i = 0; i < kRowsAhead; ++i) {
+      const uint32_t h = h0 + i;
+      if (h >= heads) break;
+      float y[8];
+      widen8(ring[i], elem, y);
+      if (h + kRowsAhead < heads) ring[i] = load8(x, row0 + 128u * (h + kRowsAhead));
+      rmsnorm_rope_f16(y, l, tab, eps);
+      subtract_mean(y, mean, 128u * h + 8u * l);
+      hadamard128(y, l);
+      float scale;
+      const uint2 w = quantize_row(y, extra, &scale);
+      const size_t out_row = (size_t)h * capacity + t;
+      reinterpret_cast<uint2*>(codes + out_row * 32)[l] = w;
+      if (l == 0) scales[out_row] = scale;
     }
-    v4f r = hadamard128(y, lane);
-    float scale;
-    uint32_t word = quantize_row(r, extra, &scale);
-    size_t out_row = (size_t)h * capacity + t;
-    codes[out_row * 32 + lane] = (int32_t)word;
-    if (lane == 0) scales[out_row] = scale;
   }
 }
 
@@ -497,7 +574,7 @@ hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int hea
                              const void* x, const float* mean, int32_t* codes, float* scales,
                              hipStream_t stream) {
   const uint32_t rows = tokens * cfg.heads;
-  dim3 grid(div_up(rows, kRowsPerBlock * kRowsAhead));
+  dim3 grid(div_up(rows, kGroupsPerBlock * kRowsAhead));
   if (head_major)
     hipLaunchKernelGGL(k_prepare_qk<true>, grid, dim3(256), 0, stream, x, mean, codes, scales,
                        tokens, cfg.row_stride, cfg.head_offset, cfg.heads, cfg.token_capacity,
@@ -513,7 +590,7 @@ hipError_t launch_prepare_qk_i4(const h3_prepare_cfg& cfg, uint32_t tokens, cons
                                 const float* mean, int32_t* codes, float* scales,
                                 hipStream_t stream) {
   const uint32_t rows = tokens * cfg.heads;
-  hipLaunchKernelGGL(k_prepare_qk_i4, dim3(div_up(rows, kRowsPerBlock * kRowsAhead)), dim3(256),
+  hipLaunchKernelGGL(k_prepare_qk_i4, dim3(div_up(rows, kGroupsPerBlock * kRowsAhead)), dim3(256),
                      0, stream, x, mean, codes, scales, tokens, cfg.row_stride, cfg.head_offset,
                      cfg.heads, cfg.extra_scale, cfg.elem);
   return hipGetLastError();
@@ -530,7 +607,7 @@ hipError_t launch_prepare_qk_rope_mean(const h3_prepare_cfg& cfg, uint32_t token
                                        const float* weight, const float* cos_t,
                                        const float* sin_t, const float* mean, int32_t* codes,
                                        float* scales, hipStream_t stream) {
-  hipLaunchKernelGGL(k_prepare_qk_rope, dim3(div_up(tokens, kRowsPerBlock)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(k_prepare_qk_rope, dim3(div_up(tokens, kGroupsPerBlock)), dim3(256), 0, stream,
                      x, weight, cos_t, sin_t, mean, codes, scales, tokens, cfg.row_stride,
                      cfg.head_offset, cfg.heads, cfg.token_capacity, cfg.extra_scale, cfg.eps,
                      cfg.elem);
