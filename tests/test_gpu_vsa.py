@@ -407,3 +407,74 @@ def test_runtime_at_config3_grid_on_sampled_rows(dev):
     tok = src[qrows]
     assert np.array_equal(from_dev(out.view(-1)).reshape(seq, w)[tok], gathered[qrows])
     vsa.close()
+
+
+def test_runtime_with_prefix_segments_layers_and_gate(dev):
+    """A DiT-like layout: 300 text rows and 20 audio rows as prefix segments, then an 8 x 10 x 12
+    video grid (clipped cubes at h), two heads, two layers with their own K means, keep 25 %.
+    Every buffer of the runtime equals the oracle pipeline's bit for bit where the reference's
+    arithmetic is fixed (gathered rows, means, scores, routes, operands, K means); the output is
+    within the north-star tolerance of the f64 attention of the runtime's own operands, plain
+    and gated."""
+    import torch
+
+    heads = 2
+    w = heads * 128
+    segs = [(0, 300), (300, 20)]
+    nt, nh, nw = 8, 10, 12
+    seq = 320 + nt * nh * nw
+    src, inverse, lengths, prefix = H.vsa_plan(segs, seq, nt, nh, nw)
+    n, nb = len(src), len(lengths)
+    rng = np.random.default_rng(21)
+    data = [O.f16_bits(rng.standard_normal((seq, w)).astype(np.float32)).reshape(seq, w)
+            for _ in range(3)]
+    data[1] = O.f16_bits((data[1].view(np.float16).astype(np.float32)
+                          + rng.standard_normal(w).astype(np.float32) * 1.4)).reshape(seq, w)
+    gates = O.f16_bits(rng.standard_normal((seq, w)).astype(np.float32) * 0.5).reshape(seq, w)
+    opts = H.VsaOptions(keep_percent=25.0)
+    vsa = H.Vsa(src, inverse, lengths, prefix, heads, opts, layers=2)
+    q, k, v = (torch_f16(d, dev) for d in data)
+    out = torch.zeros((seq * w,), dtype=torch.int16, device=dev)
+    print(f"vsa runtime prefix={prefix} blocks={nb}", flush=True)
+    means = [np.zeros(w, np.float32), np.zeros(w, np.float32)]
+    topk = O.vsa_topk(25.0, nb - prefix)
+    for call, layer in enumerate([0, 1, 0]):
+        gate = torch_f16(gates, dev) if call == 2 else None
+        vsa.attend(layer, q, k, v, out, gate=gate)
+        b = vsa.buffers(layer)
+        gq = read(b.q, np.uint16, (n, w))
+        gk = read(b.k, np.uint16, (n, w))
+        assert np.array_equal(gq, O.vsa_gather(src, seq, data[0]))
+        km = read(b.km, np.float32, (nb, w))
+        qm = read(b.qm, np.float32, (nb, w))
+        assert np.array_equal(km.view(np.uint32), O.vsa_pool(lengths, gk).view(np.uint32))
+        scores = read(b.scores, np.float32, (heads, nb, nb))
+        assert np.array_equal(scores.view(np.uint32), O.vsa_scores(qm, km, heads).view(np.uint32))
+        routes = read(b.routes, np.int32, (heads, nb, nb))
+        assert np.array_equal(routes, O.vsa_route(scores, prefix, topk))
+        kw, ksc = O.prepare_qk(gk, O.F16, means[layer], n, w, 0, heads, 1.0)
+        assert np.array_equal(read(b.ki, np.int32, (n, heads * 32)), kw)
+        assert np.array_equal(read(b.ks, np.float32, (n, heads)).view(np.uint32),
+                              ksc.view(np.uint32))
+        means[layer] = O.vsa_kmean(km)
+        assert np.array_equal(read(b.kmean, np.float32, (w,)).view(np.uint32),
+                              means[layer].view(np.uint32))
+        rows = np.arange(n, dtype=np.int32)
+        att = O.vsa_attention_f64(read(b.qi, np.int8, (n, w)), read(b.qs, np.float32, (n, heads)),
+                                  read(b.ki, np.int8, (n, w)), read(b.ks, np.float32, (n, heads)),
+                                  read(b.vt, np.uint16, (w, n)), n, n, heads, routes, lengths,
+                                  rows).reshape(n, w)
+        fine = read(b.out, np.uint16, (n, w))
+        live = src >= 0
+        mx, mean = north_star_ok(fine[live].view(np.float16).astype(np.float32), att[live])
+        assert mx < 2e-2 and mean < 2e-3, (call, mx, mean)
+        got = from_dev(out).reshape(seq, w)
+        if gate is None:
+            assert np.array_equal(got, fine[inverse])
+        else:
+            vm = O.vsa_pool(lengths, read(b.v, np.uint16, (n, w)))
+            coarse = O.vsa_coarse_f64(scores, vm).astype(np.float32)
+            want = O.vsa_gated_scatter(inverse, fine, gates, coarse)
+            diff = np.abs(got.view(np.float16).astype(np.float32) - want.view(np.float16).astype(np.float32))
+            assert diff.max() < 1e-2, diff.max()
+    vsa.close()
