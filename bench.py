@@ -170,6 +170,30 @@ class TextCross:
                                       self.mask, self.out)
 
 
+def platform_flash(torch, dev, tokens, heads, dense_ms):
+    """The platform's own attention at the same shape for scale: torch's scaled_dot_product_attention
+    in f16 (its flash backend on ROCm), f16 Q/K/V [1][heads][tokens][128] N(0,1), timed with HIP
+    events. Not part of the step; f16 QK and PV, so not the same arithmetic."""
+    import torch.nn.functional as F
+
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+    except ImportError:
+        return None
+    g = torch.Generator(device=dev).manual_seed(5)
+    shape = (1, heads, tokens, 128)
+    q, k, v = (torch.randn(shape, generator=g, device=dev, dtype=torch.float16) for _ in range(3))
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            ms = time_launches(torch, lambda: F.scaled_dot_product_attention(q, k, v), 2)
+    except RuntimeError as e:  # backend unavailable on this build
+        return {"error": str(e)[:120]}
+    ops = 4.0 * tokens * tokens * heads * 128
+    return {"kernel": "torch scaled_dot_product_attention, FLASH_ATTENTION backend, f16",
+            "ms": round(ms, 3), "tflops": round(ops / (ms * 1e-3) / 1e12, 1),
+            "int8_path_speedup": round(ms / dense_ms, 2)}
+
+
 def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
     """The VSA block-sparse path (BASELINE config 5b; src/vsa.rs, src/vsa/device.rs) at the same
     shape: the plan of the latent grid in 4x4x4 cubes (no prefix segments), the reference's
@@ -446,6 +470,9 @@ def main() -> None:
             "ms": round(cross_ms, 4),
             "tops": round(text.ops / (cross_ms * 1e-3) / 1e12, 1),
             "frac_int8_peak": round(text.ops / (cross_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+        print("# platform attention...", file=sys.stderr, flush=True)
+        line["adjacent_kernels"]["platform_flash_f16"] = platform_flash(torch, dev, tokens, heads,
+                                                                        att_avg)
         print("# vsa path...", file=sys.stderr, flush=True)
         line["adjacent_kernels"]["vsa"] = vsa_path(torch, H, dev, tokens, heads, grid, fused_bf16,
                                                    att_avg)
