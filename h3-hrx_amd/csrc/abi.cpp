@@ -206,15 +206,20 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
     size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
     if ((st = check_bindings(stage, rv, rneed, 2))) return st;
     if ((st = device_ready(stage))) return st;
-    return launched(stage, launch_attention_vsa(*cfg, token_count, heads,
-                                                static_cast<const int32_t*>(qi.ptr),
-                                                static_cast<const float*>(qs.ptr),
-                                                static_cast<const int32_t*>(ki.ptr),
-                                                static_cast<const float*>(ks.ptr),
-                                                static_cast<const uint16_t*>(vt.ptr),
-                                                static_cast<uint16_t*>(out.ptr),
-                                                static_cast<const int32_t*>(routes.ptr),
-                                                static_cast<const int32_t*>(lengths.ptr), stream));
+    // The per-segment softmax states live in a stream-ordered allocation: it is taken and given
+    // back in the order of `stream`, so calls on different streams never share it.
+    void* workspace = nullptr;
+    hipError_t e = hipMallocAsync(&workspace, vsa_workspace_bytes(token_count, heads), stream);
+    if (e != hipSuccess) return launched(stage, e);
+    e = launch_attention_vsa(*cfg, token_count, heads, static_cast<const int32_t*>(qi.ptr),
+                             static_cast<const float*>(qs.ptr),
+                             static_cast<const int32_t*>(ki.ptr),
+                             static_cast<const float*>(ks.ptr),
+                             static_cast<const uint16_t*>(vt.ptr), static_cast<uint16_t*>(out.ptr),
+                             static_cast<const int32_t*>(routes.ptr),
+                             static_cast<const int32_t*>(lengths.ptr), workspace, stream);
+    const hipError_t ef = hipFreeAsync(workspace, stream);
+    return launched(stage, e != hipSuccess ? e : ef);
   }
   if ((st = device_ready(stage))) return st;
   return launched(stage, launch_attention(*cfg, mode, skip_tau, token_count, heads,

@@ -47,6 +47,8 @@
 // Semantics follow kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:437-1067 (head-major)
 // and kernels/attention_i8qk_family.loom:193-424 (token-major): non-causal MHA, keys >= tokens
 // masked, rows >= token_count not written, f16 output [token_count][out_stride].
+#include <algorithm>
+
 #include "internal.hpp"
 
 namespace h3 {
@@ -70,9 +72,8 @@ constexpr int kSRows = kKeys / kWaves;                      // scale rows stored
 // Operand layouts: int8 codes token-major (attention_i8qk_*) or head-major (attention_i8qkhm_*),
 // and int4 codes token-major (attention_i4qk_*, eight codes per word, low nibble first).
 // kTokenI4Skip is the int4 kernel with the tile skip of attention_i4qks_* (a threshold tau).
-// kTokenI8Vsa is the int8 token-major kernel walking only the key cubes that the VSA routes
-// keep (vsa_attention_8), see k_attention_vsa.
-enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2, kTokenI4Skip = 3, kTokenI8Vsa = 4 };
+// The int8 token-major layout is also that of the VSA kernel (k_attention_vsa).
+enum Mode { kTokenI8 = 0, kHeadI8 = 1, kTokenI4 = 2, kTokenI4Skip = 3 };
 constexpr bool isI4(int mode) { return mode == kTokenI4 || mode == kTokenI4Skip; }
 constexpr int kI4RowBytes = 64;                             // int4 K tile rows in LDS
 constexpr int kKRowsOf(int mode) { return isI4(mode) ? kKeys * kI4RowBytes : kKRows; }
@@ -120,9 +121,13 @@ struct Args {
   uint32_t q_tokens;        // k_attention_cross: query rows (tokens counts the keys)
   uint32_t q_capacity;      // k_attention_cross: head-major row capacity of qi / qs
   uint32_t kv_group;        // k_attention_cross: query heads per key/value head
-  const int32_t* routes;   // kTokenI8Vsa: [head_limit][blocks][blocks], nonzero = kept
-  const int32_t* lengths;  // kTokenI8Vsa: live keys of each 64-key cube
-  uint32_t blocks;         // kTokenI8Vsa: tokens / 64
+  const int32_t* routes;   // k_attention_vsa: [head_limit][blocks][blocks], nonzero = kept
+  const int32_t* lengths;  // k_attention_vsa: live keys of each 64-key cube
+  uint32_t blocks;         // k_attention_vsa: tokens / 64
+  uint32_t base;           // k_attention_vsa: first (head, cube) item of this launch
+  uint32_t segs;           // k_attention_vsa: key segments per item
+  uint16_t* part_o;        // k_attention_vsa: per (item, segment) 64 rows of O / l, f16
+  float* part_ml;          // k_attention_vsa: per (item, segment) 64 rows of (running max, sum)
 };
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
@@ -181,14 +186,12 @@ __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane)
 
 // LDS-DMA of K tile k0 (rows past the sequence load as zero) into stage `kst`, and the load of
 // its scales into a register.
-// live_keys >= 0 overrides the keys of the tile that are read (the rest load as zero).
 template <int kMode>
 __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32_t kv_head,
-                                         uint32_t k0, char* kst, int live_keys = -1) {
+                                         uint32_t k0, char* kst) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
   constexpr uint32_t kCodeBytes = isI4(kMode) ? 64 : 128;  // code bytes per (key, head)
-  const uint32_t live = live_keys >= 0 ? (uint32_t)live_keys
-                        : a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
+  const uint32_t live = a.tokens > k0 ? min(a.tokens - k0, (uint32_t)kKeys) : 0u;
   const char* base;
   uint32_t bytes;
   const float* sbase;
@@ -237,17 +240,6 @@ __device__ __forceinline__ void store_scales(char* kst, const Stager& sg, float 
   }
 }
 
-// The same for a tile whose keys from `live` on are dead: their pair is (ks, -inf), so the
-// dequantized score acc*ks - inf is -inf and its probability exp2(-inf) is 0. The mask costs
-// nothing in the key loop.
-__device__ __forceinline__ void store_scales_live(char* kst, const Stager& sg, float ks,
-                                                  uint32_t live) {
-  if ((threadIdx.x & 63) < kSRows) {
-    float* sc = reinterpret_cast<float*>(kst + kKRows);
-    sc[sg.srow] = ks;
-    sc[kKeys + sg.srow] = swap23(sg.srow) < live ? -(kMagic * ks) : -INFINITY;
-  }
-}
 
 // Barrier between pipeline steps: this wave's LDS writes, and its staging loads from before the
 // current step, are complete; the loads issued in this step stay in flight.
@@ -424,16 +416,14 @@ __device__ __forceinline__ void first_tile(const char* kst, const v4i (&qop)[4],
 //   kst    LDS stage of K(j+1) (unused when !kNext), vst  LDS stage of V(j)
 //   u      in: tile j's dequantized scores; out: tile j+1's
 //   knext0 first key of tile j+1
-//   skip   (kTokenI4Skip and kTokenI8Vsa only, wave-uniform) tile j is skipped: no
-//          probabilities and no PV; tile j+1 is still prepared
-//   qk     (kTokenI8Vsa only, wave-uniform) tile j+1 is prepared: QK, dequant and max
+//   skip   (kTokenI4Skip only, wave-uniform) tile j is skipped: no probabilities and no PV;
+//          tile j+1 is still prepared
 template <int kMode, bool kNext, bool kMaskNext, bool kMaskCur>
 __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i (&qop)[4],
                                      float qsl, State& st, float (&u)[2][16], int n, int half,
-                                     uint32_t knext0, uint32_t tokens, bool skip = false,
-                                     bool qk = true) {
-  const bool do_pv = (kMode != kTokenI4Skip && kMode != kTokenI8Vsa) || !skip;
-  const bool do_qk = kNext && (kMode != kTokenI8Vsa || qk);
+                                     uint32_t knext0, uint32_t tokens, bool skip = false) {
+  const bool do_pv = kMode != kTokenI4Skip || !skip;
+  constexpr bool do_qk = kNext;
   // The rescale owed by the last raise of m, now that PV(j-1) has accumulated.
   if (__any(st.alpha != 1.0f)) {
 #pragma unroll
@@ -681,39 +671,257 @@ void k_attention(Args a) {
 //
 // kernels/vsa_attention_8.loom: query cube b (64 queries in the gathered layout) attends to the
 // keys of every key cube kb with routes[head][b][kb] != 0, and within a cube only to its first
-// lengths[kb] keys. A workgroup here is kWaves/2 query cubes (waves 2c and 2c+1: cube
-// (kWaves/2)qb + c), and a key tile is one cube. Per run of the key loop the workgroup scans the two
-// route rows into an LDS list of the cubes that either query cube keeps (in ascending order,
-// up to kListMax of them per run), each entry carrying which of them keeps it and its live
-// length. The pipeline of k_attention then walks that list: the K/V^T tiles of a listed cube
-// are staged for the whole workgroup, and a wave whose query cube does not keep the cube skips
-// its QK, softmax and PV (wave-uniform branches), so every wave computes exactly its own
-// routes. Dead keys are masked through their staged scale pair (store_scales_live).
-constexpr int kListMax = 1024;           // list entries per run of the key loop
-constexpr int kCubes = kWaves / 2;        // query cubes per workgroup (64 queries each)
-static_assert(kCubes == 1 || kCubes == 2, "a workgroup holds one or two query cubes");
-constexpr uint32_t kEntryCube = 0x3fffu;  // entry: cube (14 bits) | keep flags << 14 | live << 16
+// lengths[kb] keys. Each query cube keeps its own set of key cubes, so a workgroup here holds
+// one query cube (two waves of 32 queries) and walks only that cube's keys: no wave ever waits
+// on tiles another query cube keeps. To run two waves per SIMD with a K/V^T stream per
+// workgroup, four workgroups share a CU, and the three-stage rings hold 32-key tiles (half a
+// cube): 3 x (4,352 + 8,192) bytes per workgroup.
+//
+// Memory: a kept cube costs 24.5 KB of K and V^T, and the kept sets of different query cubes are
+// unrelated, so when every workgroup walks a whole key sequence the K/V^T tiles of a head (49.5
+// MB at 129k tokens) stream through each XCD's 4 MB L2 and most reads miss. The key cubes are
+// therefore split into `segs` = 8 segments, and workgroup (cube, segment) runs on the XCD of its
+// segment (the hardware deals workgroup b to XCD b % 8), so each XCD's L2 serves one eighth of
+// a head's keys to all the query cubes it runs. Each workgroup leaves its segment's softmax
+// state, (running max, sum, O / sum in f16) per query, and k_vsa_merge combines the segments of a
+// query.
+//
+// Per run of the key loop the workgroup scans its route row over the segment into an LDS list
+// of the live half-cubes it keeps (ascending keys, up to kVsaListMax per run; more runs continue
+// the same online softmax). Keys past a cube's live length are masked through their staged scale
+// pair (ks, -inf), so the loop has no masked variant. The per-tile work is that of k_attention on
+// a 32-key tile: S^T is one 32 x 32 block, whose sixteen accumulator registers hold keys
+// 8h + 0..7 (registers 0..7, h = lane / 32) and 16 + 8h + 0..7 (registers 8..15) under the same
+// K row permutation, i.e. the B operands of two 16-key f16 MFMA steps.
+constexpr int kVsaWaves = 2;
+constexpr int kVsaThreads = 64 * kVsaWaves;
+constexpr int kVsaKeys = 32;                              // keys per tile: half a cube
+constexpr int kVsaKRows = kVsaKeys * kRowBytes;           // 4096
+constexpr int kVsaKStage = kVsaKRows + 2 * kVsaKeys * 4;  // + ks[32], -M*ks[32]: 4352
+constexpr int kVsaVRowBytes = 2 * kVsaKeys;               // a V^T row: 32 keys of f16
+constexpr int kVsaVStage = 128 * kVsaVRowBytes;           // 8192
+constexpr int kVsaKLoads = kVsaKRows / 1024 / kVsaWaves;  // 1 KiB LDS-DMA loads per wave: 2
+constexpr int kVsaVLoads = kVsaVStage / 1024 / kVsaWaves; // 4
+constexpr int kVsaSRows = kVsaKeys / kVsaWaves;           // scale rows stored per wave: 16
+constexpr int kVsaWaitPrevStep = (kVsaKLoads + kVsaVLoads + 1) | (7 << 4) | (0 << 8);
+constexpr int kVsaListMax = 512;                          // list entries per run of the key loop
+// entry: cube (14 bits) | half << 14 | live keys of the half (1..32) << 16
+constexpr uint32_t kEntryCube = 0x3fffu;
+static_assert(kVsaSRows <= 64 && (kVsaSRows & (kVsaSRows - 1)) == 0, "scale rows per wave");
+
+struct VsaStager {
+  uint32_t koff[kVsaKLoads];  // byte offset inside a K tile of this lane's 16 bytes, per load
+  uint32_t voff[kVsaVLoads];  // byte offset inside a V^T tile (from the head block base + 2*k0)
+  uint32_t soff;              // ks element offset (bytes) of this lane's scale row
+  uint32_t srow;              // MFMA row whose scales this lane stores (lanes below kVsaSRows)
+  int wave;
+};
+
+// K stage: as in k_attention (128-byte rows, chunks swizzled by (row/2)%8, row m holds key
+// swap23(m)). V^T stage: 64-byte rows (one channel, 32 keys), byte o holds row o/64, logical
+// chunk ((o/16)%4) ^ ((row/4)%4), so the sixteen rows a quarter-wave reads fall on distinct banks.
+__device__ __forceinline__ VsaStager make_vsa_stager(const Args& a, int wave, int lane) {
+  VsaStager s;
+  s.wave = wave;
+#pragma unroll
+  for (int t = 0; t < kVsaKLoads; ++t) {
+    const uint32_t o = (wave * kVsaKLoads + t) * 1024 + 16 * lane;
+    const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
+    s.koff[t] = swap23(row) * a.kv_bytes + 16 * chunk;
+  }
+#pragma unroll
+  for (int t = 0; t < kVsaVLoads; ++t) {
+    const uint32_t o = (wave * kVsaVLoads + t) * 1024 + 16 * lane;
+    const uint32_t row = o >> 6, chunk = ((o >> 4) & 3) ^ ((row >> 2) & 3);
+    s.voff[t] = row * a.capacity * 2 + 16 * chunk;
+  }
+  s.srow = kVsaSRows * wave + (lane & (kVsaSRows - 1));
+  s.soff = swap23(s.srow) * a.kv_head_limit * 4;
+  return s;
+}
+
+// LDS-DMA of the `live` keys of K tile k0 into stage `kst` (rows from `live` on load as zero),
+// and the load of this lane's key scale.
+__device__ __forceinline__ float stage_k_vsa(const Args& a, const VsaStager& sg, uint32_t kv_head,
+                                             uint32_t k0, uint32_t live, char* kst) {
+  const char* base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * 128;
+  const __amdgpu_buffer_rsrc_t rk = rsrc(base, live ? (live - 1) * a.kv_bytes + 128 : 0u);
+#pragma unroll
+  for (int t = 0; t < kVsaKLoads; ++t)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rk, (lds_void*)(kst + (sg.wave * kVsaKLoads + t) * 1024), 16, sg.koff[t], 0, 0, 0);
+  const float* sbase = a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
+  const uint32_t sbytes = live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0u;
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(sbase, sbytes),
+                                                                         sg.soff, 0, 0));
+}
+
+// LDS-DMA of V^T tile k0 (32 columns of every channel row of this head's block).
+__device__ __forceinline__ void stage_v_vsa(const Args& a, const VsaStager& sg, uint32_t kv_head,
+                                            uint32_t k0, char* vst) {
+  const uint32_t blk = 128 * a.capacity;
+  const char* base = reinterpret_cast<const char*>(a.vt) + ((size_t)kv_head * blk + k0) * 2;
+  const __amdgpu_buffer_rsrc_t rv = rsrc(base, k0 < blk ? (blk - k0) * 2 : 0u);
+#pragma unroll
+  for (int t = 0; t < kVsaVLoads; ++t)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rv, (lds_void*)(vst + (sg.wave * kVsaVLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
+}
+
+// Scales of a staged tile: (ks, -1.5*2^23*ks) for a live key, (ks, -inf) for a dead one.
+__device__ __forceinline__ void store_scales_vsa(char* kst, const VsaStager& sg, float ks,
+                                                 uint32_t live) {
+  if ((threadIdx.x & 63) < kVsaSRows) {
+    float* sc = reinterpret_cast<float*>(kst + kVsaKRows);
+    sc[sg.srow] = ks;
+    sc[kVsaKeys + sg.srow] = swap23(sg.srow) < live ? -(kMagic * ks) : -INFINITY;
+  }
+}
+
+// Probabilities of slots r, r+1 of a 32-key tile into pb[r/8].
+__device__ __forceinline__ void exp_pair_vsa(const float (&u)[16], int r, float qsl, float negm,
+                                             v8h (&pb)[2]) {
+  const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qsl, negm));
+  const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r + 1], qsl, negm));
+  pb[r / 8][r % 8] = (_Float16)p0;
+  pb[r / 8][r % 8 + 1] = (_Float16)p1;
+}
+
+// Dequantize slots 4i..4i+3 of a fresh 32-key tile into u and fold them into the tile max.
+__device__ __forceinline__ void dequant_vsa(const v16i& s, int i, float4 k4, float4 c4,
+                                            float (&u)[16], float& tmax) {
+  u[4 * i + 0] = __builtin_fmaf(__int_as_float(s[4 * i + 0]), k4.x, c4.x);
+  u[4 * i + 1] = __builtin_fmaf(__int_as_float(s[4 * i + 1]), k4.y, c4.y);
+  u[4 * i + 2] = __builtin_fmaf(__int_as_float(s[4 * i + 2]), k4.z, c4.z);
+  u[4 * i + 3] = __builtin_fmaf(__int_as_float(s[4 * i + 3]), k4.w, c4.w);
+  tmax = max3(tmax, max3(u[4 * i], u[4 * i + 1], u[4 * i + 2]), u[4 * i + 3]);
+}
+
+// This lane's sum of a 32-key tile's 16 packed f16 probabilities.
+__device__ __forceinline__ float tile_sum_vsa(const v8h (&pb)[2]) {
+  const v8h t8 = pb[0] + pb[1];
+  const v4h t4 = v4h{t8[0], t8[1], t8[2], t8[3]} + v4h{t8[4], t8[5], t8[6], t8[7]};
+  const v2h t2 = v2h{t4[0], t4[1]} + v2h{t4[2], t4[3]};
+  return __builtin_amdgcn_fdot2(t2, v2h{(_Float16)1.0f, (_Float16)1.0f}, 0.0f, false);
+}
+
+// K operand of QK chunk dc (32 channels) and V^T operand of PV chunk w (channel block w%4,
+// key half w/4) for this lane.
+__device__ __forceinline__ v4i k_op_vsa(const char* kst, int n, int half, int dc) {
+  return *reinterpret_cast<const v4i*>(kst + n * kRowBytes + chunk_off(dc, half, (n >> 1) & 7));
+}
+__device__ __forceinline__ v8h v_op_vsa(const char* vst, int n, int half, int w) {
+  const int db = w & 3, g = w >> 2;
+  return *reinterpret_cast<const v8h*>(vst + (32 * db + n) * kVsaVRowBytes +
+                                       16 * ((2 * g + half) ^ ((n >> 2) & 3)));
+}
+
+// The first tile's QK and dequant.
+__device__ __forceinline__ void first_tile_vsa(const char* kst, const v4i (&qop)[4], float qsl,
+                                               State& st, float (&u)[16], int n, int half) {
+  const v16i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  const float* kss = reinterpret_cast<const float*>(kst + kVsaKRows);
+  v16i s = magic;
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc)
+    s = __builtin_amdgcn_mfma_i32_32x32x32_i8(k_op_vsa(kst, n, half, dc), qop[dc], s, 0, 0, 0);
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kb = 8 * i + 4 * half;
+    dequant_vsa(s, i, *reinterpret_cast<const float4*>(kss + kb),
+                *reinterpret_cast<const float4*>(kss + kVsaKeys + kb), u, tmax);
+  }
+  raise_max(tmax, qsl, st);
+}
+
+// One pipeline step on 32-key tiles: QK(j+1) and PV(j) under tile j's softmax and tile j+1's
+// dequant, in the issue order of step():
+//   phase A  QK(j+1): 4 int8 MFMAs  with  the probabilities of tile j's slots 0..7
+//   phase B  PV(j):   8 f16 MFMAs   with  slots 8..15 (feeding PV(j)'s second key half), then
+//                                         the dequant + max of tile j+1 and the raise of m
+template <bool kNext>
+__device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const v4i (&qop)[4],
+                                         float qsl, State& st, float (&u)[16], int n, int half) {
+  if (__any(st.alpha != 1.0f)) {  // the rescale owed by the last raise of m
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[db][r] *= st.alpha;
+    st.alpha = 1.0f;
+  }
+  const v16i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
+                      kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  const float negm = -st.m;
+  const float* kss = reinterpret_cast<const float*>(kst + kVsaKRows);
+  v16i s = magic;
+  v8h pb[2];
+  v4i kop[4];
+  v8h vop[8];
+  float4 k4[4], c4[4];
+
+  // ---- phase A: QK(j+1) || probabilities of slots 0..7
+  if (kNext) {
+#pragma unroll
+    for (int w = 0; w < kPf; ++w) kop[w] = k_op_vsa(kst, n, half, w);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if (kNext && c + kPf < 4) kop[c + kPf] = k_op_vsa(kst, n, half, c + kPf);
+    if (c >= 4 - kPf) vop[c - (4 - kPf)] = v_op_vsa(vst, n, half, c - (4 - kPf));
+    if (kNext) s = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[c], s, 0, 0, 0);
+    exp_pair_vsa(u, 2 * c, qsl, negm, pb);
+    H3_CHUNK_END();
+  }
+
+  // ---- phase B: PV(j) || probabilities of slots 8..15, then dequant + max of tile j+1
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    if (c + kPf < 8) vop[c + kPf] = v_op_vsa(vst, n, half, c + kPf);
+    if (kNext && c >= 3 - kSPf && c < 7 - kSPf) {  // scales of dequant quarter q, kSPf ahead
+      const int q = c - (3 - kSPf), kb = 8 * q + 4 * half;
+      k4[q] = *reinterpret_cast<const float4*>(kss + kb);
+      c4[q] = *reinterpret_cast<const float4*>(kss + kVsaKeys + kb);
+    }
+    st.acc[c & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[c >> 2], st.acc[c & 3], 0, 0, 0);
+    if (c < 4) exp_pair_vsa(u, 8 + 2 * c, qsl, negm, pb);
+    if (kNext && c >= 3 && c < 7) dequant_vsa(s, c - 3, k4[c - 3], c4[c - 3], u, tmax);
+    if (kNext && c == 7) {
+      st.l += tile_sum_vsa(pb);
+      raise_max(tmax, qsl, st);
+    }
+    H3_CHUNK_END();
+  }
+  if (!kNext) st.l += tile_sum_vsa(pb);
+}
 
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kVsaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention_vsa(Args a) {
-  constexpr int kMode = kTokenI8Vsa;
-  constexpr int kWaitPrevStep = kWaitPrevStepOf(kMode);
-  __shared__ __attribute__((aligned(16))) char k0s[kKStage];
-  __shared__ __attribute__((aligned(16))) char k1s[kKStage];
-  __shared__ __attribute__((aligned(16))) char k2s[kKStage];
-  __shared__ __attribute__((aligned(16))) char v0s[kVStage];
-  __shared__ __attribute__((aligned(16))) char v1s[kVStage];
-  __shared__ __attribute__((aligned(16))) char v2s[kVStage];
-  __shared__ uint32_t list[kListMax];
-  __shared__ uint32_t wave_counts[kWaves];
+  __shared__ __attribute__((aligned(16))) char k0s[kVsaKStage];
+  __shared__ __attribute__((aligned(16))) char k1s[kVsaKStage];
+  __shared__ __attribute__((aligned(16))) char k2s[kVsaKStage];
+  __shared__ __attribute__((aligned(16))) char v0s[kVsaVStage];
+  __shared__ __attribute__((aligned(16))) char v1s[kVsaVStage];
+  __shared__ __attribute__((aligned(16))) char v2s[kVsaVStage];
+  __shared__ uint32_t list[kVsaListMax];
+  __shared__ uint32_t wave_counts[kVsaWaves];
 
+  // Workgroup b runs on XCD b % 8: segment b % segs of item base + b / segs.
   const uint32_t b = blockIdx.x;
-  const uint32_t logical = (b & 7u) * a.per_xcd + (b >> 3);
-  if (logical >= a.total) return;
+  const uint32_t seg = b % a.segs;
+  const uint32_t local = b / a.segs;
+  if (local >= a.total) return;
+  const uint32_t logical = a.base + local;
+  const uint32_t seg_lo = (uint32_t)((uint64_t)a.blocks * seg / a.segs);
+  const uint32_t seg_hi = (uint32_t)((uint64_t)a.blocks * (seg + 1) / a.segs);
   const uint32_t head_y = logical / a.q_blocks;
-  const uint32_t qb = logical % a.q_blocks;
+  const uint32_t cube = logical % a.q_blocks;  // this workgroup's query cube
   const uint32_t kv_head = head_y % a.kv_head_limit;
   const uint32_t head = kv_head % a.head_limit;
 
@@ -721,14 +929,10 @@ void k_attention_vsa(Args a) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
-  const uint32_t tiles32 = (a.tokens + 31) / 32;
-  const uint32_t q_tile = qb * kWaves + wave;
-  const uint32_t q_tile_c = q_tile < tiles32 ? q_tile : tiles32 - 1;
-  const uint32_t q = q_tile_c * kQueriesPerWave + n;
+  const uint32_t q = cube * 64 + wave * kQueriesPerWave + n;
   const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
-  const uint32_t my_flag = 1u << (14 + (wave >> 1));  // keep flag of this wave's query cube
 
-  const Stager sg = make_stager<kMode>(a, wave, lane);
+  const VsaStager sg = make_vsa_stager(a, wave, lane);
   v4i qop[4];
   {
     const int32_t* src = a.qi + (size_t)q_read * (a.q_row / 4) + head * 32;
@@ -745,80 +949,82 @@ void k_attention_vsa(Args a) {
   st.m = -1.0e30f;
   st.l = 0.0f;
   st.alpha = 1.0f;
-  float u[2][16] = {};
+  float u[16] = {};
 
-  const uint32_t cube0 = kCubes * qb;
-  const bool has1 = kCubes == 2 && cube0 + 1 < a.blocks;
-  const int32_t* route0 = a.routes + ((size_t)head * a.blocks + cube0) * a.blocks;
-  const int32_t* route1 = route0 + a.blocks;
-  auto cube_of = [](uint32_t e) { return e & kEntryCube; };
-  auto live_of = [](uint32_t e) { return (int)(e >> 16); };
+  const int32_t* route = a.routes + ((size_t)head * a.blocks + cube) * a.blocks;
+  auto k0_of = [](uint32_t e) { return (e & kEntryCube) * 64 + ((e >> 14) & 1u) * kVsaKeys; };
+  auto live_of = [](uint32_t e) { return e >> 16; };
 
-  uint32_t scan = 0;  // first key cube not yet listed
-  while (scan < a.blocks) {
-    // ---- list the kept cubes from `scan` on, kThreads cubes per pass, while they fit
+  uint32_t scan = seg_lo;  // first key cube of the segment not yet listed
+  while (scan < seg_hi) {
+    // ---- list the live halves of the kept cubes from `scan` on, kVsaThreads cubes per pass
     uint32_t count = 0;
-    while (scan < a.blocks) {
+    while (scan < seg_hi) {
       const uint32_t kb = scan + threadIdx.x;
-      uint32_t f = 0;
-      if (kb < a.blocks) f = (route0[kb] != 0 ? 1u : 0u) | (has1 && route1[kb] != 0 ? 2u : 0u);
-      const uint64_t ball = __ballot(f != 0);
-      if (lane == 0) wave_counts[wave] = (uint32_t)__popcll(ball);
+      uint32_t live = 0;
+      if (kb < seg_hi && route[kb] != 0) {
+        const int len = a.lengths[kb];
+        live = len < 0 ? 0u : len > 64 ? 64u : (uint32_t)len;
+      }
+      const uint64_t ball0 = __ballot(live > 0);
+      const uint64_t ball1 = __ballot(live > (uint32_t)kVsaKeys);
+      if (lane == 0) wave_counts[wave] = (uint32_t)(__popcll(ball0) + __popcll(ball1));
       __syncthreads();
       uint32_t before = 0, pass_total = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < kVsaWaves; ++w) {
         const uint32_t c = wave_counts[w];
         before += w < wave ? c : 0u;
         pass_total += c;
       }
-      if (count + pass_total > (uint32_t)kListMax) {  // the same decision in every wave
+      if (count + pass_total > (uint32_t)kVsaListMax) {  // the same decision in every wave
         __syncthreads();
         break;
       }
-      if (f) {
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
-        const int len = a.lengths[kb];
-        const uint32_t live = len < 0 ? 0u : len > kKeys ? (uint32_t)kKeys : (uint32_t)len;
-        list[count + before + rank] = kb | (f << 14) | (live << 16);
+      if (live > 0) {
+        const uint32_t rank =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(ball0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball0, 0u)) +
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(ball1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball1, 0u));
+        const uint32_t at = count + before + rank;
+        list[at] = kb | (min(live, (uint32_t)kVsaKeys) << 16);
+        if (live > (uint32_t)kVsaKeys) list[at + 1] = kb | (1u << 14) | ((live - kVsaKeys) << 16);
       }
       count += pass_total;
-      scan += kThreads;
+      scan += kVsaThreads;
       __syncthreads();
     }
     if (count == 0) continue;
 
-    // ---- the pipeline of k_attention over list[0 .. count): tile t is cube cube_of(list[t])
+    // ---- the pipeline of k_attention over list[0 .. count): tile t is the half-cube list[t]
     auto entry = [&](uint32_t t) { return t < count ? rfl(list[t]) : 0u; };
-    uint32_t e0 = entry(0), e1 = entry(1), e2 = entry(2), e3 = entry(3);
-    float ks0 = stage_k<kMode>(a, sg, kv_head, cube_of(e0) * kKeys, k0s, live_of(e0));
-    float ks1 = stage_k<kMode>(a, sg, kv_head, cube_of(e1) * kKeys, k1s, live_of(e1));
-    float ks_held = stage_k<kMode>(a, sg, kv_head, cube_of(e2) * kKeys, k2s, live_of(e2));
-    stage_v(a, sg, kv_head, cube_of(e0) * kKeys, v0s);
-    stage_v(a, sg, kv_head, cube_of(e1) * kKeys, v1s);
-    store_scales_live(k0s, sg, ks0, live_of(e0));
-    store_scales_live(k1s, sg, ks1, live_of(e1));
+    uint32_t e2 = entry(2), e3 = entry(3);
+    {
+      const uint32_t e0 = entry(0), e1 = entry(1);
+      const float ks0 = stage_k_vsa(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
+      const float ks1 = stage_k_vsa(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
+      stage_v_vsa(a, sg, kv_head, k0_of(e0), v0s);
+      stage_v_vsa(a, sg, kv_head, k0_of(e1), v1s);
+      store_scales_vsa(k0s, sg, ks0, live_of(e0));
+      store_scales_vsa(k1s, sg, ks1, live_of(e1));
+    }
+    float ks_held = stage_k_vsa(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
     step_barrier<kWaitAll>();
-    if (e0 & my_flag) first_tile<kMode, false>(k0s, qop, qsl, st, u, n, half, a.tokens);
+    first_tile_vsa(k0s, qop, qsl, st, u, n, half);
     step_barrier<kWaitAll>();
 
-    // One step j: K(j+3) -> kc, V(j+2) -> vn2; QK(j+1) from kn if this wave keeps cube j+1,
-    // PV(j) from vc if it keeps cube j; then the scales of K(j+2) into kn2.
+    // One step j: K(j+3) -> kc, V(j+2) -> vn2; QK(j+1) from kn, PV(j) from vc; then the scales
+    // of K(j+2) into kn2.
 #define H3_VSA_STEP(kc, kn, kn2, vc, vn2)                                                      \
   {                                                                                          \
-    const float ks_new = stage_k<kMode>(a, sg, kv_head, cube_of(e3) * kKeys, kc, live_of(e3)); \
-    stage_v(a, sg, kv_head, cube_of(e2) * kKeys, vn2);                                       \
+    const float ks_new = stage_k_vsa(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
+    stage_v_vsa(a, sg, kv_head, k0_of(e2), vn2);                                             \
     const uint32_t e4 = entry(j + 4);                                                        \
-    step<kMode, true, false, false>(kn, vc, qop, qsl, st, u, n, half, 0, a.tokens,           \
-                                    (e0 & my_flag) == 0, (e1 & my_flag) != 0);               \
-    store_scales_live(kn2, sg, ks_held, live_of(e2));                                        \
+    step_vsa<true>(kn, vc, qop, qsl, st, u, n, half);                                        \
+    store_scales_vsa(kn2, sg, ks_held, live_of(e2));                                         \
     ks_held = ks_new;                                                                        \
-    e0 = e1;                                                                                 \
-    e1 = e2;                                                                                 \
     e2 = e3;                                                                                 \
     e3 = e4;                                                                                 \
-    step_barrier<kWaitPrevStep>();                                                           \
+    step_barrier<kVsaWaitPrevStep>();                                                        \
     ++j;                                                                                     \
   }
     const uint32_t steady = count - 1;
@@ -833,28 +1039,76 @@ void k_attention_vsa(Args a) {
 #undef H3_VSA_STEP
     {  // the last tile's PV (stage j % 3)
       const uint32_t r = j % 3;
-      const char* vlast = r == 0 ? v0s : r == 1 ? v1s : v2s;
-      step<kMode, false, false, false>(nullptr, vlast, qop, qsl, st, u, n, half, 0, a.tokens,
-                                       (e0 & my_flag) == 0, false);
+      step_vsa<false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, n, half);
     }
     step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
   }
 
-  // ---- normalise and store rows < token_count
+  // ---- this segment's state of the workgroup's 64 queries: O / l in f16, (m, l) in f32
   const float l_tot = st.l + __shfl_xor(st.l, 32);
-  const float inv = 1.0f / l_tot;
-  if (q_tile < tiles32 && q < a.token_count && q < a.tokens) {
-    uint16_t* dst = a.out + (size_t)q * a.out_stride + head * 128;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  const size_t prow = ((size_t)local * a.segs + seg) * 64 + wave * kQueriesPerWave + n;
+  uint16_t* dst = a.part_o + prow * 128;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+  for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
-                 (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
-        *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
-      }
+    for (int i = 0; i < 4; ++i) {
+      v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
+               (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
+      *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
     }
   }
+  if (half == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * prow) = make_float2(st.m, l_tot);
+}
+
+// Combine the segments of each query of a k_attention_vsa launch: with M the largest running
+// max among the segments that saw a key and w_s = l_s * 2^(m_s - M),
+//   out = sum_s w_s * (O_s / l_s) / sum_s w_s,
+// the online softmax over all kept keys. 16 lanes per row, 8 channels each.
+__global__ __launch_bounds__(256) void k_vsa_merge(Args a) {
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t r = t >> 4, c8 = 8 * (t & 15);
+  if (r >= a.total * 64) return;
+  const uint32_t local = r >> 6, row = r & 63;
+  const uint32_t logical = a.base + local;
+  const uint32_t head_y = logical / a.q_blocks;
+  const uint32_t cube = logical % a.q_blocks;
+  const uint32_t head = (head_y % a.kv_head_limit) % a.head_limit;
+  const uint32_t q = cube * 64 + row;
+  if (q >= a.token_count || q >= a.tokens) return;
+  const size_t prow0 = (size_t)local * a.segs * 64 + row;  // segment s: prow0 + 64 s
+  float mx = -INFINITY;
+  for (uint32_t s = 0; s < a.segs; ++s) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * (prow0 + 64 * s));
+    if (ml.y > 0.0f) mx = fmaxf(mx, ml.x);
+  }
+  float acc[8] = {};
+  float wsum = 0.0f;
+  for (uint32_t s = 0; s < a.segs; ++s) {
+    const size_t prow = prow0 + 64 * s;
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * prow);
+    if (!(ml.y > 0.0f)) continue;
+    const float w = ml.y * __builtin_amdgcn_exp2f(ml.x - mx);
+    wsum += w;
+    const uint4 v = *reinterpret_cast<const uint4*>(a.part_o + prow * 128 + c8);
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v2h h = __builtin_bit_cast(v2h, words[j]);
+      acc[2 * j] = __builtin_fmaf(w, (float)h[0], acc[2 * j]);
+      acc[2 * j + 1] = __builtin_fmaf(w, (float)h[1], acc[2 * j + 1]);
+    }
+  }
+  const float inv = 1.0f / wsum;
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const v2h h = {(_Float16)(acc[2 * j] * inv), (_Float16)(acc[2 * j + 1] * inv)};
+    o[j] = __builtin_bit_cast(uint32_t, h);
+  }
+  uint2* dst = reinterpret_cast<uint2*>(a.out + (size_t)q * a.out_stride + head * 128 + c8);
+  dst[0] = make_uint2(o[0], o[1]);  // 8-byte stores: the output needs 8-byte alignment only
+  dst[1] = make_uint2(o[2], o[3]);
 }
 
 // ---------------------------------------------------------------- cross-attention (GQA, key mask)
@@ -1057,11 +1311,40 @@ hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, co
   return hipGetLastError();
 }
 
+// CUs of the current device (cached per device).
+static uint32_t device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    cus[dev] = n;
+  }
+  return (uint32_t)cus[dev];
+}
+
+constexpr uint32_t kVsaSegs = 8;  // key segments: one per XCD
+
+// (head, query cube) items per launch of k_attention_vsa and k_vsa_merge: eight generations of
+// resident workgroups (four per CU), i.e. 1,024 items of 8 segments on 256 CUs. Measured at 129k
+// tokens: one generation per launch 49.0 ms (launch-bound), four 40.1 ms, eight 39.3 ms,
+// sixteen 39.5 ms; 4 segments 42.8 ms, 16 segments 42.5 ms.
+static uint32_t vsa_launch_items(uint32_t items) {
+  return std::min(items, std::max(1u, 8u * 4u * device_cus() / kVsaSegs));
+}
+
+size_t vsa_workspace_bytes(uint32_t token_count, uint32_t heads) {
+  const uint32_t items = (token_count + 63) / 64 * heads;
+  return (size_t)std::max(1u, vsa_launch_items(items)) * kVsaSegs * 64 * (128 * 2 + 2 * 4);
+}
+
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
                                 uint32_t heads, const int32_t* qi, const float* qs,
                                 const int32_t* ki, const float* ks, const uint16_t* vt,
                                 uint16_t* out, const int32_t* routes, const int32_t* lengths,
-                                hipStream_t stream) {
+                                void* workspace, hipStream_t stream) {
   Args a{};
   a.qi = qi;
   a.qs = qs;
@@ -1075,16 +1358,25 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
   a.q_row = cfg.q_stride;
   a.kv_bytes = cfg.kv_stride;
   a.out_stride = cfg.out_stride;
-  a.q_blocks = (token_count + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  a.q_blocks = (token_count + 63) / 64;  // one query cube per item
   a.heads = heads;
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
-  a.total = a.q_blocks * heads;
-  a.per_xcd = (a.total + 7) / 8;
   a.routes = routes;
   a.lengths = lengths;
-  a.blocks = cfg.tokens / kKeys;
-  hipLaunchKernelGGL(k_attention_vsa, dim3(a.per_xcd * 8), dim3(kThreads), 0, stream, a);
+  a.blocks = cfg.tokens / 64;
+  a.segs = kVsaSegs;
+  const uint32_t items = a.q_blocks * heads;
+  const uint32_t gen = std::max(1u, vsa_launch_items(items));
+  a.part_o = static_cast<uint16_t*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                       (size_t)gen * kVsaSegs * 64 * 128 * 2);
+  for (uint32_t base = 0; base < items; base += gen) {
+    a.base = base;
+    a.total = std::min(gen, items - base);
+    hipLaunchKernelGGL(k_attention_vsa, dim3(a.total * kVsaSegs), dim3(kVsaThreads), 0, stream, a);
+    hipLaunchKernelGGL(k_vsa_merge, dim3((a.total * 64 * 16 + 255) / 256), dim3(256), 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -83,12 +83,15 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
 hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
                                   const int32_t* ki, const float* ks, const uint16_t* vt,
                                   const uint8_t* key_mask, uint16_t* out, hipStream_t stream);
-// kTokenI8Vsa: the int8 token-major attention over the cubes `routes` keeps (attention.hip)
+// The int8 token-major attention over the cubes `routes` keeps (attention.hip). `workspace`
+// holds vsa_workspace_bytes(token_count, heads) of device memory for the per-segment softmax
+// states; it is reused launch after launch on `stream`.
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
                                 uint32_t heads, const int32_t* qi, const float* qs,
                                 const int32_t* ki, const float* ks, const uint16_t* vt,
                                 uint16_t* out, const int32_t* routes, const int32_t* lengths,
-                                hipStream_t stream);
+                                void* workspace, hipStream_t stream);
+size_t vsa_workspace_bytes(uint32_t token_count, uint32_t heads);
 // VSA operations (vsa.hip)
 hipError_t launch_vsa_gather(uint32_t tokens, uint32_t padded, uint32_t width, const int32_t* src,
                              const uint16_t* x, uint16_t* y, hipStream_t stream);

@@ -389,7 +389,10 @@ int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_st
  * 64kb + j with routes[h][t/64][kb] != 0 and j < lengths[kb]. cfg->tokens = padded (a multiple
  * of 64, blocks = tokens/64 <= 16384), token operands as h3_attention_i8qk; routes
  * [out_stride/128][blocks][blocks] i32, lengths [blocks] i32. qs must be positive (the quantizer's
- * scales are). */
+ * scales are). The key cubes are walked in eight segments whose softmax states are combined at
+ * the end; the states take a stream-ordered device allocation (hipMallocAsync / hipFreeAsync on
+ * `stream`) of 135 KB per (head, 64-query cube), at most 138 MB on a 256-CU device; if it fails
+ * the call returns H3_ERR_LAUNCH. */
 int h3_vsa_attention_i8(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_stream stream);

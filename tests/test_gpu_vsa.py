@@ -5,10 +5,12 @@
     cubes, on tied, NaN and signed-zero scores, and for every routing budget from 0 to blocks-1;
   - the coarse branch is within float rounding of its f64 statement (hardware exp);
   - the block-sparse attention matches the f64 attention of its operands over the kept keys at
-    the north-star tolerance (max-abs 2e-2, mean-abs 2e-3), with partial cubes, odd block
-    counts and routes that differ between the two query cubes of a workgroup; with every block
-    routed and full cubes it equals the dense token-major attention bit for bit; and past one
-    list run (more than 1024 listed cubes) it still agrees with the dense kernel;
+    the north-star tolerance (max-abs 2e-2, mean-abs 2e-3), with partial cubes (live lengths
+    on both sides of the 32-key tile boundary), odd block counts and routes that differ
+    between query cubes; with every block routed and full cubes it agrees with the dense
+    token-major attention to within f16 rounding (max-abs 2e-3; the two walk the keys in tiles
+    of 32 and 64, so their lazy running maxima and f16 partial sums round differently); and
+    past one list run (more than 512 listed half-cubes) it still matches the oracle;
   - the runtime (Runtime::emit) reproduces the reference's device test
     (src/vsa/device.rs:503-760): its intermediate buffers equal the oracle's bit for bit, the
     output's normalised RMSE against the independent masked attention is below 0.03 plain and
@@ -215,6 +217,7 @@ def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_cou
     ([3, 64, 49, 64, 8, 22], 1, 0.3),
     ([64] * 9, 2, 0.4),
     ([64, 17, 64, 64, 1, 64, 40, 64, 64, 33, 64], 0, 0.25),
+    ([32, 64, 33, 31, 64, 64, 2], 1, 0.3),
 ])
 def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p):
     rng = np.random.default_rng(len(lengths) * 13 + prefix)
@@ -257,14 +260,19 @@ def test_every_block_routed_is_the_dense_attention(dev, blocks, heads):
     out = torch.zeros((n * w,), dtype=torch.int16, device=dev)
     H.attention_i8qk(cfg, n, heads, to_dev(pack_codes(qc), dev), to_dev(qs, dev),
                      to_dev(pack_codes(kc), dev), to_dev(ks, dev), to_dev(vt, dev), out)
-    assert np.array_equal(got, from_dev(out).reshape(n, w))
+    dense = from_dev(out).reshape(n, w).view(np.float16).astype(np.float32)
+    sparse = got.view(np.float16).astype(np.float32)
+    assert np.isfinite(sparse).all()
+    assert np.abs(sparse - dense).max() < 2e-3, np.abs(sparse - dense).max()
+    want = O.vsa_attention_f64(qc, qs, kc, ks, vt, n, n, heads, routes, lengths,
+                               np.arange(n, dtype=np.int32)).reshape(n, -1)
+    mx, mean = north_star_ok(sparse, want)
+    assert mx < 2e-2 and mean < 2e-3, (mx, mean)
 
 
 def test_more_cubes_than_one_list_run(dev):
-    """1100 cubes, all routed: the key loop runs twice (1024 + 76 listed cubes) and must agree
-    with the dense kernel and the oracle."""
-    import torch
-
+    """1100 cubes, nearly all routed: 2,197 or 2,199 live half-cubes per query cube, so the key
+    loop runs five times (512 listed half-cubes per run) and must still match the oracle."""
     rng = np.random.default_rng(11)
     heads, blocks = 1, 1100
     lengths = np.full(blocks, 64, np.int32)
@@ -274,7 +282,7 @@ def test_more_cubes_than_one_list_run(dev):
     routes[0, :, 3] = 0
     for q in (2, 3, 4):
         routes[0, q, 3] = 1  # the neighbours keep block 3
-    print("vsa two list runs", flush=True)
+    print("vsa five list runs", flush=True)
     got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
     n = 64 * blocks
     rows = np.array([0, 1, 200, 230, 64 * 1050 + 3, 64 * 1099 + 63, 64 * 3 + 5], np.int32)
