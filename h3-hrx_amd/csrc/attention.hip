@@ -955,17 +955,28 @@ void k_attention_vsa(Args a) {
   auto k0_of = [](uint32_t e) { return (e & kEntryCube) * 64 + ((e >> 14) & 1u) * kVsaKeys; };
   auto live_of = [](uint32_t e) { return e >> 16; };
 
+  // Route flag and length of this thread's cube in the pass at `at`, loaded together (one round
+  // trip) and one pass ahead of their use.
+  auto fetch = [&](uint32_t at, int32_t& keep, int32_t& len) {
+    const uint32_t kb = at + threadIdx.x;
+    keep = 0;
+    len = 0;
+    if (kb < seg_hi) {
+      keep = route[kb];
+      len = a.lengths[kb];
+    }
+  };
   uint32_t scan = seg_lo;  // first key cube of the segment not yet listed
   while (scan < seg_hi) {
     // ---- list the live halves of the kept cubes from `scan` on, kVsaThreads cubes per pass
     uint32_t count = 0;
+    int32_t keep_next, len_next;
+    fetch(scan, keep_next, len_next);
     while (scan < seg_hi) {
       const uint32_t kb = scan + threadIdx.x;
-      uint32_t live = 0;
-      if (kb < seg_hi && route[kb] != 0) {
-        const int len = a.lengths[kb];
-        live = len < 0 ? 0u : len > 64 ? 64u : (uint32_t)len;
-      }
+      const int32_t keep = keep_next, len = len_next;
+      if (scan + kVsaThreads < seg_hi) fetch(scan + kVsaThreads, keep_next, len_next);
+      const uint32_t live = keep == 0 ? 0u : len < 0 ? 0u : len > 64 ? 64u : (uint32_t)len;
       const uint64_t ball0 = __ballot(live > 0);
       const uint64_t ball1 = __ballot(live > (uint32_t)kVsaKeys);
       if (lane == 0) wave_counts[wave] = (uint32_t)(__popcll(ball0) + __popcll(ball1));
