@@ -142,7 +142,7 @@ enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2, kModeTokenI4Skip = 3
 int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
                      uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                      h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f,
-                     h3_view routes = {}, h3_view lengths = {}) {
+                     h3_view routes = {}, h3_view lengths = {}, h3_view workspace = {}) {
   const bool head_major = mode == kModeHeadI8;
   const bool vsa = mode == kModeTokenI8Vsa;
   const size_t code_div = (mode == kModeTokenI4 || mode == kModeTokenI4Skip) ? 2 : 1;
@@ -205,20 +205,25 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
     h3_view rv[2] = {routes, lengths};
     size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
     if ((st = check_bindings(stage, rv, rneed, 2))) return st;
+    const size_t ws_need = vsa_workspace_bytes(token_count, heads);
+    if (workspace.ptr && workspace.bytes < ws_need)
+      return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
+                       stage, workspace.bytes, ws_need);
     if ((st = device_ready(stage))) return st;
-    // The per-segment softmax states live in a stream-ordered allocation: it is taken and given
-    // back in the order of `stream`, so calls on different streams never share it.
-    void* workspace = nullptr;
-    hipError_t e = hipMallocAsync(&workspace, vsa_workspace_bytes(token_count, heads), stream);
-    if (e != hipSuccess) return launched(stage, e);
+    // Without a caller's workspace the per-segment softmax states live in a stream-ordered
+    // allocation: it is taken and given back in the order of `stream`, so calls on different
+    // streams never share it.
+    void* ws = workspace.ptr;
+    hipError_t e = hipSuccess;
+    if (!ws && (e = hipMallocAsync(&ws, ws_need, stream)) != hipSuccess) return launched(stage, e);
     e = launch_attention_vsa(*cfg, token_count, heads, static_cast<const int32_t*>(qi.ptr),
                              static_cast<const float*>(qs.ptr),
                              static_cast<const int32_t*>(ki.ptr),
                              static_cast<const float*>(ks.ptr),
                              static_cast<const uint16_t*>(vt.ptr), static_cast<uint16_t*>(out.ptr),
                              static_cast<const int32_t*>(routes.ptr),
-                             static_cast<const int32_t*>(lengths.ptr), workspace, stream);
-    const hipError_t ef = hipFreeAsync(workspace, stream);
+                             static_cast<const int32_t*>(lengths.ptr), ws, stream);
+    const hipError_t ef = workspace.ptr ? hipSuccess : hipFreeAsync(ws, stream);
     return launched(stage, e != hipSuccess ? e : ef);
   }
   if ((st = device_ready(stage))) return st;
@@ -287,6 +292,13 @@ int transpose_common(const char* stage, const h3_transpose_cfg* cfg, uint32_t la
 }
 
 }  // namespace
+
+int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                        h3_view routes, h3_view lengths, h3_view workspace, hipStream_t stream) {
+  return attention_common("VSA attention", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          stream, kModeTokenI8Vsa, 0.0f, routes, lengths, workspace);
+}
 }  // namespace h3
 
 using namespace h3;

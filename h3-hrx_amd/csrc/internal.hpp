@@ -92,6 +92,12 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
                                 uint16_t* out, const int32_t* routes, const int32_t* lengths,
                                 void* workspace, hipStream_t stream);
 size_t vsa_workspace_bytes(uint32_t token_count, uint32_t heads);
+// h3_vsa_attention_i8 with a caller's workspace of at least vsa_workspace_bytes(token_count,
+// heads) bytes (abi.cpp); with an empty view it takes a stream-ordered allocation as the public
+// entry point does.
+int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                        h3_view routes, h3_view lengths, h3_view workspace, hipStream_t stream);
 // VSA operations (vsa.hip)
 hipError_t launch_vsa_gather(uint32_t tokens, uint32_t padded, uint32_t width, const int32_t* src,
                              const uint16_t* x, uint16_t* y, hipStream_t stream);

@@ -36,6 +36,7 @@ struct h3_vsa {
   h3_view src{}, inverse{}, lengths{};
   h3_view q{}, k{}, v{}, qm{}, km{}, vm{}, coarse{}, scores{}, routes{}, out{};
   h3_view qi{}, ki{}, qs{}, ks{}, vt{}, zero{};
+  h3_view ws{};  // the sparse attention's per-segment softmax states
   std::vector<h3_view> means;  // the previous call's K mean of each layer
 };
 
@@ -46,7 +47,7 @@ namespace {
 void release(h3_vsa* r) {
   for (h3_view* v : {&r->src, &r->inverse, &r->lengths, &r->q, &r->k, &r->v, &r->qm, &r->km,
                      &r->vm, &r->coarse, &r->scores, &r->routes, &r->out, &r->qi, &r->ki, &r->qs,
-                     &r->ks, &r->vt, &r->zero})
+                     &r->ks, &r->vt, &r->zero, &r->ws})
     if (v->ptr) (void)hipFree(v->ptr);
   for (h3_view& v : r->means)
     if (v.ptr) (void)hipFree(v.ptr);
@@ -225,7 +226,8 @@ int h3_vsa_build(const int32_t* src, const int32_t* inverse, const int32_t* leng
                 {&r->qs, (size_t)n * heads * 4, nullptr},
                 {&r->ks, (size_t)n * heads * 4, nullptr},
                 {&r->vt, nw2, nullptr},
-                {&r->zero, (size_t)width * 4, nullptr}};
+                {&r->zero, (size_t)width * 4, nullptr},
+                {&r->ws, vsa_workspace_bytes(n, heads), nullptr}};
   for (auto& a : allocs) {
     if ((st = allocate(a.v, a.bytes, a.upload))) {
       release(r);
@@ -286,8 +288,9 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
   if ((st = h3_prepare_qk_i8(&r->prep_q, c->padded, r->q, r->zero, r->qi, r->qs, stream)) ||
       (st = h3_prepare_qk_i8(&r->prep_k, c->padded, r->k, mean, r->ki, r->ks, stream)) ||
       (st = h3_transpose_f16(&r->transpose, c->padded, c->padded, r->v, r->vt, stream)) ||
-      (st = h3_vsa_attention_i8(&r->attention, c->padded, c->heads, r->qi, r->qs, r->ki, r->ks,
-                                r->vt, r->out, r->routes, r->lengths, stream)))
+      (st = vsa_attention_i8_ws(&r->attention, c->padded, c->heads, r->qi, r->qs, r->ki, r->ks,
+                                r->vt, r->out, r->routes, r->lengths, r->ws,
+                                reinterpret_cast<hipStream_t>(stream))))
     return st;
   // 334-346: this call's mean of the block K means, for the layer's next call
   if ((st = h3_vsa_kmean(c->width, c->blocks, r->km, mean, stream))) return st;

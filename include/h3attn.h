@@ -392,7 +392,7 @@ int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_st
  * scales are). The key cubes are walked in eight segments whose softmax states are combined at
  * the end; the states take a stream-ordered device allocation (hipMallocAsync / hipFreeAsync on
  * `stream`) of 135 KB per (head, 64-query cube), at most 138 MB on a 256-CU device; if it fails
- * the call returns H3_ERR_LAUNCH. */
+ * the call returns H3_ERR_LAUNCH. (h3_vsa_attend uses a workspace h3_vsa_build allocates.) */
 int h3_vsa_attention_i8(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_stream stream);
