@@ -205,26 +205,23 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
     h3_view rv[2] = {routes, lengths};
     size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
     if ((st = check_bindings(stage, rv, rneed, 2))) return st;
+    // A workspace selects the segmented kernel (per-segment softmax states, then a merge);
+    // without one every workgroup walks whole key sequences and nothing is allocated.
     const size_t ws_need = vsa_workspace_bytes(token_count, heads);
     if (workspace.ptr && workspace.bytes < ws_need)
       return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
                        stage, workspace.bytes, ws_need);
     if ((st = device_ready(stage))) return st;
-    // Without a caller's workspace the per-segment softmax states live in a stream-ordered
-    // allocation: it is taken and given back in the order of `stream`, so calls on different
-    // streams never share it.
-    void* ws = workspace.ptr;
-    hipError_t e = hipSuccess;
-    if (!ws && (e = hipMallocAsync(&ws, ws_need, stream)) != hipSuccess) return launched(stage, e);
-    e = launch_attention_vsa(*cfg, token_count, heads, static_cast<const int32_t*>(qi.ptr),
-                             static_cast<const float*>(qs.ptr),
-                             static_cast<const int32_t*>(ki.ptr),
-                             static_cast<const float*>(ks.ptr),
-                             static_cast<const uint16_t*>(vt.ptr), static_cast<uint16_t*>(out.ptr),
-                             static_cast<const int32_t*>(routes.ptr),
-                             static_cast<const int32_t*>(lengths.ptr), ws, stream);
-    const hipError_t ef = workspace.ptr ? hipSuccess : hipFreeAsync(ws, stream);
-    return launched(stage, e != hipSuccess ? e : ef);
+    return launched(stage, launch_attention_vsa(*cfg, token_count, heads,
+                                                static_cast<const int32_t*>(qi.ptr),
+                                                static_cast<const float*>(qs.ptr),
+                                                static_cast<const int32_t*>(ki.ptr),
+                                                static_cast<const float*>(ks.ptr),
+                                                static_cast<const uint16_t*>(vt.ptr),
+                                                static_cast<uint16_t*>(out.ptr),
+                                                static_cast<const int32_t*>(routes.ptr),
+                                                static_cast<const int32_t*>(lengths.ptr),
+                                                workspace.ptr, stream));
   }
   if ((st = device_ready(stage))) return st;
   return launched(stage, launch_attention(*cfg, mode, skip_tau, token_count, heads,
@@ -744,6 +741,21 @@ int h3_vsa_attention_i8(const h3_attention_cfg* cfg, uint32_t token_count, uint3
   return attention_common("VSA attention", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI8Vsa, 0.0f, routes,
                           lengths);
+}
+
+size_t h3_vsa_attention_workspace_bytes(uint32_t token_count, uint32_t heads) {
+  if (device_ready("VSA attention workspace")) return 0;
+  return vsa_workspace_bytes(token_count, heads);
+}
+
+int h3_vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                           h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                           h3_view out, h3_view routes, h3_view lengths, h3_view workspace,
+                           h3_stream stream) {
+  if (!workspace.ptr)
+    return set_error(H3_ERR_ARGUMENT, "VSA attention: null workspace (use h3_vsa_attention_i8)");
+  return vsa_attention_i8_ws(cfg, token_count, heads, qi, qs, ki, ks, vt, out, routes, lengths,
+                             workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

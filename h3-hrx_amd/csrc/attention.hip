@@ -901,6 +901,9 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
 
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// kSplit: workgroup (item, segment) leaves its segment's softmax state for k_vsa_merge.
+// Otherwise one workgroup walks all key cubes of its item and writes the output rows.
+template <bool kSplit>
 __global__ __launch_bounds__(kVsaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention_vsa(Args a) {
   __shared__ __attribute__((aligned(16))) char k0s[kVsaKStage];
@@ -912,14 +915,15 @@ void k_attention_vsa(Args a) {
   __shared__ uint32_t list[kVsaListMax];
   __shared__ uint32_t wave_counts[kVsaWaves];
 
-  // Workgroup b runs on XCD b % 8: segment b % segs of item base + b / segs.
+  // Workgroup b runs on XCD b % 8. Split: segment b % segs of item base + b / segs. Whole: the
+  // XCD-aware remap of k_attention over the launch's items (each XCD a contiguous range).
   const uint32_t b = blockIdx.x;
-  const uint32_t seg = b % a.segs;
-  const uint32_t local = b / a.segs;
+  const uint32_t seg = kSplit ? b % a.segs : 0u;
+  const uint32_t local = kSplit ? b / a.segs : (b & 7u) * a.per_xcd + (b >> 3);
   if (local >= a.total) return;
   const uint32_t logical = a.base + local;
-  const uint32_t seg_lo = (uint32_t)((uint64_t)a.blocks * seg / a.segs);
-  const uint32_t seg_hi = (uint32_t)((uint64_t)a.blocks * (seg + 1) / a.segs);
+  const uint32_t seg_lo = kSplit ? (uint32_t)((uint64_t)a.blocks * seg / a.segs) : 0u;
+  const uint32_t seg_hi = kSplit ? (uint32_t)((uint64_t)a.blocks * (seg + 1) / a.segs) : a.blocks;
   const uint32_t head_y = logical / a.q_blocks;
   const uint32_t cube = logical % a.q_blocks;  // this workgroup's query cube
   const uint32_t kv_head = head_y % a.kv_head_limit;
@@ -1055,8 +1059,23 @@ void k_attention_vsa(Args a) {
     step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
   }
 
-  // ---- this segment's state of the workgroup's 64 queries: O / l in f16, (m, l) in f32
   const float l_tot = st.l + __shfl_xor(st.l, 32);
+  if (!kSplit) {  // ---- normalise and store rows < token_count
+    if (q >= a.token_count || q >= a.tokens) return;
+    const float inv = 1.0f / l_tot;
+    uint16_t* dst = a.out + (size_t)q * a.out_stride + head * 128;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
+                 (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
+        *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
+      }
+    }
+    return;
+  }
+  // ---- this segment's state of the workgroup's 64 queries: O / l in f16, (m, l) in f32
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   const size_t prow = ((size_t)local * a.segs + seg) * 64 + wave * kQueriesPerWave + n;
   uint16_t* dst = a.part_o + prow * 128;
@@ -1376,8 +1395,24 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
   a.routes = routes;
   a.lengths = lengths;
   a.blocks = cfg.tokens / 64;
-  a.segs = kVsaSegs;
   const uint32_t items = a.q_blocks * heads;
+  if (!workspace) {
+    // Whole key sequences, one launch per generation of resident workgroups (four per CU): its
+    // workgroups start together and walk their ascending key lists at about the same pace, so
+    // more of the tiles they share are still in L2 (measured at 129k tokens: 45.9 ms against
+    // 56.5 ms for one launch of all the work).
+    a.segs = 1;
+    const uint32_t gen = std::max(1u, 4u * device_cus());
+    for (uint32_t base = 0; base < items; base += gen) {
+      a.base = base;
+      a.total = std::min(gen, items - base);
+      a.per_xcd = (a.total + 7) / 8;
+      hipLaunchKernelGGL(k_attention_vsa<false>, dim3(a.per_xcd * 8), dim3(kVsaThreads), 0,
+                         stream, a);
+    }
+    return hipGetLastError();
+  }
+  a.segs = kVsaSegs;
   const uint32_t gen = std::max(1u, vsa_launch_items(items));
   a.part_o = static_cast<uint16_t*>(workspace);
   a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
@@ -1385,7 +1420,8 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
   for (uint32_t base = 0; base < items; base += gen) {
     a.base = base;
     a.total = std::min(gen, items - base);
-    hipLaunchKernelGGL(k_attention_vsa, dim3(a.total * kVsaSegs), dim3(kVsaThreads), 0, stream, a);
+    hipLaunchKernelGGL(k_attention_vsa<true>, dim3(a.total * kVsaSegs), dim3(kVsaThreads), 0,
+                       stream, a);
     hipLaunchKernelGGL(k_vsa_merge, dim3((a.total * 64 * 16 + 255) / 256), dim3(256), 0, stream, a);
   }
   return hipGetLastError();

@@ -83,9 +83,10 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
 hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
                                   const int32_t* ki, const float* ks, const uint16_t* vt,
                                   const uint8_t* key_mask, uint16_t* out, hipStream_t stream);
-// The int8 token-major attention over the cubes `routes` keeps (attention.hip). `workspace`
-// holds vsa_workspace_bytes(token_count, heads) of device memory for the per-segment softmax
-// states; it is reused launch after launch on `stream`.
+// The int8 token-major attention over the cubes `routes` keeps (attention.hip). With a
+// `workspace` of vsa_workspace_bytes(token_count, heads) bytes the key cubes are walked in
+// per-XCD segments whose softmax states it holds (reused launch after launch on `stream`);
+// with nullptr every workgroup walks whole key sequences.
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
                                 uint32_t heads, const int32_t* qi, const float* qs,
                                 const int32_t* ki, const float* ks, const uint16_t* vt,
@@ -93,7 +94,7 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
                                 void* workspace, hipStream_t stream);
 size_t vsa_workspace_bytes(uint32_t token_count, uint32_t heads);
 // h3_vsa_attention_i8 with a caller's workspace of at least vsa_workspace_bytes(token_count,
-// heads) bytes (abi.cpp); with an empty view it takes a stream-ordered allocation as the public
+// heads) bytes (abi.cpp); with an empty view it runs the whole-sequence kernel as the public
 // entry point does.
 int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,

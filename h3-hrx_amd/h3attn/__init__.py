@@ -217,6 +217,10 @@ SIGNATURES = {
     "h3_vsa_attention_i8": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, View, _S], ctypes.c_int),
+    "h3_vsa_attention_i8_ws": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         View, View, View, _S], ctypes.c_int),
+    "h3_vsa_attention_workspace_bytes": ([ctypes.c_uint32, ctypes.c_uint32], ctypes.c_size_t),
     "h3_vsa_plan_blocks": (
         [_P(VsaSegment), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
          _P(ctypes.c_uint32)], ctypes.c_int),
@@ -530,6 +534,17 @@ def vsa_attention_i8(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki
     check(lib().h3_vsa_attention_i8(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
                                     view(ki), view(ks), view(vt), view(out), view(routes),
                                     view(lengths), stream_ptr(stream)))
+
+
+def vsa_attention_workspace_bytes(token_count: int, heads: int) -> int:
+    return int(lib().h3_vsa_attention_workspace_bytes(token_count, heads))
+
+
+def vsa_attention_i8_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                        routes, lengths, workspace, stream=None) -> None:
+    check(lib().h3_vsa_attention_i8_ws(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                       view(ki), view(ks), view(vt), view(out), view(routes),
+                                       view(lengths), view(workspace), stream_ptr(stream)))
 
 
 class VsaOptions:

@@ -10,7 +10,10 @@
     between query cubes; with every block routed and full cubes it agrees with the dense
     token-major attention to within f16 rounding (max-abs 2e-3; the two walk the keys in tiles
     of 32 and 64, so their lazy running maxima and f16 partial sums round differently); and
-    past one list run (more than 512 listed half-cubes) it still matches the oracle;
+    past one list run (more than 512 listed half-cubes) it still matches the oracle. Each case
+    runs both forms: whole key sequences (h3_vsa_attention_i8) and per-XCD key segments with a
+    merge (h3_vsa_attention_i8_ws, on a NaN-filled workspace), which also agree with each other
+    to within the f16 rounding of the segment states;
   - the runtime (Runtime::emit) reproduces the reference's device test
     (src/vsa/device.rs:503-760): its intermediate buffers equal the oracle's bit for bit, the
     output's normalised RMSE against the independent masked attention is below 0.03 plain and
@@ -198,7 +201,10 @@ def random_routes(rng, heads, blocks, prefix, p):
     return r
 
 
-def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_count=None):
+def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_count=None,
+                      segmented=False):
+    """h3_vsa_attention_i8 (whole key sequences) or, segmented, h3_vsa_attention_i8_ws (per-XCD
+    key segments and a merge, on a workspace filled with NaN beforehand)."""
     import torch
 
     n = qc.shape[0]
@@ -206,10 +212,20 @@ def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_cou
     token_count = n if token_count is None else token_count
     cfg = H.AttentionCfg(w, w, w, n, n, H.config_f32(1 / math.sqrt(128)))
     out = torch.full((token_count * w,), 0x7E00, dtype=torch.int16, device=dev)
-    H.vsa_attention_i8(cfg, token_count, heads, to_dev(pack_codes(qc), dev), to_dev(qs, dev),
-                       to_dev(pack_codes(kc), dev), to_dev(ks, dev), to_dev(vt, dev), out,
-                       to_dev(routes, dev), to_dev(lengths, dev))
+    args = (cfg, token_count, heads, to_dev(pack_codes(qc), dev), to_dev(qs, dev),
+            to_dev(pack_codes(kc), dev), to_dev(ks, dev), to_dev(vt, dev), out,
+            to_dev(routes, dev), to_dev(lengths, dev))
+    if segmented:
+        nbytes = H.vsa_attention_workspace_bytes(token_count, heads)
+        assert nbytes > 0 and nbytes % (8 * 64 * 264) == 0  # whole (head, cube) items
+        ws = torch.full((nbytes // 2,), 0x7E00, dtype=torch.int16, device=dev)
+        H.vsa_attention_i8_ws(*args, ws)
+    else:
+        H.vsa_attention_i8(*args)
     return from_dev(out).reshape(token_count, w)
+
+
+SEGMENTED = pytest.mark.parametrize("segmented", [False, True], ids=["whole", "segmented"])
 
 
 @pytest.mark.parametrize("lengths,prefix,p", [
@@ -219,15 +235,16 @@ def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_cou
     ([64, 17, 64, 64, 1, 64, 40, 64, 64, 33, 64], 0, 0.25),
     ([32, 64, 33, 31, 64, 64, 2], 1, 0.3),
 ])
-def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p):
+@SEGMENTED
+def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p, segmented):
     rng = np.random.default_rng(len(lengths) * 13 + prefix)
     heads = 2
     lengths = np.array(lengths, np.int32)
     blocks = len(lengths)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = random_routes(rng, heads, blocks, prefix, p)
-    print(f"vsa attention blocks={blocks} prefix={prefix} p={p}", flush=True)
-    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
+    print(f"vsa attention blocks={blocks} prefix={prefix} p={p} segmented={segmented}", flush=True)
+    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
     n = 64 * blocks
     want = O.vsa_attention_f64(qc, qs, kc, ks, vt, n, n, heads, routes, lengths,
                                np.arange(n, dtype=np.int32)).reshape(n, -1)
@@ -235,26 +252,43 @@ def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p):
     assert mx < 2e-2 and mean < 2e-3, (mx, mean)
 
 
-def test_token_count_limits_the_rows_written(dev):
+@SEGMENTED
+def test_token_count_limits_the_rows_written(dev, segmented):
     rng = np.random.default_rng(3)
     heads, lengths = 1, np.array([64, 64, 64], np.int32)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = random_routes(rng, heads, 3, 0, 0.5)
-    full = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
-    part = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_count=100)
+    full = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
+    part = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_count=100,
+                             segmented=segmented)
     assert np.array_equal(part, full[:100])
 
 
+def test_segmented_and_whole_paths_agree(dev):
+    """The two forms differ only in rounding: the segment states are f16 before the merge."""
+    rng = np.random.default_rng(21)
+    heads, lengths = 3, np.array([64, 40, 64, 64, 7, 64, 64, 64, 33, 64, 64, 64, 64, 1, 64, 64,
+                                  64, 64, 64], np.int32)
+    qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
+    routes = random_routes(rng, heads, len(lengths), 1, 0.35)
+    a = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
+    b = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=True)
+    a32, b32 = (x.view(np.float16).astype(np.float32) for x in (a, b))
+    assert np.isfinite(b32).all()
+    assert np.abs(a32 - b32).max() < 2e-3, np.abs(a32 - b32).max()
+
+
 @pytest.mark.parametrize("blocks,heads", [(5, 2), (16, 3)])
-def test_every_block_routed_is_the_dense_attention(dev, blocks, heads):
+@SEGMENTED
+def test_every_block_routed_is_the_dense_attention(dev, blocks, heads, segmented):
     import torch
 
     rng = np.random.default_rng(blocks)
     lengths = np.full(blocks, 64, np.int32)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = np.ones((heads, blocks, blocks), np.int32)
-    print(f"vsa dense equivalence blocks={blocks}", flush=True)
-    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
+    print(f"vsa dense equivalence blocks={blocks} segmented={segmented}", flush=True)
+    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
     n, w = 64 * blocks, heads * 128
     cfg = H.AttentionCfg(w, w, w, n, n, H.config_f32(1 / math.sqrt(128)))
     out = torch.zeros((n * w,), dtype=torch.int16, device=dev)
@@ -270,9 +304,11 @@ def test_every_block_routed_is_the_dense_attention(dev, blocks, heads):
     assert mx < 2e-2 and mean < 2e-3, (mx, mean)
 
 
-def test_more_cubes_than_one_list_run(dev):
+@SEGMENTED
+def test_more_cubes_than_one_list_run(dev, segmented):
     """1100 cubes, nearly all routed: 2,197 or 2,199 live half-cubes per query cube, so the key
-    loop runs five times (512 listed half-cubes per run) and must still match the oracle."""
+    loop runs five times (512 listed half-cubes per run) in the whole form, once per segment of
+    about 274 half-cubes in the segmented form, and must still match the oracle."""
     rng = np.random.default_rng(11)
     heads, blocks = 1, 1100
     lengths = np.full(blocks, 64, np.int32)
@@ -282,8 +318,8 @@ def test_more_cubes_than_one_list_run(dev):
     routes[0, :, 3] = 0
     for q in (2, 3, 4):
         routes[0, q, 3] = 1  # the neighbours keep block 3
-    print("vsa five list runs", flush=True)
-    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
+    print(f"vsa several list runs segmented={segmented}", flush=True)
+    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
     n = 64 * blocks
     rows = np.array([0, 1, 200, 230, 64 * 1050 + 3, 64 * 1099 + 63, 64 * 3 + 5], np.int32)
     want = O.vsa_attention_f64(qc, qs, kc, ks, vt, n, n, heads, routes, lengths, rows)

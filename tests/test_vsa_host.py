@@ -122,6 +122,24 @@ def test_vsa_attention_checks_routes_and_lengths():
     assert st == H.H3_ERR_CONFIG, H.last_error()
 
 
+def test_vsa_attention_workspace_is_checked():
+    """h3_vsa_attention_i8_ws: 135,168 bytes of segment states per (head, 64-query cube) item
+    (8 segments x 64 rows x (128 f16 + max and sum)), a null workspace refused."""
+    heads, blocks = 2, 5
+    n, w = 64 * blocks, 256
+    a = H.AttentionCfg(w, w, w, n, n, 0.088)
+    big = fake(1 << 28)
+    L = H.lib()
+    need = heads * blocks * 8 * 64 * (128 * 2 + 8)
+    st = L.h3_vsa_attention_i8_ws(ctypes.byref(a), n, heads, big, big, big, big, big, big, big,
+                                  big, fake(need - 1), None)
+    assert st == H.H3_ERR_BINDING
+    assert H.last_error() == f"VSA attention: workspace is {need - 1} bytes, the kernel addresses {need}"
+    st = L.h3_vsa_attention_i8_ws(ctypes.byref(a), n, heads, big, big, big, big, big, big, big,
+                                  big, H.raw_view(0, need), None)
+    assert st == H.H3_ERR_ARGUMENT and "null workspace" in H.last_error()
+
+
 def test_runtime_build_refuses_bad_options_without_allocating():
     src, inverse, lengths, prefix = H.vsa_plan([(0, 65), (65, 6)], 246, 5, 5, 7)
     with pytest.raises(H.H3Error, match="keep_percent"):
