@@ -200,9 +200,9 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
     default options (keep 10% of the non-prefix cubes per query cube and head, plus the
     diagonal +-1), INT8 attention. Times the whole runtime sequence (gather, pool, scores,
     route, operands, V^T, sparse attention, K-mean update, scatter) and the sparse attention
-    alone, in the runtime's form (per-XCD key segments on a workspace, h3_vsa_attention_i8_ws)
-    and in the allocation-free form (h3_vsa_attention_i8); counts the (query, key) pairs the
-    routes keep."""
+    alone, in the runtime's form (key scales transposed head-major into a lent workspace,
+    h3_vsa_attention_i8_ws) and in the allocation-free form on the token-major scales
+    (h3_vsa_attention_i8); counts the (query, key) pairs the routes keep."""
     import ctypes
 
     import numpy as np
@@ -219,12 +219,11 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
     out = torch.empty((tokens, width), dtype=torch.float16, device=dev)
     run_ms = time_launches(torch, lambda: vsa.attend(0, q, k, v, out), 3)
     b = vsa.buffers(0)
-    ws = torch.empty(H.vsa_attention_workspace_bytes(b.attention.tokens, heads), dtype=torch.uint8,
-                     device=dev)
+    ws = torch.empty(H.vsa_attention_workspace_bytes(b.attention), dtype=torch.uint8, device=dev)
     att_ms = time_launches(torch, lambda: H.vsa_attention_i8_ws(
         b.attention, b.attention.tokens, heads, b.qi, b.qs, b.ki, b.ks, b.vt, b.out, b.routes,
         b.lengths, ws), 5)
-    whole_ms = time_launches(torch, lambda: H.vsa_attention_i8(
+    plain_ms = time_launches(torch, lambda: H.vsa_attention_i8(
         b.attention, b.attention.tokens, heads, b.qi, b.qs, b.ki, b.ks, b.vt, b.out, b.routes,
         b.lengths), 3)
     nb = len(lengths)
@@ -246,7 +245,7 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
                     "N(0,1) q/k/v (K offset N(0,2))",
         "runtime_ms": round(run_ms, 3),
         "sparse_attention_ms": round(att_ms, 3),
-        "sparse_attention_whole_sequences_ms": round(whole_ms, 3),
+        "sparse_attention_token_major_scales_ms": round(plain_ms, 3),
         "density_useful": round(useful / (float(tokens) * tokens * heads), 4),
         "density_executed": round(executed / ((64.0 * nb) ** 2 * heads), 4),
         "useful_tops": round(4.0 * 128 * useful / (att_ms * 1e-3) / 1e12, 1),

@@ -205,9 +205,9 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
     h3_view rv[2] = {routes, lengths};
     size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
     if ((st = check_bindings(stage, rv, rneed, 2))) return st;
-    // A workspace selects the segmented kernel (per-segment softmax states, then a merge);
-    // without one every workgroup walks whole key sequences and nothing is allocated.
-    const size_t ws_need = vsa_workspace_bytes(token_count, heads);
+    // A workspace receives a head-major copy of the key scales, which the kernel then reads;
+    // without one it reads them token-major, and nothing is allocated either way.
+    const size_t ws_need = vsa_workspace_bytes(*cfg);
     if (workspace.ptr && workspace.bytes < ws_need)
       return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
                        stage, workspace.bytes, ws_need);
@@ -743,9 +743,8 @@ int h3_vsa_attention_i8(const h3_attention_cfg* cfg, uint32_t token_count, uint3
                           lengths);
 }
 
-size_t h3_vsa_attention_workspace_bytes(uint32_t token_count, uint32_t heads) {
-  if (device_ready("VSA attention workspace")) return 0;
-  return vsa_workspace_bytes(token_count, heads);
+size_t h3_vsa_attention_workspace_bytes(const h3_attention_cfg* cfg) {
+  return cfg ? vsa_workspace_bytes(*cfg) : 0;
 }
 
 int h3_vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,

@@ -125,9 +125,6 @@ struct Args {
   const int32_t* lengths;  // k_attention_vsa: live keys of each 64-key cube
   uint32_t blocks;         // k_attention_vsa: tokens / 64
   uint32_t base;           // k_attention_vsa: first (head, cube) item of this launch
-  uint32_t segs;           // k_attention_vsa: key segments per item
-  uint16_t* part_o;        // k_attention_vsa: per (item, segment) 64 rows of O / l, f16
-  float* part_ml;          // k_attention_vsa: per (item, segment) 64 rows of (running max, sum)
 };
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
@@ -677,14 +674,14 @@ void k_attention(Args a) {
 // workgroup, four workgroups share a CU, and the three-stage rings hold 32-key tiles (half a
 // cube): 3 x (4,352 + 8,192) bytes per workgroup.
 //
-// Memory: a kept cube costs 24.5 KB of K and V^T, and the kept sets of different query cubes are
-// unrelated, so when every workgroup walks a whole key sequence the K/V^T tiles of a head (49.5
-// MB at 129k tokens) stream through each XCD's 4 MB L2 and most reads miss. The key cubes are
-// therefore split into `segs` = 8 segments, and workgroup (cube, segment) runs on the XCD of its
-// segment (the hardware deals workgroup b to XCD b % 8), so each XCD's L2 serves one eighth of
-// a head's keys to all the query cubes it runs. Each workgroup leaves its segment's softmax
-// state, (running max, sum, O / sum in f16) per query, and k_vsa_merge combines the segments of a
-// query.
+// Memory: a kept cube costs 24.5 KB of K and V^T, and the kept sets of different query cubes
+// are unrelated, so the tiles mostly come from beyond L2. Two things keep that traffic down:
+// one launch per generation of resident workgroups (they start together and walk their
+// ascending key lists at about the same pace, so more shared tiles are still in L2), and key
+// scales in head-major order when the caller lends a workspace: token-major scales
+// ([token][head] f32) put each key's scale in its own 128-byte line shared with the other heads,
+// so a 32-key tile would pull 4 KB of lines for 128 bytes of scales (kHmScales: the launcher
+// first transposes them into the workspace).
 //
 // Per run of the key loop the workgroup scans its route row over the segment into an LDS list
 // of the live half-cubes it keeps (ascending keys, up to kVsaListMax per run; more runs continue
@@ -720,6 +717,7 @@ struct VsaStager {
 // K stage: as in k_attention (128-byte rows, chunks swizzled by (row/2)%8, row m holds key
 // swap23(m)). V^T stage: 64-byte rows (one channel, 32 keys), byte o holds row o/64, logical
 // chunk ((o/16)%4) ^ ((row/4)%4), so the sixteen rows a quarter-wave reads fall on distinct banks.
+template <bool kHmScales>
 __device__ __forceinline__ VsaStager make_vsa_stager(const Args& a, int wave, int lane) {
   VsaStager s;
   s.wave = wave;
@@ -736,12 +734,13 @@ __device__ __forceinline__ VsaStager make_vsa_stager(const Args& a, int wave, in
     s.voff[t] = row * a.capacity * 2 + 16 * chunk;
   }
   s.srow = kVsaSRows * wave + (lane & (kVsaSRows - 1));
-  s.soff = swap23(s.srow) * a.kv_head_limit * 4;
+  s.soff = swap23(s.srow) * (kHmScales ? 4u : a.kv_head_limit * 4);
   return s;
 }
 
 // LDS-DMA of the `live` keys of K tile k0 into stage `kst` (rows from `live` on load as zero),
-// and the load of this lane's key scale.
+// and the load of this lane's key scale (head-major or token-major scales).
+template <bool kHmScales>
 __device__ __forceinline__ float stage_k_vsa(const Args& a, const VsaStager& sg, uint32_t kv_head,
                                              uint32_t k0, uint32_t live, char* kst) {
   const char* base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * 128;
@@ -750,8 +749,10 @@ __device__ __forceinline__ float stage_k_vsa(const Args& a, const VsaStager& sg,
   for (int t = 0; t < kVsaKLoads; ++t)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rk, (lds_void*)(kst + (sg.wave * kVsaKLoads + t) * 1024), 16, sg.koff[t], 0, 0, 0);
-  const float* sbase = a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
-  const uint32_t sbytes = live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0u;
+  const float* sbase = kHmScales ? a.ks + (size_t)kv_head * a.tokens + k0
+                                 : a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
+  const uint32_t sbytes = kHmScales ? live * 4
+                                    : live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0u;
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(sbase, sbytes),
                                                                          sg.soff, 0, 0));
 }
@@ -901,9 +902,9 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
 
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// kSplit: workgroup (item, segment) leaves its segment's softmax state for k_vsa_merge.
-// Otherwise one workgroup walks all key cubes of its item and writes the output rows.
-template <bool kSplit>
+// kHmScales: a.ks is head-major, [kv_head_limit][tokens]; otherwise token-major as the
+// operands' producer writes it, [tokens][kv_head_limit].
+template <bool kHmScales>
 __global__ __launch_bounds__(kVsaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention_vsa(Args a) {
   __shared__ __attribute__((aligned(16))) char k0s[kVsaKStage];
@@ -915,15 +916,12 @@ void k_attention_vsa(Args a) {
   __shared__ uint32_t list[kVsaListMax];
   __shared__ uint32_t wave_counts[kVsaWaves];
 
-  // Workgroup b runs on XCD b % 8. Split: segment b % segs of item base + b / segs. Whole: the
-  // XCD-aware remap of k_attention over the launch's items (each XCD a contiguous range).
+  // XCD-aware remap of k_attention over the launch's items [base, base + total): each XCD runs
+  // a contiguous range of (head, cube) work.
   const uint32_t b = blockIdx.x;
-  const uint32_t seg = kSplit ? b % a.segs : 0u;
-  const uint32_t local = kSplit ? b / a.segs : (b & 7u) * a.per_xcd + (b >> 3);
+  const uint32_t local = (b & 7u) * a.per_xcd + (b >> 3);
   if (local >= a.total) return;
   const uint32_t logical = a.base + local;
-  const uint32_t seg_lo = kSplit ? (uint32_t)((uint64_t)a.blocks * seg / a.segs) : 0u;
-  const uint32_t seg_hi = kSplit ? (uint32_t)((uint64_t)a.blocks * (seg + 1) / a.segs) : a.blocks;
   const uint32_t head_y = logical / a.q_blocks;
   const uint32_t cube = logical % a.q_blocks;  // this workgroup's query cube
   const uint32_t kv_head = head_y % a.kv_head_limit;
@@ -936,7 +934,7 @@ void k_attention_vsa(Args a) {
   const uint32_t q = cube * 64 + wave * kQueriesPerWave + n;
   const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
 
-  const VsaStager sg = make_vsa_stager(a, wave, lane);
+  const VsaStager sg = make_vsa_stager<kHmScales>(a, wave, lane);
   v4i qop[4];
   {
     const int32_t* src = a.qi + (size_t)q_read * (a.q_row / 4) + head * 32;
@@ -965,21 +963,21 @@ void k_attention_vsa(Args a) {
     const uint32_t kb = at + threadIdx.x;
     keep = 0;
     len = 0;
-    if (kb < seg_hi) {
+    if (kb < a.blocks) {
       keep = route[kb];
       len = a.lengths[kb];
     }
   };
-  uint32_t scan = seg_lo;  // first key cube of the segment not yet listed
-  while (scan < seg_hi) {
+  uint32_t scan = 0;  // first key cube not yet listed
+  while (scan < a.blocks) {
     // ---- list the live halves of the kept cubes from `scan` on, kVsaThreads cubes per pass
     uint32_t count = 0;
     int32_t keep_next, len_next;
     fetch(scan, keep_next, len_next);
-    while (scan < seg_hi) {
+    while (scan < a.blocks) {
       const uint32_t kb = scan + threadIdx.x;
       const int32_t keep = keep_next, len = len_next;
-      if (scan + kVsaThreads < seg_hi) fetch(scan + kVsaThreads, keep_next, len_next);
+      if (scan + kVsaThreads < a.blocks) fetch(scan + kVsaThreads, keep_next, len_next);
       const uint32_t live = keep == 0 ? 0u : len < 0 ? 0u : len > 64 ? 64u : (uint32_t)len;
       const uint64_t ball0 = __ballot(live > 0);
       const uint64_t ball1 = __ballot(live > (uint32_t)kVsaKeys);
@@ -1015,14 +1013,14 @@ void k_attention_vsa(Args a) {
     uint32_t e2 = entry(2), e3 = entry(3);
     {
       const uint32_t e0 = entry(0), e1 = entry(1);
-      const float ks0 = stage_k_vsa(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
-      const float ks1 = stage_k_vsa(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
+      const float ks0 = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
+      const float ks1 = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
       stage_v_vsa(a, sg, kv_head, k0_of(e0), v0s);
       stage_v_vsa(a, sg, kv_head, k0_of(e1), v1s);
       store_scales_vsa(k0s, sg, ks0, live_of(e0));
       store_scales_vsa(k1s, sg, ks1, live_of(e1));
     }
-    float ks_held = stage_k_vsa(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
+    float ks_held = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
     step_barrier<kWaitAll>();
     first_tile_vsa(k0s, qop, qsl, st, u, n, half);
     step_barrier<kWaitAll>();
@@ -1031,7 +1029,7 @@ void k_attention_vsa(Args a) {
     // of K(j+2) into kn2.
 #define H3_VSA_STEP(kc, kn, kn2, vc, vn2)                                                      \
   {                                                                                          \
-    const float ks_new = stage_k_vsa(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
+    const float ks_new = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
     stage_v_vsa(a, sg, kv_head, k0_of(e2), vn2);                                             \
     const uint32_t e4 = entry(j + 4);                                                        \
     step_vsa<true>(kn, vc, qop, qsl, st, u, n, half);                                        \
@@ -1059,10 +1057,10 @@ void k_attention_vsa(Args a) {
     step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
   }
 
+  // ---- normalise and store rows < token_count
   const float l_tot = st.l + __shfl_xor(st.l, 32);
-  if (!kSplit) {  // ---- normalise and store rows < token_count
-    if (q >= a.token_count || q >= a.tokens) return;
-    const float inv = 1.0f / l_tot;
+  const float inv = 1.0f / l_tot;
+  if (q < a.token_count && q < a.tokens) {
     uint16_t* dst = a.out + (size_t)q * a.out_stride + head * 128;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -1073,72 +1071,26 @@ void k_attention_vsa(Args a) {
         *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
       }
     }
-    return;
   }
-  // ---- this segment's state of the workgroup's 64 queries: O / l in f16, (m, l) in f32
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  const size_t prow = ((size_t)local * a.segs + seg) * 64 + wave * kQueriesPerWave + n;
-  uint16_t* dst = a.part_o + prow * 128;
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v4h o = {(_Float16)(st.acc[db][4 * i + 0] * inv), (_Float16)(st.acc[db][4 * i + 1] * inv),
-               (_Float16)(st.acc[db][4 * i + 2] * inv), (_Float16)(st.acc[db][4 * i + 3] * inv)};
-      *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = o;
-    }
-  }
-  if (half == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * prow) = make_float2(st.m, l_tot);
 }
 
-// Combine the segments of each query of a k_attention_vsa launch: with M the largest running
-// max among the segments that saw a key and w_s = l_s * 2^(m_s - M),
-//   out = sum_s w_s * (O_s / l_s) / sum_s w_s,
-// the online softmax over all kept keys. 16 lanes per row, 8 channels each.
-__global__ __launch_bounds__(256) void k_vsa_merge(Args a) {
-  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
-  const uint32_t r = t >> 4, c8 = 8 * (t & 15);
-  if (r >= a.total * 64) return;
-  const uint32_t local = r >> 6, row = r & 63;
-  const uint32_t logical = a.base + local;
-  const uint32_t head_y = logical / a.q_blocks;
-  const uint32_t cube = logical % a.q_blocks;
-  const uint32_t head = (head_y % a.kv_head_limit) % a.head_limit;
-  const uint32_t q = cube * 64 + row;
-  if (q >= a.token_count || q >= a.tokens) return;
-  const size_t prow0 = (size_t)local * a.segs * 64 + row;  // segment s: prow0 + 64 s
-  float mx = -INFINITY;
-  for (uint32_t s = 0; s < a.segs; ++s) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * (prow0 + 64 * s));
-    if (ml.y > 0.0f) mx = fmaxf(mx, ml.x);
+// Transpose of the key scales of the VSA attention, [tokens][heads] -> [heads][tokens] f32,
+// through a 64 x 64 LDS tile (coalesced reads and writes).
+__global__ __launch_bounds__(256) void k_scales_head_major(const float* __restrict__ ks,
+                                                           float* __restrict__ out,
+                                                           uint32_t tokens, uint32_t heads) {
+  __shared__ float tile[64][65];
+  const uint32_t t0 = blockIdx.x * 64, h0 = blockIdx.y * 64;
+  const uint32_t x = threadIdx.x & 63, y = threadIdx.x >> 6;  // 64 x 4 threads
+  for (uint32_t r = y; r < 64; r += 4) {
+    const uint32_t t = t0 + r, h = h0 + x;
+    if (t < tokens && h < heads) tile[r][x] = ks[(size_t)t * heads + h];
   }
-  float acc[8] = {};
-  float wsum = 0.0f;
-  for (uint32_t s = 0; s < a.segs; ++s) {
-    const size_t prow = prow0 + 64 * s;
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * prow);
-    if (!(ml.y > 0.0f)) continue;
-    const float w = ml.y * __builtin_amdgcn_exp2f(ml.x - mx);
-    wsum += w;
-    const uint4 v = *reinterpret_cast<const uint4*>(a.part_o + prow * 128 + c8);
-    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const v2h h = __builtin_bit_cast(v2h, words[j]);
-      acc[2 * j] = __builtin_fmaf(w, (float)h[0], acc[2 * j]);
-      acc[2 * j + 1] = __builtin_fmaf(w, (float)h[1], acc[2 * j + 1]);
-    }
+  __syncthreads();
+  for (uint32_t r = y; r < 64; r += 4) {
+    const uint32_t h = h0 + r, t = t0 + x;
+    if (t < tokens && h < heads) out[(size_t)h * tokens + t] = tile[x][r];
   }
-  const float inv = 1.0f / wsum;
-  uint32_t o[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const v2h h = {(_Float16)(acc[2 * j] * inv), (_Float16)(acc[2 * j + 1] * inv)};
-    o[j] = __builtin_bit_cast(uint32_t, h);
-  }
-  uint2* dst = reinterpret_cast<uint2*>(a.out + (size_t)q * a.out_stride + head * 128 + c8);
-  dst[0] = make_uint2(o[0], o[1]);  // 8-byte stores: the output needs 8-byte alignment only
-  dst[1] = make_uint2(o[2], o[3]);
 }
 
 // ---------------------------------------------------------------- cross-attention (GQA, key mask)
@@ -1355,19 +1307,8 @@ static uint32_t device_cus() {
   return (uint32_t)cus[dev];
 }
 
-constexpr uint32_t kVsaSegs = 8;  // key segments: one per XCD
-
-// (head, query cube) items per launch of k_attention_vsa and k_vsa_merge: eight generations of
-// resident workgroups (four per CU), i.e. 1,024 items of 8 segments on 256 CUs. Measured at 129k
-// tokens: one generation per launch 49.0 ms (launch-bound), four 40.1 ms, eight 39.3 ms,
-// sixteen 39.5 ms; 4 segments 42.8 ms, 16 segments 42.5 ms.
-static uint32_t vsa_launch_items(uint32_t items) {
-  return std::min(items, std::max(1u, 8u * 4u * device_cus() / kVsaSegs));
-}
-
-size_t vsa_workspace_bytes(uint32_t token_count, uint32_t heads) {
-  const uint32_t items = (token_count + 63) / 64 * heads;
-  return (size_t)std::max(1u, vsa_launch_items(items)) * kVsaSegs * 64 * (128 * 2 + 2 * 4);
+size_t vsa_workspace_bytes(const h3_attention_cfg& cfg) {
+  return (size_t)(cfg.kv_stride / 128) * cfg.tokens * 4;
 }
 
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
@@ -1388,41 +1329,33 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
   a.q_row = cfg.q_stride;
   a.kv_bytes = cfg.kv_stride;
   a.out_stride = cfg.out_stride;
-  a.q_blocks = (token_count + 63) / 64;  // one query cube per item
+  a.q_blocks = (token_count + 63) / 64;  // one query cube per workgroup
   a.heads = heads;
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
   a.routes = routes;
   a.lengths = lengths;
   a.blocks = cfg.tokens / 64;
-  const uint32_t items = a.q_blocks * heads;
-  if (!workspace) {
-    // Whole key sequences, one launch per generation of resident workgroups (four per CU): its
-    // workgroups start together and walk their ascending key lists at about the same pace, so
-    // more of the tiles they share are still in L2 (measured at 129k tokens: 45.9 ms against
-    // 56.5 ms for one launch of all the work).
-    a.segs = 1;
-    const uint32_t gen = std::max(1u, 4u * device_cus());
-    for (uint32_t base = 0; base < items; base += gen) {
-      a.base = base;
-      a.total = std::min(gen, items - base);
-      a.per_xcd = (a.total + 7) / 8;
-      hipLaunchKernelGGL(k_attention_vsa<false>, dim3(a.per_xcd * 8), dim3(kVsaThreads), 0,
-                         stream, a);
-    }
-    return hipGetLastError();
+  if (workspace) {  // head-major key scales for the kernel
+    float* ks_hm = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(k_scales_head_major, dim3((a.tokens + 63) / 64, (a.kv_head_limit + 63) / 64),
+                       dim3(256), 0, stream, ks, ks_hm, a.tokens, a.kv_head_limit);
+    a.ks = ks_hm;
   }
-  a.segs = kVsaSegs;
-  const uint32_t gen = std::max(1u, vsa_launch_items(items));
-  a.part_o = static_cast<uint16_t*>(workspace);
-  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                       (size_t)gen * kVsaSegs * 64 * 128 * 2);
+  // One launch per generation of resident workgroups (four per CU): its workgroups start
+  // together and walk their ascending key lists at about the same pace, so more of the tiles
+  // they share are still in L2 (measured at 129k tokens with token-major scales: 45.9 ms against
+  // 56.5 ms for one launch of all the work).
+  const uint32_t items = a.q_blocks * heads;
+  const uint32_t gen = std::max(1u, 4u * device_cus());
   for (uint32_t base = 0; base < items; base += gen) {
     a.base = base;
     a.total = std::min(gen, items - base);
-    hipLaunchKernelGGL(k_attention_vsa<true>, dim3(a.total * kVsaSegs), dim3(kVsaThreads), 0,
-                       stream, a);
-    hipLaunchKernelGGL(k_vsa_merge, dim3((a.total * 64 * 16 + 255) / 256), dim3(256), 0, stream, a);
+    a.per_xcd = (a.total + 7) / 8;
+    if (workspace)
+      hipLaunchKernelGGL(k_attention_vsa<true>, dim3(a.per_xcd * 8), dim3(kVsaThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL(k_attention_vsa<false>, dim3(a.per_xcd * 8), dim3(kVsaThreads), 0, stream, a);
   }
   return hipGetLastError();
 }

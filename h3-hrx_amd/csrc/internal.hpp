@@ -84,18 +84,17 @@ hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, co
                                   const int32_t* ki, const float* ks, const uint16_t* vt,
                                   const uint8_t* key_mask, uint16_t* out, hipStream_t stream);
 // The int8 token-major attention over the cubes `routes` keeps (attention.hip). With a
-// `workspace` of vsa_workspace_bytes(token_count, heads) bytes the key cubes are walked in
-// per-XCD segments whose softmax states it holds (reused launch after launch on `stream`);
-// with nullptr every workgroup walks whole key sequences.
+// `workspace` of vsa_workspace_bytes(cfg) bytes the key scales are first transposed into it
+// (head-major) and the kernel reads them from there; with nullptr it reads the token-major
+// scales (one 128-byte line per key and head).
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
                                 uint32_t heads, const int32_t* qi, const float* qs,
                                 const int32_t* ki, const float* ks, const uint16_t* vt,
                                 uint16_t* out, const int32_t* routes, const int32_t* lengths,
                                 void* workspace, hipStream_t stream);
-size_t vsa_workspace_bytes(uint32_t token_count, uint32_t heads);
-// h3_vsa_attention_i8 with a caller's workspace of at least vsa_workspace_bytes(token_count,
-// heads) bytes (abi.cpp); with an empty view it runs the whole-sequence kernel as the public
-// entry point does.
+size_t vsa_workspace_bytes(const h3_attention_cfg& cfg);
+// h3_vsa_attention_i8 with a caller's workspace of at least vsa_workspace_bytes(*cfg) bytes
+// (abi.cpp); with an empty view it reads the token-major scales as the public entry point does.
 int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_view workspace, hipStream_t stream);

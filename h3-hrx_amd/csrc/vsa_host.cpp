@@ -36,7 +36,7 @@ struct h3_vsa {
   h3_view src{}, inverse{}, lengths{};
   h3_view q{}, k{}, v{}, qm{}, km{}, vm{}, coarse{}, scores{}, routes{}, out{};
   h3_view qi{}, ki{}, qs{}, ks{}, vt{}, zero{};
-  h3_view ws{};  // the sparse attention's per-segment softmax states
+  h3_view ws{};  // the sparse attention's head-major copy of the key scales
   std::vector<h3_view> means;  // the previous call's K mean of each layer
 };
 
@@ -227,7 +227,7 @@ int h3_vsa_build(const int32_t* src, const int32_t* inverse, const int32_t* leng
                 {&r->ks, (size_t)n * heads * 4, nullptr},
                 {&r->vt, nw2, nullptr},
                 {&r->zero, (size_t)width * 4, nullptr},
-                {&r->ws, vsa_workspace_bytes(n, heads), nullptr}};
+                {&r->ws, vsa_workspace_bytes(r->attention), nullptr}};
   for (auto& a : allocs) {
     if ((st = allocate(a.v, a.bytes, a.upload))) {
       release(r);

@@ -220,7 +220,7 @@ SIGNATURES = {
     "h3_vsa_attention_i8_ws": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, View, View, _S], ctypes.c_int),
-    "h3_vsa_attention_workspace_bytes": ([ctypes.c_uint32, ctypes.c_uint32], ctypes.c_size_t),
+    "h3_vsa_attention_workspace_bytes": ([_P(AttentionCfg)], ctypes.c_size_t),
     "h3_vsa_plan_blocks": (
         [_P(VsaSegment), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
          _P(ctypes.c_uint32)], ctypes.c_int),
@@ -536,8 +536,8 @@ def vsa_attention_i8(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki
                                     view(lengths), stream_ptr(stream)))
 
 
-def vsa_attention_workspace_bytes(token_count: int, heads: int) -> int:
-    return int(lib().h3_vsa_attention_workspace_bytes(token_count, heads))
+def vsa_attention_workspace_bytes(cfg: AttentionCfg) -> int:
+    return int(lib().h3_vsa_attention_workspace_bytes(ctypes.byref(cfg)))
 
 
 def vsa_attention_i8_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,

@@ -389,26 +389,25 @@ int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_st
  * 64kb + j with routes[h][t/64][kb] != 0 and j < lengths[kb]. cfg->tokens = padded (a multiple
  * of 64, blocks = tokens/64 <= 16384), token operands as h3_attention_i8qk; routes
  * [out_stride/128][blocks][blocks] i32, lengths [blocks] i32. qs must be positive (the quantizer's
- * scales are). Allocates nothing: every workgroup walks the kept cubes of one query cube over
- * the whole key sequence. h3_vsa_attention_i8_ws is the faster form for callers that can lend a
- * workspace. */
+ * scales are). Allocates nothing. h3_vsa_attention_i8_ws is the faster form for callers that
+ * can lend a workspace. */
 int h3_vsa_attention_i8(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_stream stream);
 /* h3_vsa_attention_i8_ws: no counterpart in the reference; h3_vsa_attention_i8 for callers that
- * can lend device memory (the VSA runtime, h3_vsa_attend, lends its own). The key cubes are
- * walked in eight segments, each on its own XCD so that its L2 serves one eighth of a head, and a
- * merge combines the segments' softmax states, which `workspace` holds: at least
- * h3_vsa_attention_workspace_bytes(token_count, heads) bytes (135 KB per (head, 64-query cube),
- * at most 138 MB on a 256-CU device), reused by the call's launches in stream order, so calls
- * that share a workspace must not overlap. A short workspace fails with H3_ERR_BINDING, a null
- * one with H3_ERR_ARGUMENT. Same results to within f16 rounding of the segment states. */
+ * can lend device memory (the VSA runtime, h3_vsa_attend, lends its own). The token-major key
+ * scales put each (key, head) scale in a 128-byte line shared with the other heads, so every
+ * key tile pulls one line per key; this form first transposes them head-major into
+ * `workspace` (h3_vsa_attention_workspace_bytes(cfg) = (kv_stride/128) * tokens * 4 bytes,
+ * 16.5 MB at 129k tokens and 32 heads) and reads them from there. Results are bit-identical to
+ * h3_vsa_attention_i8. Calls that share a workspace must not overlap. A short workspace fails
+ * with H3_ERR_BINDING, a null one with H3_ERR_ARGUMENT. */
 int h3_vsa_attention_i8_ws(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                            h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                            h3_view out, h3_view routes, h3_view lengths, h3_view workspace,
                            h3_stream stream);
-/* Workspace bytes h3_vsa_attention_i8_ws needs on the current device (0 without a device). */
-size_t h3_vsa_attention_workspace_bytes(uint32_t token_count, uint32_t heads);
+/* Workspace bytes h3_vsa_attention_i8_ws needs for `cfg` (0 for a null cfg). */
+size_t h3_vsa_attention_workspace_bytes(const h3_attention_cfg *cfg);
 
 /* ---- VSA host policy (src/vsa.rs), no device work */
 

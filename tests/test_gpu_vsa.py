@@ -11,9 +11,9 @@
     token-major attention to within f16 rounding (max-abs 2e-3; the two walk the keys in tiles
     of 32 and 64, so their lazy running maxima and f16 partial sums round differently); and
     past one list run (more than 512 listed half-cubes) it still matches the oracle. Each case
-    runs both forms: whole key sequences (h3_vsa_attention_i8) and per-XCD key segments with a
-    merge (h3_vsa_attention_i8_ws, on a NaN-filled workspace), which also agree with each other
-    to within the f16 rounding of the segment states;
+    runs both forms: token-major key scales (h3_vsa_attention_i8) and scales transposed
+    head-major into a NaN-filled workspace (h3_vsa_attention_i8_ws), whose outputs are also
+    bit-identical to each other;
   - the runtime (Runtime::emit) reproduces the reference's device test
     (src/vsa/device.rs:503-760): its intermediate buffers equal the oracle's bit for bit, the
     output's normalised RMSE against the independent masked attention is below 0.03 plain and
@@ -202,9 +202,9 @@ def random_routes(rng, heads, blocks, prefix, p):
 
 
 def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_count=None,
-                      segmented=False):
-    """h3_vsa_attention_i8 (whole key sequences) or, segmented, h3_vsa_attention_i8_ws (per-XCD
-    key segments and a merge, on a workspace filled with NaN beforehand)."""
+                      lent=False):
+    """h3_vsa_attention_i8 (token-major key scales) or, lent, h3_vsa_attention_i8_ws (the
+    scales transposed head-major into a workspace filled with NaN beforehand)."""
     import torch
 
     n = qc.shape[0]
@@ -215,9 +215,9 @@ def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_cou
     args = (cfg, token_count, heads, to_dev(pack_codes(qc), dev), to_dev(qs, dev),
             to_dev(pack_codes(kc), dev), to_dev(ks, dev), to_dev(vt, dev), out,
             to_dev(routes, dev), to_dev(lengths, dev))
-    if segmented:
-        nbytes = H.vsa_attention_workspace_bytes(token_count, heads)
-        assert nbytes > 0 and nbytes % (8 * 64 * 264) == 0  # whole (head, cube) items
+    if lent:
+        nbytes = H.vsa_attention_workspace_bytes(cfg)
+        assert nbytes == heads * n * 4
         ws = torch.full((nbytes // 2,), 0x7E00, dtype=torch.int16, device=dev)
         H.vsa_attention_i8_ws(*args, ws)
     else:
@@ -225,7 +225,7 @@ def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_cou
     return from_dev(out).reshape(token_count, w)
 
 
-SEGMENTED = pytest.mark.parametrize("segmented", [False, True], ids=["whole", "segmented"])
+LENT = pytest.mark.parametrize("lent", [False, True], ids=["plain", "workspace"])
 
 
 @pytest.mark.parametrize("lengths,prefix,p", [
@@ -235,16 +235,16 @@ SEGMENTED = pytest.mark.parametrize("segmented", [False, True], ids=["whole", "s
     ([64, 17, 64, 64, 1, 64, 40, 64, 64, 33, 64], 0, 0.25),
     ([32, 64, 33, 31, 64, 64, 2], 1, 0.3),
 ])
-@SEGMENTED
-def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p, segmented):
+@LENT
+def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p, lent):
     rng = np.random.default_rng(len(lengths) * 13 + prefix)
     heads = 2
     lengths = np.array(lengths, np.int32)
     blocks = len(lengths)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = random_routes(rng, heads, blocks, prefix, p)
-    print(f"vsa attention blocks={blocks} prefix={prefix} p={p} segmented={segmented}", flush=True)
-    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
+    print(f"vsa attention blocks={blocks} prefix={prefix} p={p} lent={lent}", flush=True)
+    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, lent=lent)
     n = 64 * blocks
     want = O.vsa_attention_f64(qc, qs, kc, ks, vt, n, n, heads, routes, lengths,
                                np.arange(n, dtype=np.int32)).reshape(n, -1)
@@ -252,43 +252,42 @@ def test_sparse_attention_matches_the_oracle(dev, lengths, prefix, p, segmented)
     assert mx < 2e-2 and mean < 2e-3, (mx, mean)
 
 
-@SEGMENTED
-def test_token_count_limits_the_rows_written(dev, segmented):
+@LENT
+def test_token_count_limits_the_rows_written(dev, lent):
     rng = np.random.default_rng(3)
     heads, lengths = 1, np.array([64, 64, 64], np.int32)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = random_routes(rng, heads, 3, 0, 0.5)
-    full = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
+    full = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, lent=lent)
     part = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_count=100,
-                             segmented=segmented)
+                             lent=lent)
     assert np.array_equal(part, full[:100])
 
 
-def test_segmented_and_whole_paths_agree(dev):
-    """The two forms differ only in rounding: the segment states are f16 before the merge."""
+def test_plain_and_workspace_forms_are_identical(dev):
+    """The two forms read the same scales from different layouts: bit-identical outputs."""
     rng = np.random.default_rng(21)
     heads, lengths = 3, np.array([64, 40, 64, 64, 7, 64, 64, 64, 33, 64, 64, 64, 64, 1, 64, 64,
                                   64, 64, 64], np.int32)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = random_routes(rng, heads, len(lengths), 1, 0.35)
     a = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads)
-    b = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=True)
-    a32, b32 = (x.view(np.float16).astype(np.float32) for x in (a, b))
-    assert np.isfinite(b32).all()
-    assert np.abs(a32 - b32).max() < 2e-3, np.abs(a32 - b32).max()
+    b = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, lent=True)
+    assert np.isfinite(b.view(np.float16)).all()
+    assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("blocks,heads", [(5, 2), (16, 3)])
-@SEGMENTED
-def test_every_block_routed_is_the_dense_attention(dev, blocks, heads, segmented):
+@LENT
+def test_every_block_routed_is_the_dense_attention(dev, blocks, heads, lent):
     import torch
 
     rng = np.random.default_rng(blocks)
     lengths = np.full(blocks, 64, np.int32)
     qc, qs, kc, ks, vt = sparse_operands(rng, heads, lengths)
     routes = np.ones((heads, blocks, blocks), np.int32)
-    print(f"vsa dense equivalence blocks={blocks} segmented={segmented}", flush=True)
-    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
+    print(f"vsa dense equivalence blocks={blocks} lent={lent}", flush=True)
+    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, lent=lent)
     n, w = 64 * blocks, heads * 128
     cfg = H.AttentionCfg(w, w, w, n, n, H.config_f32(1 / math.sqrt(128)))
     out = torch.zeros((n * w,), dtype=torch.int16, device=dev)
@@ -304,11 +303,10 @@ def test_every_block_routed_is_the_dense_attention(dev, blocks, heads, segmented
     assert mx < 2e-2 and mean < 2e-3, (mx, mean)
 
 
-@SEGMENTED
-def test_more_cubes_than_one_list_run(dev, segmented):
+@LENT
+def test_more_cubes_than_one_list_run(dev, lent):
     """1100 cubes, nearly all routed: 2,197 or 2,199 live half-cubes per query cube, so the key
-    loop runs five times (512 listed half-cubes per run) in the whole form, once per segment of
-    about 274 half-cubes in the segmented form, and must still match the oracle."""
+    loop runs five times (512 listed half-cubes per run) and must still match the oracle."""
     rng = np.random.default_rng(11)
     heads, blocks = 1, 1100
     lengths = np.full(blocks, 64, np.int32)
@@ -318,8 +316,8 @@ def test_more_cubes_than_one_list_run(dev, segmented):
     routes[0, :, 3] = 0
     for q in (2, 3, 4):
         routes[0, q, 3] = 1  # the neighbours keep block 3
-    print(f"vsa several list runs segmented={segmented}", flush=True)
-    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, segmented=segmented)
+    print(f"vsa several list runs lent={lent}", flush=True)
+    got = run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, lent=lent)
     n = 64 * blocks
     rows = np.array([0, 1, 200, 230, 64 * 1050 + 3, 64 * 1099 + 63, 64 * 3 + 5], np.int32)
     want = O.vsa_attention_f64(qc, qs, kc, ks, vt, n, n, heads, routes, lengths, rows)

@@ -123,14 +123,15 @@ def test_vsa_attention_checks_routes_and_lengths():
 
 
 def test_vsa_attention_workspace_is_checked():
-    """h3_vsa_attention_i8_ws: 135,168 bytes of segment states per (head, 64-query cube) item
-    (8 segments x 64 rows x (128 f16 + max and sum)), a null workspace refused."""
+    """h3_vsa_attention_i8_ws: a head-major copy of the key scales, (kv_stride/128) x tokens
+    f32; a short or null workspace refused."""
     heads, blocks = 2, 5
     n, w = 64 * blocks, 256
     a = H.AttentionCfg(w, w, w, n, n, 0.088)
     big = fake(1 << 28)
     L = H.lib()
-    need = heads * blocks * 8 * 64 * (128 * 2 + 8)
+    need = (w // 128) * n * 4
+    assert H.vsa_attention_workspace_bytes(a) == need
     st = L.h3_vsa_attention_i8_ws(ctypes.byref(a), n, heads, big, big, big, big, big, big, big,
                                   big, fake(need - 1), None)
     assert st == H.H3_ERR_BINDING
