@@ -73,7 +73,9 @@ def time_launches(torch, fn, reps):
 def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
     """The INT4 QK family at the same shape (BASELINE config 5a's int4 QK, with the reference's
     per-(token, head) absmax/7 scales): prepare_qk_i4 of Q and K from the fused rows, then
-    attention_i4qk and its skip twin at tau = 2 (natural-log units of the scores)."""
+    attention_i4qk and its skip twin at tau = 2 (natural-log units of the scores), each with the
+    key scales read from a head-major copy in a lent workspace (the _ws forms) and, as the
+    reference's bindings give them, token-major."""
     width = heads * 128
     cap = H.capacity(tokens)
     qi = torch.zeros((cap, width // 8), dtype=torch.int32, device=dev)
@@ -87,16 +89,24 @@ def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
                                             H.prepare_qk_i4(pk, tokens, fused, None, ki, ks)), 5)
     ac = H.AttentionCfg(width, width, width, tokens, cap, 1.0)
     ops = 4.0 * tokens * tokens * heads * 128
-    att_ms = time_launches(torch, lambda: H.attention_i4qk(ac, tokens, heads, qi, qs, ki, ks, vt,
-                                                           out), 2)
+    ws = torch.empty(H.scales_workspace_bytes(ac), dtype=torch.uint8, device=dev)
+    att_ms = time_launches(torch, lambda: H.attention_i4qk_ws(ac, tokens, heads, qi, qs, ki, ks,
+                                                              vt, out, ws), 2)
+    att_tm_ms = time_launches(torch, lambda: H.attention_i4qk(ac, tokens, heads, qi, qs, ki, ks,
+                                                              vt, out), 2)
     sc = H.AttentionSkipCfg(width, width, width, tokens, cap, 1.0, 2.0)
-    skip_ms = time_launches(torch, lambda: H.attention_i4qks(sc, tokens, heads, qi, qs, ki, ks,
-                                                             vt, out), 2)
+    skip_ms = time_launches(torch, lambda: H.attention_i4qks_ws(sc, tokens, heads, qi, qs, ki,
+                                                                ks, vt, out, ws), 2)
+    skip_tm_ms = time_launches(torch, lambda: H.attention_i4qks(sc, tokens, heads, qi, qs, ki, ks,
+                                                                vt, out), 2)
     return {"prepare_qk_i4_x2_ms": round(prep_ms, 4),
             "attention_i4qk_ms": round(att_ms, 3),
             "attention_i4qk_tops": round(ops / (att_ms * 1e-3) / 1e12, 1),
+            "attention_i4qk_token_major_scales_ms": round(att_tm_ms, 3),
             "attention_i4qks_tau2_ms": round(skip_ms, 3),
-            "note": "no int4 MFMA on gfx950: codes are widened to int8 in registers"}
+            "attention_i4qks_tau2_token_major_scales_ms": round(skip_tm_ms, 3),
+            "note": "no int4 MFMA on gfx950: codes are widened to int8 in registers; _ms figures "
+                    "use the _ws forms (key scales copied head-major into a lent workspace)"}
 
 
 def adjacent_kernels(torch, H, dev, tokens, width, out):
@@ -219,7 +229,7 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
     out = torch.empty((tokens, width), dtype=torch.float16, device=dev)
     run_ms = time_launches(torch, lambda: vsa.attend(0, q, k, v, out), 3)
     b = vsa.buffers(0)
-    ws = torch.empty(H.vsa_attention_workspace_bytes(b.attention), dtype=torch.uint8, device=dev)
+    ws = torch.empty(H.scales_workspace_bytes(b.attention), dtype=torch.uint8, device=dev)
     att_ms = time_launches(torch, lambda: H.vsa_attention_i8_ws(
         b.attention, b.attention.tokens, heads, b.qi, b.qs, b.ki, b.ks, b.vt, b.out, b.routes,
         b.lengths, ws), 5)

@@ -195,6 +195,14 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   h3_view views[6] = {qi, qs, ki, ks, vt, out};
   int st = check_bindings(stage, views, need, 6);
   if (st) return st;
+  // A workspace (token-major operands) receives a head-major copy of the key scales, which the
+  // kernel then reads; without one it reads them token-major. Nothing is allocated either way.
+  if (workspace.ptr) {
+    const size_t ws_need = scales_workspace_bytes(*cfg);
+    if (workspace.bytes < ws_need)
+      return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
+                       stage, workspace.bytes, ws_need);
+  }
   if (vsa) {
     // kernels/vsa_attention_8.loom:145-150: blocks = tokens / 64, routes [heads][blocks][blocks]
     // i32, lengths [blocks] i32. Whole cubes only: tokens is the padded row count.
@@ -205,12 +213,6 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
     h3_view rv[2] = {routes, lengths};
     size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
     if ((st = check_bindings(stage, rv, rneed, 2))) return st;
-    // A workspace receives a head-major copy of the key scales, which the kernel then reads;
-    // without one it reads them token-major, and nothing is allocated either way.
-    const size_t ws_need = vsa_workspace_bytes(*cfg);
-    if (workspace.ptr && workspace.bytes < ws_need)
-      return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
-                       stage, workspace.bytes, ws_need);
     if ((st = device_ready(stage))) return st;
     return launched(stage, launch_attention_vsa(*cfg, token_count, heads,
                                                 static_cast<const int32_t*>(qi.ptr),
@@ -230,7 +232,8 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
                                           static_cast<const int32_t*>(ki.ptr),
                                           static_cast<const float*>(ks.ptr),
                                           static_cast<const uint16_t*>(vt.ptr),
-                                          static_cast<uint16_t*>(out.ptr), stream));
+                                          static_cast<uint16_t*>(out.ptr), workspace.ptr,
+                                          stream));
 }
 
 // kernels/vsa_ops.loom:3-9 (h3.vsa.*), plus the relations src/vsa/device.rs:63-77 builds the
@@ -542,9 +545,10 @@ int h3_attention_i4qk(const h3_attention_cfg* cfg, uint32_t token_count, uint32_
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI4);
 }
 
-int h3_attention_i4qks(const h3_attention_skip_cfg* cfg, uint32_t token_count, uint32_t heads,
-                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
-                       h3_stream stream) {
+namespace {
+int attention_i4qks(const h3_attention_skip_cfg* cfg, uint32_t token_count, uint32_t heads,
+                    h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                    h3_view workspace, h3_stream stream) {
   const char* stage = "attention_i4qks";
   if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
   if (!(cfg->skip_tau == cfg->skip_tau) || cfg->skip_tau > 3.0e38f || cfg->skip_tau < -3.0e38f)
@@ -553,7 +557,47 @@ int h3_attention_i4qks(const h3_attention_skip_cfg* cfg, uint32_t token_count, u
                                  cfg->token_capacity, cfg->scale};
   return attention_common(stage, &base, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI4Skip,
-                          cfg->skip_tau);
+                          cfg->skip_tau, {}, {}, workspace);
+}
+
+int null_workspace(const char* stage) {
+  return set_error(H3_ERR_ARGUMENT, "%s: null workspace (use the form without _ws)", stage);
+}
+}  // namespace
+
+int h3_attention_i4qks(const h3_attention_skip_cfg* cfg, uint32_t token_count, uint32_t heads,
+                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                       h3_stream stream) {
+  return attention_i4qks(cfg, token_count, heads, qi, qs, ki, ks, vt, out, {}, stream);
+}
+
+size_t h3_scales_workspace_bytes(const h3_attention_cfg* cfg) {
+  return cfg ? scales_workspace_bytes(*cfg) : 0;
+}
+
+int h3_attention_i8qk_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                         h3_view workspace, h3_stream stream) {
+  if (!workspace.ptr) return null_workspace("attention_i8qk");
+  return attention_common("attention_i8qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI8, 0.0f, {}, {},
+                          workspace);
+}
+
+int h3_attention_i4qk_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                         h3_view workspace, h3_stream stream) {
+  if (!workspace.ptr) return null_workspace("attention_i4qk");
+  return attention_common("attention_i4qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI4, 0.0f, {}, {},
+                          workspace);
+}
+
+int h3_attention_i4qks_ws(const h3_attention_skip_cfg* cfg, uint32_t token_count, uint32_t heads,
+                          h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                          h3_view out, h3_view workspace, h3_stream stream) {
+  if (!workspace.ptr) return null_workspace("attention_i4qks");
+  return attention_i4qks(cfg, token_count, heads, qi, qs, ki, ks, vt, out, workspace, stream);
 }
 
 // ---------------------------------------------------------------- VSA (kernels/vsa_ops.loom)
@@ -743,16 +787,11 @@ int h3_vsa_attention_i8(const h3_attention_cfg* cfg, uint32_t token_count, uint3
                           lengths);
 }
 
-size_t h3_vsa_attention_workspace_bytes(const h3_attention_cfg* cfg) {
-  return cfg ? vsa_workspace_bytes(*cfg) : 0;
-}
-
 int h3_vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                            h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                            h3_view out, h3_view routes, h3_view lengths, h3_view workspace,
                            h3_stream stream) {
-  if (!workspace.ptr)
-    return set_error(H3_ERR_ARGUMENT, "VSA attention: null workspace (use h3_vsa_attention_i8)");
+  if (!workspace.ptr) return null_workspace("VSA attention");
   return vsa_attention_i8_ws(cfg, token_count, heads, qi, qs, ki, ks, vt, out, routes, lengths,
                              workspace, reinterpret_cast<hipStream_t>(stream));
 }

@@ -148,7 +148,9 @@ struct Stager {
 // LDS byte o of a K/V^T stage holds row o/128, logical chunk ((o/16)%8) ^ ((row/2)%8). An int4
 // K stage has 64-byte rows: byte o holds row o/64, logical chunk ((o/16)%4) ^ ((row/4)%4), so the
 // sixteen rows a quarter-wave reads with one 16-byte load each fall on distinct banks.
-template <int kMode>
+// kHmScales (token-major modes): the key scales are read from a head-major copy,
+// [kv_head_limit][tokens], instead of the token-major [token][kv_head_limit] array.
+template <int kMode, bool kHmScales = false>
 __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
   Stager s;
@@ -177,13 +179,13 @@ __device__ __forceinline__ Stager make_stager(const Args& a, int wave, int lane)
   }
   s.srow = kSRows * wave + (lane & (kSRows - 1));
   const uint32_t skey = swap23(s.srow);
-  s.soff = kHeadMajor ? skey * 4 : skey * a.kv_head_limit * 4;
+  s.soff = kHeadMajor || kHmScales ? skey * 4 : skey * a.kv_head_limit * 4;
   return s;
 }
 
 // LDS-DMA of K tile k0 (rows past the sequence load as zero) into stage `kst`, and the load of
 // its scales into a register.
-template <int kMode>
+template <int kMode, bool kHmScales = false>
 __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32_t kv_head,
                                          uint32_t k0, char* kst) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
@@ -201,8 +203,13 @@ __device__ __forceinline__ float stage_k(const Args& a, const Stager& sg, uint32
   } else {
     base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * kCodeBytes;
     bytes = live ? (live - 1) * a.kv_bytes + kCodeBytes : 0;
-    sbase = a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
-    sbytes = live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0;
+    if (kHmScales) {
+      sbase = a.ks + (size_t)kv_head * a.tokens + k0;
+      sbytes = live * 4;
+    } else {
+      sbase = a.ks + (size_t)k0 * a.kv_head_limit + kv_head;
+      sbytes = live ? ((live - 1) * a.kv_head_limit + 1) * 4 : 0;
+    }
   }
   const __amdgpu_buffer_rsrc_t rk = rsrc(base, bytes);
 #pragma unroll
@@ -509,7 +516,7 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   if (!do_qk && do_pv) st.l += tile_sum(pb);
 }
 
-template <int kMode>
+template <int kMode, bool kHmScales = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention(Args a) {
   constexpr bool kHeadMajor = kMode == kHeadI8;
@@ -545,14 +552,14 @@ void k_attention(Args a) {
   const uint32_t q = q_tile_c * kQueriesPerWave + n;
   const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
 
-  const Stager sg = make_stager<kMode>(a, wave, lane);
+  const Stager sg = make_stager<kMode, kHmScales>(a, wave, lane);
   const uint32_t n_tiles = (a.tokens + kKeys - 1) / kKeys;
   const uint32_t full = a.tokens / kKeys;  // tiles with no key past the sequence
 
   // ---- prologue: K(0..2) and V(0..1) in flight, scales of K(0), K(1) stored, K(2)'s held
-  float ks0 = stage_k<kMode>(a, sg, kv_head, 0, k0s);
-  float ks1 = stage_k<kMode>(a, sg, kv_head, kKeys, k1s);
-  float ks_held = stage_k<kMode>(a, sg, kv_head, 2 * kKeys, k2s);
+  float ks0 = stage_k<kMode, kHmScales>(a, sg, kv_head, 0, k0s);
+  float ks1 = stage_k<kMode, kHmScales>(a, sg, kv_head, kKeys, k1s);
+  float ks_held = stage_k<kMode, kHmScales>(a, sg, kv_head, 2 * kKeys, k2s);
   stage_v(a, sg, kv_head, 0, v0s);
   stage_v(a, sg, kv_head, kKeys, v1s);
 
@@ -610,7 +617,7 @@ void k_attention(Args a) {
   // scales of K(j+2) (stage kn2) loaded one step earlier.
 #define H3_STEADY(kc, kn, kn2, vc, vn2)                                                       \
   {                                                                                          \
-    const float ks_new = stage_k<kMode>(a, sg, kv_head, (j + 3) * kKeys, kc);                \
+    const float ks_new = stage_k<kMode, kHmScales>(a, sg, kv_head, (j + 3) * kKeys, kc);           \
     stage_v(a, sg, kv_head, (j + 2) * kKeys, vn2);                                           \
     H3_STEP(true, false, false, kn, vc, (j + 1) * kKeys)                                     \
     store_scales<kMode>(kn2, sg, ks_held);                                                   \
@@ -1029,7 +1036,7 @@ void k_attention_vsa(Args a) {
     // of K(j+2) into kn2.
 #define H3_VSA_STEP(kc, kn, kn2, vc, vn2)                                                      \
   {                                                                                          \
-    const float ks_new = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
+    const float ks_new = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);       \
     stage_v_vsa(a, sg, kv_head, k0_of(e2), vn2);                                             \
     const uint32_t e4 = entry(j + 4);                                                        \
     step_vsa<true>(kn, vc, qop, qsl, st, u, n, half);                                        \
@@ -1231,7 +1238,7 @@ void k_attention_cross(Args a) {
 hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
                             uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
-                            const float* ks, const uint16_t* vt, uint16_t* out,
+                            const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream) {
   Args a;
   a.qi = qi;
@@ -1254,6 +1261,19 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
   a.total = a.q_blocks * heads;
   a.per_xcd = (a.total + 7) / 8;
   dim3 grid(a.per_xcd * 8);
+  if (workspace && mode != kHeadI8) {  // token-major codes, head-major copy of the key scales
+    float* ks_hm = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(k_scales_head_major, dim3((a.tokens + 63) / 64, (a.kv_head_limit + 63) / 64),
+                       dim3(256), 0, stream, ks, ks_hm, a.tokens, a.kv_head_limit);
+    a.ks = ks_hm;
+    if (mode == kTokenI4)
+      hipLaunchKernelGGL((k_attention<kTokenI4, true>), grid, dim3(kThreads), 0, stream, a);
+    else if (mode == kTokenI4Skip)
+      hipLaunchKernelGGL((k_attention<kTokenI4Skip, true>), grid, dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((k_attention<kTokenI8, true>), grid, dim3(kThreads), 0, stream, a);
+    return hipGetLastError();
+  }
   if (mode == kHeadI8)
     hipLaunchKernelGGL(k_attention<kHeadI8>, grid, dim3(kThreads), 0, stream, a);
   else if (mode == kTokenI4)
@@ -1307,7 +1327,7 @@ static uint32_t device_cus() {
   return (uint32_t)cus[dev];
 }
 
-size_t vsa_workspace_bytes(const h3_attention_cfg& cfg) {
+size_t scales_workspace_bytes(const h3_attention_cfg& cfg) {
   return (size_t)(cfg.kv_stride / 128) * cfg.tokens * 4;
 }
 

@@ -76,15 +76,18 @@ hipError_t launch_prepare_plain(uint32_t width, uint32_t out_stride, uint32_t el
 hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
                             uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
-                            const float* ks, const uint16_t* vt, uint16_t* out,
+                            const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream);
+// Bytes of the head-major key-scale copy the token-major attention kernels read when a caller
+// lends a workspace: (kv_stride / 128) * tokens f32.
+size_t scales_workspace_bytes(const h3_attention_cfg& cfg);
 
 // Cross-attention with grouped heads and a key-padding mask (attention.hip)
 hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
                                   const int32_t* ki, const float* ks, const uint16_t* vt,
                                   const uint8_t* key_mask, uint16_t* out, hipStream_t stream);
 // The int8 token-major attention over the cubes `routes` keeps (attention.hip). With a
-// `workspace` of vsa_workspace_bytes(cfg) bytes the key scales are first transposed into it
+// `workspace` of scales_workspace_bytes(cfg) bytes the key scales are first transposed into it
 // (head-major) and the kernel reads them from there; with nullptr it reads the token-major
 // scales (one 128-byte line per key and head).
 hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_count,
@@ -92,8 +95,7 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
                                 const int32_t* ki, const float* ks, const uint16_t* vt,
                                 uint16_t* out, const int32_t* routes, const int32_t* lengths,
                                 void* workspace, hipStream_t stream);
-size_t vsa_workspace_bytes(const h3_attention_cfg& cfg);
-// h3_vsa_attention_i8 with a caller's workspace of at least vsa_workspace_bytes(*cfg) bytes
+// h3_vsa_attention_i8 with a caller's workspace of at least scales_workspace_bytes(*cfg) bytes
 // (abi.cpp); with an empty view it reads the token-major scales as the public entry point does.
 int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,

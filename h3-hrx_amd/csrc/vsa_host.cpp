@@ -227,7 +227,7 @@ int h3_vsa_build(const int32_t* src, const int32_t* inverse, const int32_t* leng
                 {&r->ks, (size_t)n * heads * 4, nullptr},
                 {&r->vt, nw2, nullptr},
                 {&r->zero, (size_t)width * 4, nullptr},
-                {&r->ws, vsa_workspace_bytes(r->attention), nullptr}};
+                {&r->ws, scales_workspace_bytes(r->attention), nullptr}};
   for (auto& a : allocs) {
     if ((st = allocate(a.v, a.bytes, a.upload))) {
       release(r);

@@ -220,7 +220,16 @@ SIGNATURES = {
     "h3_vsa_attention_i8_ws": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, View, View, _S], ctypes.c_int),
-    "h3_vsa_attention_workspace_bytes": ([_P(AttentionCfg)], ctypes.c_size_t),
+    "h3_scales_workspace_bytes": ([_P(AttentionCfg)], ctypes.c_size_t),
+    "h3_attention_i8qk_ws": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         View, _S], ctypes.c_int),
+    "h3_attention_i4qk_ws": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         View, _S], ctypes.c_int),
+    "h3_attention_i4qks_ws": (
+        [_P(AttentionSkipCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View,
+         View, View, _S], ctypes.c_int),
     "h3_vsa_plan_blocks": (
         [_P(VsaSegment), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
          _P(ctypes.c_uint32)], ctypes.c_int),
@@ -536,8 +545,33 @@ def vsa_attention_i8(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki
                                     view(lengths), stream_ptr(stream)))
 
 
-def vsa_attention_workspace_bytes(cfg: AttentionCfg) -> int:
-    return int(lib().h3_vsa_attention_workspace_bytes(ctypes.byref(cfg)))
+def scales_workspace_bytes(cfg) -> int:
+    """Bytes of the head-major key-scale copy the _ws attention forms need for `cfg`."""
+    if isinstance(cfg, AttentionSkipCfg):
+        cfg = AttentionCfg(cfg.q_stride, cfg.kv_stride, cfg.out_stride, cfg.tokens,
+                           cfg.token_capacity, cfg.scale)
+    return int(lib().h3_scales_workspace_bytes(ctypes.byref(cfg)))
+
+
+def attention_i8qk_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                      workspace, stream=None) -> None:
+    check(lib().h3_attention_i8qk_ws(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                     view(ki), view(ks), view(vt), view(out), view(workspace),
+                                     stream_ptr(stream)))
+
+
+def attention_i4qk_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                      workspace, stream=None) -> None:
+    check(lib().h3_attention_i4qk_ws(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                     view(ki), view(ks), view(vt), view(out), view(workspace),
+                                     stream_ptr(stream)))
+
+
+def attention_i4qks_ws(cfg: AttentionSkipCfg, token_count: int, heads: int, qi, qs, ki, ks, vt,
+                       out, workspace, stream=None) -> None:
+    check(lib().h3_attention_i4qks_ws(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                      view(ki), view(ks), view(vt), view(out), view(workspace),
+                                      stream_ptr(stream)))
 
 
 def vsa_attention_i8_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,

@@ -297,6 +297,27 @@ int h3_attention_i4qks(const h3_attention_skip_cfg *cfg, uint32_t token_count, u
                        h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                        h3_stream stream);
 
+/* The _ws forms of the token-major attention entries (h3_attention_i8qk, h3_attention_i4qk,
+ * h3_attention_i4qks; h3_vsa_attention_i8_ws below) have no counterpart in the reference; they
+ * are for callers that can lend device memory. Token-major key scales ([token][heads] f32, the
+ * reference's layout) put every (key, head) scale in its own 128-byte line shared with the other
+ * heads, so each key tile pulls one line per key. A _ws form first transposes the scales
+ * head-major into `workspace`, at least h3_scales_workspace_bytes(cfg) = (kv_stride/128) *
+ * tokens * 4 bytes, and the kernel reads them from there (measured at 129k tokens and 32 heads:
+ * 7-8 % faster dense, 28 % faster VSA attention). Results are bit-identical to the form without
+ * _ws. Calls that share a workspace must not overlap. A short workspace fails with
+ * H3_ERR_BINDING, a null one with H3_ERR_ARGUMENT. */
+size_t h3_scales_workspace_bytes(const h3_attention_cfg *cfg);
+int h3_attention_i8qk_ws(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                         h3_view workspace, h3_stream stream);
+int h3_attention_i4qk_ws(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                         h3_view workspace, h3_stream stream);
+int h3_attention_i4qks_ws(const h3_attention_skip_cfg *cfg, uint32_t token_count, uint32_t heads,
+                          h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                          h3_view out, h3_view workspace, h3_stream stream);
+
 /* Cross-attention with grouped heads and a key-padding mask: BASELINE config 4's text
  * cross-attention (32 query heads over 8 key/value heads, 512 text tokens, padded positions
  * masked). An extension: the reference has no such kernel.
@@ -394,20 +415,15 @@ int h3_vsa_kmean(uint32_t width, uint32_t tokens, h3_view x, h3_view mean, h3_st
 int h3_vsa_attention_i8(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_stream stream);
-/* h3_vsa_attention_i8_ws: no counterpart in the reference; h3_vsa_attention_i8 for callers that
- * can lend device memory (the VSA runtime, h3_vsa_attend, lends its own). The token-major key
- * scales put each (key, head) scale in a 128-byte line shared with the other heads, so every
- * key tile pulls one line per key; this form first transposes them head-major into
- * `workspace` (h3_vsa_attention_workspace_bytes(cfg) = (kv_stride/128) * tokens * 4 bytes,
- * 16.5 MB at 129k tokens and 32 heads) and reads them from there. Results are bit-identical to
- * h3_vsa_attention_i8. Calls that share a workspace must not overlap. A short workspace fails
- * with H3_ERR_BINDING, a null one with H3_ERR_ARGUMENT. */
+/* h3_vsa_attention_i8_ws: h3_vsa_attention_i8 with the key scales read from a head-major copy in
+ * a lent workspace of h3_scales_workspace_bytes(cfg) bytes (16.5 MB at 129k tokens and 32
+ * heads), as the _ws forms above; no counterpart in the reference. The VSA runtime
+ * (h3_vsa_attend) lends its own. */
 int h3_vsa_attention_i8_ws(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                            h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                            h3_view out, h3_view routes, h3_view lengths, h3_view workspace,
                            h3_stream stream);
-/* Workspace bytes h3_vsa_attention_i8_ws needs for `cfg` (0 for a null cfg). */
-size_t h3_vsa_attention_workspace_bytes(const h3_attention_cfg *cfg);
+
 
 /* ---- VSA host policy (src/vsa.rs), no device work */
 

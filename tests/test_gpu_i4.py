@@ -256,3 +256,42 @@ def test_skip_twin_drops_exactly_the_far_tiles(dev):
     mx, mean = north_star_ok(got[rows], want)
     assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
     assert np.abs(full - want).max() > 0.05  # the dropped tiles carry real weight
+
+
+@pytest.mark.parametrize("tokens,heads", [(97, 2), (1000, 3), (4097, 2)])
+def test_workspace_forms_are_bit_identical(dev, tokens, heads):
+    """h3_attention_i4qk_ws, h3_attention_i4qks_ws and h3_attention_i8qk_ws read the key scales
+    from a head-major copy in a lent (NaN-filled) workspace: the outputs equal those of the forms
+    without _ws bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(tokens * 7 + heads)
+    stride = heads * 128
+    cap = H.capacity(tokens)
+    q = rng.integers(-7, 8, (cap, stride)).astype(np.int8)
+    k = rng.integers(-7, 8, (cap, stride)).astype(np.int8)
+    q[tokens:] = 0
+    k[tokens:] = 0
+    qs = rng.uniform(0.005, 0.05, (cap, heads)).astype(np.float32)
+    ks = rng.uniform(0.005, 0.05, (cap, heads)).astype(np.float32)
+    v = O.f16_bits(rng.standard_normal((tokens, stride)).astype(np.float32)).reshape(tokens, stride)
+    vt = O.transpose(v, O.F16, tokens, stride, 0, stride, cap, cap)
+    cfg = H.AttentionCfg(stride, stride, stride, tokens, cap, 1.0)
+    scfg = H.AttentionSkipCfg(stride, stride, stride, tokens, cap, 1.0, 1.5)
+    nbytes = H.scales_workspace_bytes(cfg)
+    assert nbytes == heads * tokens * 4 and H.scales_workspace_bytes(scfg) == nbytes
+    ops = [(pack_i4(q), pack_i4(k), H.attention_i4qk, H.attention_i4qk_ws, cfg),
+           (pack_i4(q), pack_i4(k), H.attention_i4qks, H.attention_i4qks_ws, scfg),
+           (q.view(np.int32), k.view(np.int32), H.attention_i8qk, H.attention_i8qk_ws, cfg)]
+    for qq, kk, plain, lent, c in ops:
+        print(f"ws form {plain.__name__} tokens={tokens} heads={heads}", flush=True)
+        args = (c, tokens, heads, to_dev(qq, dev), to_dev(qs, dev), to_dev(kk, dev),
+                to_dev(ks, dev), to_dev(vt, dev))
+        a = torch.zeros((tokens, stride), dtype=torch.float16, device=dev)
+        b = torch.zeros_like(a)
+        plain(*args, a)
+        ws = torch.full((nbytes // 2,), 0x7E00, dtype=torch.int16, device=dev)
+        lent(*args, b, ws)
+        torch.cuda.synchronize()
+        assert np.isfinite(from_dev(b).view(np.float16)).all()
+        assert np.array_equal(from_dev(a), from_dev(b)), plain.__name__

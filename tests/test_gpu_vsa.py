@@ -216,7 +216,7 @@ def run_vsa_attention(dev, qc, qs, kc, ks, vt, routes, lengths, heads, token_cou
             to_dev(pack_codes(kc), dev), to_dev(ks, dev), to_dev(vt, dev), out,
             to_dev(routes, dev), to_dev(lengths, dev))
     if lent:
-        nbytes = H.vsa_attention_workspace_bytes(cfg)
+        nbytes = H.scales_workspace_bytes(cfg)
         assert nbytes == heads * n * 4
         ws = torch.full((nbytes // 2,), 0x7E00, dtype=torch.int16, device=dev)
         H.vsa_attention_i8_ws(*args, ws)

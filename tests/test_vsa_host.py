@@ -122,6 +122,28 @@ def test_vsa_attention_checks_routes_and_lengths():
     assert st == H.H3_ERR_CONFIG, H.last_error()
 
 
+def test_workspace_forms_check_their_workspace():
+    """The dense _ws forms: a head-major scale copy of (kv_stride/128) x tokens f32."""
+    heads, tokens = 3, 500
+    cap = H.capacity(tokens)
+    w = heads * 128
+    a = H.AttentionCfg(w, w, w, tokens, cap, 1.0)
+    s = H.AttentionSkipCfg(w, w, w, tokens, cap, 1.0, 1.0)
+    big = fake(1 << 28)
+    need = heads * tokens * 4
+    assert H.scales_workspace_bytes(a) == need
+    L = H.lib()
+    for fn, c, stage in [(L.h3_attention_i8qk_ws, a, "attention_i8qk"),
+                         (L.h3_attention_i4qk_ws, a, "attention_i4qk"),
+                         (L.h3_attention_i4qks_ws, s, "attention_i4qks")]:
+        st = fn(ctypes.byref(c), tokens, heads, big, big, big, big, big, big, fake(need - 4), None)
+        assert st == H.H3_ERR_BINDING
+        assert H.last_error() == f"{stage}: workspace is {need - 4} bytes, the kernel addresses {need}"
+        st = fn(ctypes.byref(c), tokens, heads, big, big, big, big, big, big, H.raw_view(0, need),
+                None)
+        assert st == H.H3_ERR_ARGUMENT and "null workspace" in H.last_error()
+
+
 def test_vsa_attention_workspace_is_checked():
     """h3_vsa_attention_i8_ws: a head-major copy of the key scales, (kv_stride/128) x tokens
     f32; a short or null workspace refused."""
@@ -131,7 +153,7 @@ def test_vsa_attention_workspace_is_checked():
     big = fake(1 << 28)
     L = H.lib()
     need = (w // 128) * n * 4
-    assert H.vsa_attention_workspace_bytes(a) == need
+    assert H.scales_workspace_bytes(a) == need
     st = L.h3_vsa_attention_i8_ws(ctypes.byref(a), n, heads, big, big, big, big, big, big, big,
                                   big, fake(need - 1), None)
     assert st == H.H3_ERR_BINDING
