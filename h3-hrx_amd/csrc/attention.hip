@@ -690,7 +690,7 @@ void k_attention(Args a) {
 // so a 32-key tile would pull 4 KB of lines for 128 bytes of scales (kHmScales: the launcher
 // first transposes them into the workspace).
 //
-// Per run of the key loop the workgroup scans its route row over the segment into an LDS list
+// Per run of the key loop the workgroup scans its route row into an LDS list
 // of the live half-cubes it keeps (ascending keys, up to kVsaListMax per run; more runs continue
 // the same online softmax). Keys past a cube's live length are masked through their staged scale
 // pair (ks, -inf), so the loop has no masked variant. The per-tile work is that of k_attention on
