@@ -153,7 +153,10 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 __device__ __forceinline__ bool key_is_nan(uint32_t k) { return k < 0x007fffffu || k > 0xff800000u; }
 
 // h3_vsa_route: one workgroup per (q, head) row. Four 8-bit radix passes find the topk-th
-// largest candidate key (candidates: j >= prefix, not NaN); the row is then written.
+// largest candidate key (candidates: j >= prefix, not NaN); the row is then written. kPer > 0:
+// each thread keeps the keys of its candidates j = prefix + tid + kThreads*i (i < kPer) in
+// registers, so the row is read from memory once instead of once per pass.
+template <int kPer>
 __global__ __launch_bounds__(kThreads) void k_vsa_route(const float* __restrict__ scores,
                                                         int32_t* __restrict__ routes,
                                                         uint32_t blocks, uint32_t prefix,
@@ -166,13 +169,29 @@ __global__ __launch_bounds__(kThreads) void k_vsa_route(const float* __restrict_
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const bool select = topk > 0 && q >= prefix;  // a prefix row keeps everything
   uint32_t want = topk, bits = 0, mask = 0, candidates = 0;
+  uint32_t cache[kPer > 0 ? kPer : 1];  // order keys of this thread's candidates (0: a NaN key)
+  if constexpr (kPer > 0) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t j = prefix + tid + kThreads * i;
+      cache[i] = j < blocks ? order_key(row[j]) : 0u;
+    }
+  }
   for (int pass = 0; pass < 4 && select; ++pass) {
     const int shift = 24 - 8 * pass;
     hist[tid] = 0;
     __syncthreads();
-    for (uint32_t j = prefix + tid; j < blocks; j += kThreads) {
-      const uint32_t k = order_key(row[j]);
-      if (!key_is_nan(k) && (k & mask) == bits) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    if constexpr (kPer > 0) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const uint32_t k = cache[i];
+        if (!key_is_nan(k) && (k & mask) == bits) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+      }
+    } else {
+      for (uint32_t j = prefix + tid; j < blocks; j += kThreads) {
+        const uint32_t k = order_key(row[j]);
+        if (!key_is_nan(k) && (k & mask) == bits) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+      }
     }
     __syncthreads();
     if (tid < 64) {  // lane l scans bins 255-4l, 254-4l, 253-4l, 252-4l (descending)
@@ -216,18 +235,22 @@ __global__ __launch_bounds__(kThreads) void k_vsa_route(const float* __restrict_
     __syncthreads();
   }
   const bool all = select && candidates < topk;
-  for (uint32_t j = tid; j < blocks; j += kThreads) {
-    const bool forced = q < prefix || j < prefix || (j <= q + 1 && q <= j + 1);
-    int32_t keep = 1;
-    if (!forced) {
-      if (topk == 0) {
-        keep = 0;
-      } else if (!all) {
-        const uint32_t k = order_key(row[j]);
-        keep = key_is_nan(k) || k >= bits;
-      }
+  // routes[q][j]: 1 when forced (a prefix row or column, |q - j| <= 1); else 0 without a budget,
+  // 1 when there are fewer candidates than the budget, else NaN or at least the threshold key.
+  auto keep_of = [&](uint32_t j, uint32_t k) -> int32_t {
+    if (q < prefix || j < prefix || (j <= q + 1 && q <= j + 1)) return 1;
+    if (topk == 0) return 0;
+    return all || key_is_nan(k) || k >= bits ? 1 : 0;
+  };
+  if constexpr (kPer > 0) {
+    for (uint32_t j = tid; j < prefix && j < blocks; j += kThreads) out[j] = 1;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t j = prefix + tid + kThreads * i;
+      if (j < blocks) out[j] = keep_of(j, cache[i]);
     }
-    out[j] = keep;
+  } else {
+    for (uint32_t j = tid; j < blocks; j += kThreads) out[j] = keep_of(j, order_key(row[j]));
   }
 }
 
@@ -372,8 +395,13 @@ hipError_t launch_vsa_scores(uint32_t blocks, uint32_t heads, const float* qm, c
 
 hipError_t launch_vsa_route(uint32_t blocks, uint32_t heads, uint32_t prefix, uint32_t topk,
                             const float* scores, int32_t* routes, hipStream_t stream) {
-  hipLaunchKernelGGL(k_vsa_route, dim3(blocks, heads), dim3(kThreads), 0, stream, scores, routes,
-                     blocks, prefix, topk);
+  constexpr int kPer = 16;  // rows of up to 4,096 candidates stay in registers
+  if (blocks <= prefix + (uint32_t)kPer * kThreads)
+    hipLaunchKernelGGL(k_vsa_route<kPer>, dim3(blocks, heads), dim3(kThreads), 0, stream, scores,
+                       routes, blocks, prefix, topk);
+  else
+    hipLaunchKernelGGL(k_vsa_route<0>, dim3(blocks, heads), dim3(kThreads), 0, stream, scores,
+                       routes, blocks, prefix, topk);
   return hipGetLastError();
 }
 

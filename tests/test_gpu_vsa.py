@@ -31,7 +31,7 @@ import h3attn as H
 import oracle as O
 from helpers import from_dev, north_star_ok, pack_codes, to_dev
 from test_oracle_vsa import (EXTRA_Q, independent_expected, nrmse, oracle_pipeline,
-                             reference_device_inputs)
+                             reference_device_inputs, route_rows_by_rank)
 
 pytestmark = pytest.mark.gpu
 
@@ -105,6 +105,24 @@ def test_scores_and_routes_are_exact(dev, blocks, prefix):
                         max(nonprefix - 1, 0), nonprefix + 3}):
         _, routes = gpu_scores_routes(dev, qm, km, heads, prefix, topk, blocks)
         assert np.array_equal(routes, O.vsa_route(want, prefix, topk)), f"topk={topk}"
+
+
+@pytest.mark.parametrize("blocks,prefix", [(4098, 2), (4099, 2), (5003, 5)])
+def test_routes_of_long_rows_are_exact(dev, blocks, prefix):
+    """Rows of up to 4,096 candidates are kept in registers by the route kernel, longer ones are
+    re-read per radix pass: both sides of that boundary, on sampled rows with ties."""
+    rng = np.random.default_rng(blocks)
+    heads = 1
+    qm = rng.standard_normal((blocks, 128)).astype(np.float32)
+    km = rng.standard_normal((blocks, 128)).astype(np.float32)
+    km[blocks // 3] = km[7]  # exact ties
+    nonprefix = blocks - prefix
+    print(f"vsa long-row routes blocks={blocks}", flush=True)
+    for topk in (1, O.vsa_topk(10.0, nonprefix), nonprefix - 1):
+        scores, routes = gpu_scores_routes(dev, qm, km, heads, prefix, topk, blocks)
+        for q in (0, 1, prefix, 7, blocks // 3, blocks // 2, blocks - 1):
+            want = route_rows_by_rank(scores[0, q], q, prefix, topk)
+            assert np.array_equal(routes[0, q], want), (topk, q)
 
 
 def test_route_on_special_scores_is_exact(dev):

@@ -397,3 +397,30 @@ def test_pipeline_planted_route_mistake_is_caught():
     topk = O.vsa_topk(keep, len(lengths) - prefix)
     off = O.vsa_route(O.vsa_scores(qm, km, heads), prefix, topk + 1)
     assert not np.array_equal(off, want_routes)
+
+
+def route_rows_by_rank(scores_row, q, prefix, topk):
+    """routes[q][j] of one row by the reference's rank rule (vsa_ops.loom h3_vsa_route), with
+    the ranks from a sort: rank(j) = #{k >= prefix, not NaN : score_k > score_j}, NaN ranks 0."""
+    blocks = scores_row.shape[0]
+    cand = scores_row[prefix:]
+    valid = np.sort(cand[~np.isnan(cand)])
+    own = scores_row
+    rank = np.where(np.isnan(own), 0, len(valid) - np.searchsorted(valid, own, side="right"))
+    j = np.arange(blocks)
+    forced = (np.abs(j - q) <= 1) | (q < prefix) | (j < prefix)
+    return np.where(forced, 1, (rank < topk).astype(np.int32)).astype(np.int32)
+
+
+def test_sorted_rank_route_equals_the_oracle():
+    """The sort-based route rule the long-row GPU test checks with equals the oracle's rank
+    count row by row, with ties, NaN scores, prefixes and every budget."""
+    rng = np.random.default_rng(0)
+    for blocks, prefix in [(9, 0), (23, 2), (40, 5)]:
+        s = rng.integers(-3, 4, (1, blocks, blocks)).astype(np.float32)
+        s[0, 3, 5] = np.nan
+        s[0, 4, 1] = np.nan
+        for topk in range(0, blocks - prefix + 2):
+            want = O.vsa_route(s, prefix, topk)
+            for q in range(blocks):
+                assert np.array_equal(route_rows_by_rank(s[0, q], q, prefix, topk), want[0, q])
