@@ -340,12 +340,27 @@ __device__ __forceinline__ void raise_max(float tmax, float qsl, State& st) {
   st.m = m_new;
 }
 
+// max(v, v of the lane the DPP control selects): quad_perm [1,0,3,2] (0xB1) and [2,3,0,1]
+// (0x4E), row_half_mirror (0x141, lane i <-> 7-i of each 8) and row_mirror (0x140, i <-> 15-i of
+// each 16) reduce over 16 lanes on the vector pipe, with no LDS round trip.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), kCtrl, 0xF, 0xF,
+                                            false);
+  return fmaxf(v, __int_as_float(o));
+}
+
 // Tile skip decision (kernels/attention_i4qks_family.loom:318-324): the largest gap between a
-// tile's max and the running max before it over the wave's 32 queries, wave-uniform.
+// tile's max and the running max before it over the wave's 32 queries (lanes 0-31; lanes 32-63
+// hold the same queries), wave-uniform.
 __device__ __forceinline__ float wave_gap(float gap) {
-#pragma unroll
-  for (int k = 1; k < 32; k <<= 1) gap = fmaxf(gap, __shfl_xor(gap, k));
-  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gap)));
+  gap = dpp_max<0xB1>(gap);
+  gap = dpp_max<0x4E>(gap);
+  gap = dpp_max<0x141>(gap);
+  gap = dpp_max<0x140>(gap);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gap), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gap), 16));
+  return fmaxf(a, b);
 }
 
 // LDS byte offset, inside a row, of logical 16-byte chunk 2x + half for rows with (row/2)%8 = sw.
