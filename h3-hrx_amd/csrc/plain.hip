@@ -96,27 +96,14 @@ __device__ __forceinline__ uint32_t code(float y, float inv_s) {
   return (uint32_t)(int)q & 0xffu;
 }
 
-// One token row per wave (kWide == false, width <= 4096: lanes >= width/64 idle) or per
-// workgroup of width/64 lanes (kWide).
+// Transform of the lane's 64 channels (the four radix-4 stages), the row's absmax (over the wave,
+// and through `wave_amax` over the workgroup when kWide), and the codes and scale of the row.
 template <bool kWide>
-__global__ __launch_bounds__(kWide ? 512 : 256) void k_prepare_plain(
-    const void* __restrict__ x, uint32_t tokens, uint32_t width, uint32_t out_stride, int elem,
-    uint8_t* __restrict__ codes, float* __restrict__ scales) {
-  __shared__ float wave_amax[8];
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t row = kWide ? blockIdx.x : blockIdx.x * 4 + wave;
-  const uint32_t g = kWide ? threadIdx.x : lane;  // channel group of this lane
-  const uint32_t groups = width / kGroup;
-  const bool active = row < tokens && g < groups;
-  if (!kWide && row >= tokens) return;  // whole wave past the rows
-
-  float v[kGroup];
-  if (active) {
-    load_group(x, (size_t)row * width + (size_t)g * kGroup, elem, v);
-  } else {
-#pragma unroll
-    for (int i = 0; i < kGroup; ++i) v[i] = 0.0f;
-  }
+__device__ __forceinline__ void transform_store(float (&v)[kGroup], float* wave_amax,
+                                                uint32_t wave, uint32_t lane, uint32_t row,
+                                                uint32_t g, bool active, uint32_t out_stride,
+                                                uint8_t* __restrict__ codes,
+                                                float* __restrict__ scales) {
   radix4_in_lane<1>(v);
   radix4_in_lane<4>(v);
   radix4_in_lane<16>(v);
@@ -158,13 +145,91 @@ __global__ __launch_bounds__(kWide ? 512 : 256) void k_prepare_plain(
   if (g == 0) scales[row] = s;
 }
 
+// One token row per wave (kWide == false, width <= 4096: lanes >= width/64 idle) or per
+// workgroup of width/64 lanes (kWide).
+template <bool kWide>
+__global__ __launch_bounds__(kWide ? 512 : 256) void k_prepare_plain(
+    const void* __restrict__ x, uint32_t tokens, uint32_t width, uint32_t out_stride, int elem,
+    uint8_t* __restrict__ codes, float* __restrict__ scales) {
+  __shared__ float wave_amax[8];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t row = kWide ? blockIdx.x : blockIdx.x * 4 + wave;
+  const uint32_t g = kWide ? threadIdx.x : lane;  // channel group of this lane
+  const uint32_t groups = width / kGroup;
+  const bool active = row < tokens && g < groups;
+  if (!kWide && row >= tokens) return;  // whole wave past the rows
+
+  float v[kGroup];
+  if (active) {
+    load_group(x, (size_t)row * width + (size_t)g * kGroup, elem, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) v[i] = 0.0f;
+  }
+  transform_store<kWide>(v, wave_amax, wave, lane, row, g, active, out_stride, codes, scales);
+}
+
+// 16-bit rows of up to 4,096 channels: one wave per row as k_prepare_plain<false>, but each wave
+// walks kRowsPerWave rows (row0, row0 + stride, ...) and loads the next row's inputs (8 x 16
+// bytes per lane) while it transforms the current one, so a row's loads are in flight under the
+// arithmetic of the previous row.
+#ifndef H3_PLAIN_ROWS_PER_WAVE
+#define H3_PLAIN_ROWS_PER_WAVE 8
+#endif
+constexpr uint32_t kRowsPerWave = H3_PLAIN_ROWS_PER_WAVE;
+
+__global__ __launch_bounds__(256) void k_prepare_plain_rows(const uint16_t* __restrict__ x,
+                                                            uint32_t tokens, uint32_t width,
+                                                            uint32_t out_stride, int elem,
+                                                            uint8_t* __restrict__ codes,
+                                                            float* __restrict__ scales) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t g = lane;
+  const bool active = g < width / kGroup;
+  const uint32_t stride = gridDim.x * 4;
+  uint32_t row = blockIdx.x * 4 + wave;
+  if (row >= tokens) return;  // whole wave
+  uint4 cur[kGroup / 8], nxt[kGroup / 8];
+  auto load = [&](uint32_t r, uint4 (&dst)[kGroup / 8]) {
+    const uint4* p = reinterpret_cast<const uint4*>(x + (size_t)r * width + (size_t)g * kGroup);
+#pragma unroll
+    for (int i = 0; i < kGroup / 8; ++i) dst[i] = active ? p[i] : make_uint4(0, 0, 0, 0);
+  };
+  load(row, cur);
+  for (; row < tokens; row += stride) {
+    const bool more = row + stride < tokens;  // wave-uniform
+    if (more) load(row + stride, nxt);
+    float v[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup / 8; ++i) {
+      const v4f lo = widen4(make_uint2(cur[i].x, cur[i].y), elem);
+      const v4f hi = widen4(make_uint2(cur[i].z, cur[i].w), elem);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * i + j] = lo[j];
+        v[8 * i + 4 + j] = hi[j];
+      }
+    }
+    transform_store<false>(v, nullptr, wave, lane, row, g, active, out_stride, codes, scales);
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < kGroup / 8; ++i) cur[i] = nxt[i];
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_prepare_plain(uint32_t width, uint32_t out_stride, uint32_t elem,
                                 uint32_t tokens, const void* x, uint8_t* codes, float* scales,
                                 hipStream_t stream) {
   const uint32_t groups = width / kGroup;
-  if (groups <= 64) {
+  if (groups <= 64 && elem != H3_ELEM_F32) {
+    const uint32_t waves = (tokens + kRowsPerWave - 1) / kRowsPerWave;
+    hipLaunchKernelGGL(k_prepare_plain_rows, dim3((waves + 3) / 4), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), tokens, width, out_stride, (int)elem,
+                       codes, scales);
+  } else if (groups <= 64) {
     hipLaunchKernelGGL(k_prepare_plain<false>, dim3((tokens + 3) / 4), dim3(256), 0, stream, x,
                        tokens, width, out_stride, (int)elem, codes, scales);
   } else {
