@@ -724,6 +724,7 @@ constexpr int kVsaVLoads = kVsaVStage / 1024 / kVsaWaves; // 4
 constexpr int kVsaSRows = kVsaKeys / kVsaWaves;           // scale rows stored per wave: 16
 constexpr int kVsaWaitPrevStep = (kVsaKLoads + kVsaVLoads + 1) | (7 << 4) | (0 << 8);
 constexpr int kVsaListMax = 512;                          // list entries per run of the key loop
+constexpr int kVsaPf = 1;  // MFMA operands and key scales read from LDS one chunk ahead (2: +1 %)
 // entry: cube (14 bits) | half << 14 | live keys of the half (1..32) << 16
 constexpr uint32_t kEntryCube = 0x3fffu;
 static_assert(kVsaSRows <= 64 && (kVsaSRows & (kVsaSRows - 1)) == 0, "scale rows per wave");
@@ -889,12 +890,12 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
   // ---- phase A: QK(j+1) || probabilities of slots 0..7
   if (kNext) {
 #pragma unroll
-    for (int w = 0; w < kPf; ++w) kop[w] = k_op_vsa(kst, n, half, w);
+    for (int w = 0; w < kVsaPf; ++w) kop[w] = k_op_vsa(kst, n, half, w);
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    if (kNext && c + kPf < 4) kop[c + kPf] = k_op_vsa(kst, n, half, c + kPf);
-    if (c >= 4 - kPf) vop[c - (4 - kPf)] = v_op_vsa(vst, n, half, c - (4 - kPf));
+    if (kNext && c + kVsaPf < 4) kop[c + kVsaPf] = k_op_vsa(kst, n, half, c + kVsaPf);
+    if (c >= 4 - kVsaPf) vop[c - (4 - kVsaPf)] = v_op_vsa(vst, n, half, c - (4 - kVsaPf));
     if (kNext) s = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[c], s, 0, 0, 0);
     exp_pair_vsa(u, 2 * c, qsl, negm, pb);
     H3_CHUNK_END();
@@ -904,9 +905,9 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
   float tmax = -INFINITY;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    if (c + kPf < 8) vop[c + kPf] = v_op_vsa(vst, n, half, c + kPf);
-    if (kNext && c >= 3 - kSPf && c < 7 - kSPf) {  // scales of dequant quarter q, kSPf ahead
-      const int q = c - (3 - kSPf), kb = 8 * q + 4 * half;
+    if (c + kVsaPf < 8) vop[c + kVsaPf] = v_op_vsa(vst, n, half, c + kVsaPf);
+    if (kNext && c >= 3 - kVsaPf && c < 7 - kVsaPf) {  // scales of dequant quarter q, kVsaPf ahead
+      const int q = c - (3 - kVsaPf), kb = 8 * q + 4 * half;
       k4[q] = *reinterpret_cast<const float4*>(kss + kb);
       c4[q] = *reinterpret_cast<const float4*>(kss + kVsaKeys + kb);
     }
