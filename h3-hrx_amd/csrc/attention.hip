@@ -547,10 +547,12 @@ void k_attention(Args a) {
   __shared__ __attribute__((aligned(16))) char v2s[kVStage];
 
   // XCD-aware remap: hardware hands block b to XCD b % 8; give each XCD a contiguous range of
-  // (head, query block) work so its resident blocks share one head's K/V stream in L2.
+  // the launch's (head, query block) work [base, base + total) so its resident blocks share one
+  // head's K/V stream in L2.
   const uint32_t b = blockIdx.x;
-  const uint32_t logical = (b & 7u) * a.per_xcd + (b >> 3);
-  if (logical >= a.total) return;
+  const uint32_t local = (b & 7u) * a.per_xcd + (b >> 3);
+  if (local >= a.total) return;
+  const uint32_t logical = a.base + local;
   const uint32_t head_y = logical / a.q_blocks;
   const uint32_t qb = logical % a.q_blocks;
   const uint32_t kv_head = head_y % a.kv_head_limit;
@@ -1251,6 +1253,20 @@ void k_attention_cross(Args a) {
 
 }  // namespace
 
+// CUs of the current device (cached per device).
+static uint32_t device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    cus[dev] = n;
+  }
+  return (uint32_t)cus[dev];
+}
+
 hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,
                             uint32_t token_count,
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
@@ -1274,30 +1290,44 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
   a.heads = heads;
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
-  a.total = a.q_blocks * heads;
-  a.per_xcd = (a.total + 7) / 8;
-  dim3 grid(a.per_xcd * 8);
-  if (workspace && mode != kHeadI8) {  // token-major codes, head-major copy of the key scales
+  const bool hm_scales = workspace && mode != kHeadI8;
+  if (hm_scales) {  // token-major codes, head-major copy of the key scales
     float* ks_hm = static_cast<float*>(workspace);
     hipLaunchKernelGGL(k_scales_head_major, dim3((a.tokens + 63) / 64, (a.kv_head_limit + 63) / 64),
                        dim3(256), 0, stream, ks, ks_hm, a.tokens, a.kv_head_limit);
     a.ks = ks_hm;
-    if (mode == kTokenI4)
-      hipLaunchKernelGGL((k_attention<kTokenI4, true>), grid, dim3(kThreads), 0, stream, a);
-    else if (mode == kTokenI4Skip)
-      hipLaunchKernelGGL((k_attention<kTokenI4Skip, true>), grid, dim3(kThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((k_attention<kTokenI8, true>), grid, dim3(kThreads), 0, stream, a);
-    return hipGetLastError();
   }
-  if (mode == kHeadI8)
-    hipLaunchKernelGGL(k_attention<kHeadI8>, grid, dim3(kThreads), 0, stream, a);
-  else if (mode == kTokenI4)
-    hipLaunchKernelGGL(k_attention<kTokenI4>, grid, dim3(kThreads), 0, stream, a);
-  else if (mode == kTokenI4Skip)
-    hipLaunchKernelGGL(k_attention<kTokenI4Skip>, grid, dim3(kThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
+  // Head-major: one launch. Token-major: one launch per eight generations of resident
+  // workgroups (two per CU), so the workgroups of a launch start together and stay closer in
+  // the key stream, whose K rows and scales they share in L2 with fewer heads' neighbours
+  // (measured at C3: -5.5 % int4, -6.8 % int8 token-major, -2.7 % int4 with head-major scales;
+  // +0.4-1.5 % for head-major, which stays one launch).
+  const uint32_t items = a.q_blocks * heads;
+  const uint32_t gen = mode == kHeadI8 ? items : std::max(1u, 16u * device_cus());
+  for (uint32_t base = 0; base < items; base += gen) {
+    a.base = base;
+    a.total = std::min(gen, items - base);
+    a.per_xcd = (a.total + 7) / 8;
+    const dim3 grid(a.per_xcd * 8);
+    if (mode == kHeadI8) {
+      hipLaunchKernelGGL(k_attention<kHeadI8>, grid, dim3(kThreads), 0, stream, a);
+    } else if (mode == kTokenI4) {
+      if (hm_scales)
+        hipLaunchKernelGGL((k_attention<kTokenI4, true>), grid, dim3(kThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL(k_attention<kTokenI4>, grid, dim3(kThreads), 0, stream, a);
+    } else if (mode == kTokenI4Skip) {
+      if (hm_scales)
+        hipLaunchKernelGGL((k_attention<kTokenI4Skip, true>), grid, dim3(kThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL(k_attention<kTokenI4Skip>, grid, dim3(kThreads), 0, stream, a);
+    } else {
+      if (hm_scales)
+        hipLaunchKernelGGL((k_attention<kTokenI8, true>), grid, dim3(kThreads), 0, stream, a);
+      else
+        hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
+    }
+  }
   return hipGetLastError();
 }
 
@@ -1327,20 +1357,6 @@ hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, co
   a.per_xcd = (a.total + 7) / 8;
   hipLaunchKernelGGL(k_attention_cross, dim3(a.per_xcd * 8), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
-}
-
-// CUs of the current device (cached per device).
-static uint32_t device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return 256;
-    cus[dev] = n;
-  }
-  return (uint32_t)cus[dev];
 }
 
 size_t scales_workspace_bytes(const h3_attention_cfg& cfg) {
