@@ -21,7 +21,7 @@ CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 OUT = HERE / "libh3attn.so"
 OBJ = HERE / "_build"
-SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "gemm.hip", "abi.cpp", "stack.cpp",
+SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "attention_hm.hip", "gemm.hip", "abi.cpp", "stack.cpp",
            "tables.cpp", "vsa.hip", "vsa_host.cpp"]
 ARCH = "gfx950"
 
@@ -49,7 +49,7 @@ FLAGS = [
 # sees NaN operands, so it may drop the NaN-quieting canonicalisations IEEE mode otherwise adds
 # to every max; infinities stay honoured (masked keys are -inf). The quantizer files keep full
 # IEEE semantics.
-EXTRA = {"attention.hip": ["-fno-honor-nans"]}
+EXTRA = {"attention.hip": ["-fno-honor-nans"], "attention_hm.hip": ["-fno-honor-nans"]}
 
 
 def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:

@@ -1272,7 +1272,9 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream) {
-  Args a;
+  if (mode == kHeadI8)
+    return launch_attention_hm(cfg, token_count, heads, qi, qs, ki, ks, vt, out, stream);
+  Args a{};
   a.qi = qi;
   a.qs = qs;
   a.ki = ki;

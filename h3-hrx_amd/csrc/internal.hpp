@@ -78,6 +78,12 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream);
+// attention_i8qkhm: the head-major INT8 kernel of attention_hm.hip (one wave per SIMD, two query
+// tiles per wave). Shapes are validated by the caller.
+hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count, uint32_t heads,
+                               const int32_t* qi, const float* qs, const int32_t* ki,
+                               const float* ks, const uint16_t* vt, uint16_t* out,
+                               hipStream_t stream);
 // Bytes of the head-major key-scale copy the token-major attention kernels read when a caller
 // lends a workspace: (kv_stride / 128) * tokens f32.
 size_t scales_workspace_bytes(const h3_attention_cfg& cfg);
