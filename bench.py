@@ -26,7 +26,8 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "h3-hrx_amd"))
 
 METRIC = "INT8 attn TOPS + ms/call at S=129k,H=32,D=128; % of gfx950 int8 MFMA peak"
-PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s (at the 2.4 GHz spec clock)
+BOX_CPU_SHARE = 16       # host threads a one-GPU box grants a job
 WORKLOADS = {
     # name: (tokens, heads, rope grid (t, h, w))
     "c3": (129024, 32, (32, 42, 96)),
@@ -269,6 +270,69 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
     return res
 
 
+class ClockSampler:
+    """The GFX engine clock, sampled with ROCm's SMI library (amdsmi) on a background thread
+    every `period` seconds while the timed steps run. MFMA peaks scale with this clock: the spec
+    figures assume 2.4 GHz, and under sustained matrix load the part runs well below it."""
+
+    SPEC_MHZ = 2400.0
+
+    def __init__(self, period: float = 0.02):
+        import threading
+        self.period = period
+        self.samples: list = []
+        self.error = None
+        self._stop = threading.Event()
+        self._thread = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self._smi = amdsmi
+            self._handle = amdsmi.amdsmi_get_processor_handles()[0]
+            self._read()
+            self.samples.clear()
+        except Exception as exc:  # no SMI on this host: the figure is reported as missing
+            self.error = f"{type(exc).__name__}: {exc}"
+        if self.error is None:
+            self._thread = threading.Thread(target=self._run, daemon=True)
+
+    def _read(self) -> float:
+        info = self._smi.amdsmi_get_clock_info(self._handle, self._smi.AmdSmiClkType.GFX)
+        return float(info["clk"])
+
+    def _run(self) -> None:
+        while not self._stop.is_set():
+            try:
+                self.samples.append(self._read())
+            except Exception as exc:
+                self.error = f"{type(exc).__name__}: {exc}"
+                return
+            self._stop.wait(self.period)
+
+    def __enter__(self):
+        if self._thread is not None:
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join()
+        return False
+
+    def summary(self) -> dict:
+        if not self.samples:
+            return {"mhz_mean": None, "samples": 0, "error": self.error or "no samples"}
+        xs = sorted(self.samples)
+        # samples taken while the GPU idled between launches (deep-sleep clocks) are left out
+        busy = [x for x in xs if x >= 0.5 * xs[-1]]
+        return {"mhz_mean": round(sum(busy) / len(busy), 1), "mhz_min": busy[0],
+                "mhz_max": busy[-1], "mhz_median": busy[len(busy) // 2], "samples": len(busy),
+                "idle_samples_dropped": len(xs) - len(busy),
+                "source": "amdsmi_get_clock_info(GFX) every %.0f ms during the timed steps"
+                          % (self.period * 1e3)}
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per attention launch from the committed rocprofv3 PMC summary, if present."""
     p = ROOT / "profiles" / f"attention_i8qkhm_{workload}_pmc.md"
@@ -287,8 +351,9 @@ def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    threads = min(threads, 16)
+    # every host thread the GPU box grants one GPU (its CPU share is 16, whatever nproc says)
+    nproc = os.cpu_count()
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", "0")) or nproc, BOX_CPU_SHARE)
     rng = np.random.default_rng(1)
     rows = np.sort(rng.choice(tokens, size=rows_per_head, replace=False)).astype(np.int32)
     sample_s, fixed_s, _ = O.cpu_baseline(q16, k16, v16, tokens, heads, rows, threads)
@@ -307,6 +372,9 @@ def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
         "unit": "TOPS",
         "ms_per_call": call_s * 1e3,
         "cores": threads,
+        "nproc": nproc,
+        "cores_note": (f"{threads} threads: all of the host threads a one-GPU box grants "
+                       f"(its CPU share is {BOX_CPU_SHARE}; nproc reports {nproc})"),
         "kind": "port",
         "sample": (f"{rows_per_head} query rows x {heads} heads of S={tokens} (f64 attention, "
                    f"{sample_s:.2f} s) plus the per-call K operand/mean/V^T pass "
@@ -417,11 +485,13 @@ def main() -> None:
         step(False)
     torch.cuda.synchronize()
     print(f"# warmup done: {args.workload} S={tokens} H={heads}", file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(True)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    clock = ClockSampler()
+    with clock:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(True)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     att_ms = [a.elapsed_time(b) for a, b in att_events]
     att_avg = sum(att_ms) / len(att_ms)
@@ -431,6 +501,10 @@ def main() -> None:
     value = step_ops / (ms_step * 1e-3) / 1e12
     achieved = ops / (att_avg * 1e-3) / 1e12
     out_ok = bool(torch.isfinite(out).all().item())
+    clk = clock.summary()
+    # the int8 MFMA peak at the engine clock measured during the run (spec: 2.4 GHz)
+    peak_clk = (PEAK_INT8_TOPS * clk["mhz_mean"] / ClockSampler.SPEC_MHZ
+                if clk["mhz_mean"] else None)
 
     line = {
         "metric": METRIC,
@@ -464,13 +538,19 @@ def main() -> None:
         "attention_tops": round(achieved, 3),
         "attention_frac_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
         "output_finite": out_ok,
+        "engine_clock": clk,
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 3),
             "peak": PEAK_INT8_TOPS,
-            "unit": "TFLOP/s",
+            "unit": "TOP/s",
             "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "peak_at_measured_clock": round(peak_clk, 1) if peak_clk else None,
+            "frac_at_measured_clock": round(achieved / peak_clk, 4) if peak_clk else None,
             "traffic": traffic_from_profiles(args.workload),
+            "traffic_source": (f"copied from profiles/attention_i8qkhm_{args.workload}_pmc.md "
+                               "(rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE of this kernel, "
+                               "calibrated on a plain copy); not measured in this run"),
         },
     }
     if not args.no_adjacent:

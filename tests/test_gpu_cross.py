@@ -1,7 +1,9 @@
 """The cross-attention extension on the GPU (h3_attention_i8qkhm_cross): grouped heads and a
 key-padding mask, against the f64 oracle at the north-star tolerance (max-abs 2e-2, mean-abs
-2e-3); bit-identical to attention_i8qkhm when queries and keys are one sequence with whole
-64-key tiles, ungrouped heads and no mask; BASELINE config 4's text shape (130,272 queries,
+2e-3); the same attention as attention_i8qkhm (both at the oracle's tolerance, and within
+2e-3 of each other: the dense head-major kernel rounds its exponent arguments and probabilities
+through f16 on a different schedule, so the two are no longer bit-identical) when queries and
+keys are one sequence with whole 64-key tiles, ungrouped heads and no mask; BASELINE config 4's text shape (130,272 queries,
 32 query heads over 8 key/value heads, 512 text tokens, the last 20 % padding) on sampled rows.
 """
 import numpy as np
@@ -58,7 +60,15 @@ def test_one_sequence_unmasked_is_the_dense_kernel(dev):
     out = torch.zeros((tokens * heads * 128,), dtype=torch.int16, device=dev)
     H.attention_i8qkhm(cfg, tokens, heads, to_dev(pack_codes(qc), dev), to_dev(qs, dev),
                        to_dev(pack_codes(kc), dev), to_dev(ks, dev), to_dev(vt, dev), out)
-    assert np.array_equal(got, from_dev(out).reshape(tokens, -1))
+    dense = from_dev(out).reshape(tokens, -1)
+    rows = np.arange(tokens, dtype=np.int32)
+    want = O.cross_attention_f64(qc, qs, kc, ks, vt, np.ones(tokens, np.uint8), tokens,
+                                 rows).reshape(tokens, -1)
+    for name, o in (("cross", got), ("dense", dense)):
+        mx, mean = north_star_ok(o.view(np.float16).astype(np.float32), want)
+        assert mx < 2e-2 and mean < 2e-3, (name, mx, mean)
+    diff = np.abs(got.view(np.float16).astype(np.float64) - dense.view(np.float16).astype(np.float64))
+    assert diff.max() <= 2e-3, diff.max()
 
 
 def test_config4_text_shape_on_sampled_rows(dev):
