@@ -21,7 +21,8 @@ CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 OUT = HERE / "libh3attn.so"
 OBJ = HERE / "_build"
-SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "attention_hm.hip", "gemm.hip", "abi.cpp", "stack.cpp",
+SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "attention_hm.hip", "noalloc.hip", "gemm.hip",
+           "abi.cpp", "stack.cpp",
            "tables.cpp", "vsa.hip", "vsa_host.cpp"]
 ARCH = "gfx950"
 

@@ -227,6 +227,9 @@ SIGNATURES = {
     "h3_attention_i4qk_ws": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, _S], ctypes.c_int),
+    "h3_attention_i8qk_static": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         _S], ctypes.c_int),
     "h3_attention_i4qks_ws": (
         [_P(AttentionSkipCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View,
          View, View, _S], ctypes.c_int),
@@ -271,6 +274,14 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        # torch ships its own libamdhip64 (same soname, but its libraries ask for the unversioned
+        # file name), so a process that loaded this library first would end up with two HIP
+        # runtimes once torch is imported, and this library's would find no device. Loaded after
+        # torch, the library binds to torch's runtime.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         handle = ctypes.CDLL(str(LIB_PATH))
         for name, (args, res) in SIGNATURES.items():
             fn = getattr(handle, name)
@@ -558,6 +569,14 @@ def attention_i8qk_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, k
     check(lib().h3_attention_i8qk_ws(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
                                      view(ki), view(ks), view(vt), view(out), view(workspace),
                                      stream_ptr(stream)))
+
+
+def attention_i8qk_static(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt,
+                          out, stream=None) -> None:
+    """h3_attention_i8qk_static: the _ws form with the library's static scratch array."""
+    check(lib().h3_attention_i8qk_static(ctypes.byref(cfg), token_count, heads, view(qi),
+                                         view(qs), view(ki), view(ks), view(vt), view(out),
+                                         stream_ptr(stream)))
 
 
 def attention_i4qk_ws(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,

@@ -318,6 +318,20 @@ int h3_attention_i4qks_ws(const h3_attention_skip_cfg *cfg, uint32_t token_count
                           h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                           h3_view out, h3_view workspace, h3_stream stream);
 
+/* h3_attention_i8qk_static has no counterpart in the reference. It is for callers that cannot
+ * allocate device memory and have none to lend (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): h3_attention_i8qk_ws with the workspace in a static
+ * device array of 8 MiB that the library holds on each GPU it runs on until the process ends.
+ * Same arguments as h3_attention_i8qk and results bit-identical to h3_attention_i8qk_ws; it
+ * allocates nothing (the first call on a device looks up that device's array with
+ * hipGetSymbolAddress). Limit: h3_scales_workspace_bytes(cfg) <= 8 MiB, i.e. (kv_stride/128) *
+ * tokens <= 2,097,152 (32 heads up to 65,536 tokens); beyond it the call fails with
+ * H3_ERR_CONFIG and launches nothing. Calls on one device share the array: calls that overlap on
+ * one device (unordered streams) race. */
+int h3_attention_i8qk_static(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                             h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                             h3_view out, h3_stream stream);
+
 /* Cross-attention with grouped heads and a key-padding mask: BASELINE config 4's text
  * cross-attention (32 query heads over 8 key/value heads, 512 text tokens, padded positions
  * masked). An extension: the reference has no such kernel.
