@@ -44,6 +44,32 @@ int check_bindings(const char* stage, const h3_view* views, const size_t* need, 
     if (need[i] > 0 && views[i].ptr == nullptr)
       return set_error(H3_ERR_ARGUMENT, "%s: binding %d is null", stage, i);
   }
+  // With a device present, every binding must be memory the current device can address: a host
+  // pointer or another device's buffer handed to a kernel faults the GPU. The HIP runtime knows
+  // this process's allocations (device, managed and pinned host memory); anything else it
+  // refuses. On a host with no device, device_ready() reports that instead.
+  int devices = 0, current = 0;
+  if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+    (void)hipGetLastError();
+    return H3_OK;
+  }
+  if (hipGetDevice(&current) != hipSuccess) {
+    (void)hipGetLastError();
+    return H3_OK;
+  }
+  for (int i = 0; i < n; ++i) {
+    if (need[i] == 0) continue;
+    hipPointerAttribute_t attr{};
+    const hipError_t e = hipPointerGetAttributes(&attr, views[i].ptr);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(H3_ERR_ARGUMENT, "%s: binding %d is not memory the device can address (%s)",
+                       stage, i, hipGetErrorString(e));
+    }
+    if (attr.type == hipMemoryTypeDevice && attr.device != current)
+      return set_error(H3_ERR_ARGUMENT, "%s: binding %d lives on device %d, the current device is %d",
+                       stage, i, attr.device, current);
+  }
   return H3_OK;
 }
 

@@ -49,6 +49,8 @@
 // masked, rows >= token_count not written, f16 output [token_count][out_stride].
 #include <algorithm>
 
+#include <atomic>
+
 #include "internal.hpp"
 
 namespace h3 {
@@ -1255,16 +1257,16 @@ void k_attention_cross(Args a) {
 
 // CUs of the current device (cached per device).
 static uint32_t device_cus() {
-  static int cus[64] = {};
+  static std::atomic<int> cus[64] = {};  // per device, once known (host threads may race to fill)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       return 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return (uint32_t)cus[dev];
+  return (uint32_t)n;
 }
 
 hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_tau,

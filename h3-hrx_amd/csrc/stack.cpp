@@ -111,13 +111,18 @@ int h3_stack_build(const h3_stack_dims* dims, h3_stack** out) {
                 {&s->ks, cap * heads * 4}, {&s->kmean, inner * 4u}, {&s->zmean, inner * 4u},
                 {&s->vt, (size_t)inner * cap * 2}};
   for (auto& a : allocs) {
-    if (hipMalloc(&a.v->ptr, a.bytes) != hipSuccess || hipMemset(a.v->ptr, 0, a.bytes) != hipSuccess) {
-      a.v->ptr = nullptr;
+    if (hipMalloc(&a.v->ptr, a.bytes) != hipSuccess) {
+      a.v->ptr = nullptr;  // nothing to free for this one; release() frees the others
       release(s);
       delete s;
       return set_error(H3_ERR_NO_DEVICE, "stack: allocating %zu bytes failed", a.bytes);
     }
     a.v->bytes = a.bytes;
+    if (hipMemset(a.v->ptr, 0, a.bytes) != hipSuccess) {  // release() frees it with the others
+      release(s);
+      delete s;
+      return set_error(H3_ERR_NO_DEVICE, "stack: clearing %zu bytes failed", a.bytes);
+    }
   }
   *out = s;
   return H3_OK;

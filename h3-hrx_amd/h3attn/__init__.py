@@ -313,12 +313,20 @@ EXTRA_Q = config_f32(1.0 / math.sqrt(128.0) / 128.0)  # src/stack.rs:622-625
 # ------------------------------------------------------------------------- tensor plumbing
 
 def view(t) -> View:
-    """A binding of a torch tensor (any dtype): device pointer and byte length."""
+    """A binding of a torch tensor (any dtype): device pointer and byte length. The tensor must
+    live on the current GPU: a host or other-device pointer handed to a kernel faults the GPU."""
     if t is None:
         return View(None, 0)
     if hasattr(t, "data_ptr"):
         if not t.is_contiguous():
             raise ValueError("bindings must be contiguous")
+        if not t.is_cuda:
+            raise ValueError(f"bindings must be GPU tensors, got one on {t.device}")
+        import torch
+
+        if t.device.index != torch.cuda.current_device():
+            raise ValueError(f"binding on {t.device}, the current device is "
+                             f"cuda:{torch.cuda.current_device()}")
         return View(t.data_ptr(), t.numel() * t.element_size())
     if isinstance(t, View):
         return t
