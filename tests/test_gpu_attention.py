@@ -160,3 +160,60 @@ def test_baseline_shapes_on_sampled_rows(dev, tokens, heads):
     mx, mean = north_star_ok(got[rows], want)
     assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("head_major", [True, False])
+@pytest.mark.parametrize("flat", ["exact", "near"])
+def test_row_sum_error_is_bounded_on_long_flat_rows_with_large_values(dev, flat, head_major):
+    """The output is O / l with both O (the PV accumulators) and the row sum l built from the
+    same f16-rounded probabilities p~ = p(1 + d), |d| <= 2^-11, summed in f32. It is therefore
+    the exact weighted mean of V under the weights p~ / sum p~, each within a relative
+    2^-10 / (1 - 2^-11) of the exact softmax weight, so |out - exact| <= ~2^-10 max|V| plus f32
+    accumulation and the f16 output rounding. Long rows (BASELINE config 3's 129,024 keys) with
+    |V| up to ~1,500 and either exactly flat scores (every p = 1, out = mean of V) or nearly
+    flat ones (every p a distinct value near 1, each rounded) check that bound at scale.
+    The token-major kernel adds a tile's 16 probabilities per lane in a packed f16 tree before the
+    f32 row sum, which adds at most ~2^-9 relative to l (four levels of f16 additions of values
+    <= 2^12), so its bound is 2^-10 + 2^-9 of max|V|."""
+    import torch
+
+    heads, tokens = 2, 129024
+    cap = O.capacity(tokens)
+    rng = np.random.default_rng(77 if flat == "near" else 78)
+    qc, qs, kc, ks, vt = head_major_operands(rng, heads, tokens, cap, late_match=False)
+    if flat == "exact":
+        qc[:] = 0
+    else:
+        qs[:, :tokens] = np.float32(1.0 / 2048.0)
+    vt = (rng.standard_normal((heads * 128, cap), np.float32) * 300.0).astype(np.float16)
+    vt[:, tokens:] = 0
+    vmax = float(np.abs(vt.astype(np.float64)).max())
+    vt = vt.view(np.uint16)
+    stride = heads * 128
+    cfg = H.AttentionCfg(stride, stride, stride, tokens, cap, 1.0)
+    out = torch.empty((tokens, stride), dtype=torch.float16, device=dev)
+    print(f"row-sum bound, {flat} flat rows, S={tokens} H={heads} head_major={head_major}",
+          flush=True)
+    if head_major:
+        H.attention_i8qkhm(cfg, tokens, heads,
+                           to_dev(pack_codes(qc).reshape(heads * cap, 32), dev), to_dev(qs, dev),
+                           to_dev(pack_codes(kc).reshape(heads * cap, 32), dev), to_dev(ks, dev),
+                           to_dev(vt, dev), out)
+    else:  # the same operands in the token-major layout: [cap][heads] rows of codes and scales
+        tm = lambda c: pack_codes(c.transpose(1, 0, 2)).reshape(cap, heads * 32)
+        H.attention_i8qk(cfg, tokens, heads, to_dev(tm(qc), dev), to_dev(qs.T.copy(), dev),
+                         to_dev(tm(kc), dev), to_dev(ks.T.copy(), dev), to_dev(vt, dev), out)
+    torch.cuda.synchronize()
+    got = from_dev(out).view(np.float16).astype(np.float64).reshape(tokens, heads, 128)
+    rows = np.unique(np.concatenate([[0, 31, 32, 255, 256, tokens - 1],
+                                     rng.integers(0, tokens, 6)])).astype(np.int32)
+    want = O.attention_f64(qc, qs, kc, ks, vt, tokens, cap, heads, rows)
+    if flat == "exact":  # closed form: every key weighs the same
+        mean_v = vt[:, :tokens].view(np.float16).astype(np.float64).mean(1).reshape(heads, 128)
+        assert np.allclose(want, mean_v[None], rtol=0, atol=1e-9 * vmax)
+    err = np.abs(got[rows] - want)
+    rel = 2.0 ** -10 + (2.0 ** -12 if head_major else 2.0 ** -9)
+    bound = rel * vmax + 2.0 ** -11 * np.abs(want)
+    assert np.all(err <= bound), (flat, float(err.max()), vmax)
+    assert float(err.mean()) <= 5e-5 * vmax, (flat, float(err.mean()), vmax)
+    assert np.all(np.isfinite(got))
