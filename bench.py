@@ -142,6 +142,38 @@ def adjacent_kernels(torch, H, dev, tokens, width, out):
     return res
 
 
+# Wall time of one dependent fp32 add in a single wave's chain on MI355X (measured with a probe
+# kernel of back-to-back dependent v_add_f32, one wave and one wave per CU alike: 3.54 ns).
+CHAIN_NS_PER_ADD = 3.54
+
+
+def smoothed_route(torch, H, dev, tokens, heads, cap, fused, knorm, cos_t, sin_t):
+    """The north star's fused K-mean smoothing (h3_prepare_k_rope_smooth_i8hm: the column mean of
+    RMSNorm+RoPE(K) in sequential fp32 order, then the quantizer on K minus that mean; the
+    reference's smoothed route src/stack.rs:1727-1791) at the step's shape, against the
+    unsmoothed K quantizer it replaces. The column mean is bounded below by its add chain:
+    `tokens` dependent fp32 adds per column, CHAIN_NS_PER_ADD each."""
+    width = heads * 128
+    ki = torch.empty(heads * cap * 32, dtype=torch.int32, device=dev)
+    ks = torch.empty(heads * cap, dtype=torch.float32, device=dev)
+    mean = torch.empty(width, dtype=torch.float32, device=dev)
+    pk = H.PrepareCfg(3 * width, width, heads, 1.0, cap, 1e-5, H.H3_ELEM_BF16)
+    smooth_ms = time_launches(torch, lambda: H.prepare_k_rope_smooth_i8hm(
+        pk, tokens, fused, knorm, cos_t, sin_t, mean, ki, ks), 10)
+    plain_ms = time_launches(torch, lambda: H.prepare_qk_rope_i8hm(
+        pk, tokens, fused, knorm, cos_t, sin_t, ki, ks), 10)
+    floor_ms = tokens * CHAIN_NS_PER_ADD * 1e-6
+    colmean_ms = smooth_ms - plain_ms
+    return {"shape": f"K of tokens={tokens} heads={heads}, bf16 fused QKV rows",
+            "ms": round(smooth_ms, 4), "unsmoothed_k_quantizer_ms": round(plain_ms, 4),
+            "column_mean_passes_ms": round(colmean_ms, 4),
+            "column_chain_floor_ms": round(floor_ms, 4),
+            "column_mean_vs_floor": round(colmean_ms / floor_ms, 2),
+            "note": "column_mean_passes_ms = ms - unsmoothed_k_quantizer_ms: the row-norm pass "
+                    "(k_rope_rms) plus the column chains (k_rope_colmean); the floor is tokens "
+                    f"dependent fp32 adds at {CHAIN_NS_PER_ADD} ns each"}
+
+
 TEXT_TOKENS, TEXT_KV_HEADS, TEXT_PAD = 512, 8, 0.2  # BASELINE config 4's text cross-attention
 
 
@@ -392,6 +424,81 @@ def cpu_baseline(q16, k16, v16, tokens, heads, rows_per_head):
 
 COPY_BYTES = 1 << 30
 
+# The reference's own attention benchmark (benches/kernels.rs:562-656): attention_i8qkhm at the
+# model's 56 heads (INNER 7168) over these token counts, capacity (t + 16).div_ceil(128) * 128.
+SWEEP_HEADS = 56
+SWEEP_TOKENS = (1, 129, 256, 257, 2048, 4095, 4096, 4097, 8192, 8193, 15666, 16384, 16385,
+                32768, 37977)
+
+
+def sweep_case(torch, H, dev, tokens, reps):
+    """One case of the reference's sweep with its synthetic operands: int8 codes
+    ((i*37 + seed) % 15) - 7 (benches/kernels.rs:110-119, seeds 3 and 7), head-major scales
+    (1 + (i % cap + 3 (i / cap)) % period) / 512 (periods 7 and 11), channel-major V^T
+    ((i*37 % 997) - 498) / 512 in f16. Checks what the reference's bench asserts (finite, not all
+    zero, the timed launches leave the output bit-identical) and times back-to-back launches with
+    HIP events, and synchronised calls (launch + wait, the reference's timed unit) by wall clock."""
+    heads, inner = SWEEP_HEADS, SWEEP_HEADS * 128
+    cap = -(-(tokens + 16) // 128) * 128
+    i = torch.arange(cap * inner, dtype=torch.int64, device=dev)
+    q = ((i * 37 + 3) % 15 - 7).to(torch.int8).view(torch.int32)
+    k = ((i * 37 + 7) % 15 - 7).to(torch.int8).view(torch.int32)
+    vt = (((i * 37) % 997 - 498).to(torch.float32) / 512.0).to(torch.float16)
+    del i
+    j = torch.arange(cap * heads, dtype=torch.int64, device=dev)
+    base = j % cap + 3 * (j // cap)
+    qs = ((1 + base % 7).to(torch.float32) / 512.0).contiguous()
+    ks = ((1 + base % 11).to(torch.float32) / 512.0).contiguous()
+    del j, base
+    out = torch.zeros((tokens, inner), dtype=torch.float16, device=dev)
+    cfg = H.AttentionCfg(inner, inner, inner, tokens, cap, 1.0)
+
+    def run():
+        H.attention_i8qkhm(cfg, tokens, heads, q, qs, k, ks, vt, out)
+
+    run()
+    torch.cuda.synchronize()
+    expected = out.clone()
+    finite = bool(torch.isfinite(expected).all().item())
+    nonzero = bool((expected.view(torch.int16) != 0).any().item())
+    ms = time_launches(torch, run, reps)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+        torch.cuda.synchronize()
+    ms_sync = (time.perf_counter() - t0) * 1e3 / reps
+    stable = bool(torch.equal(out.view(torch.int16), expected.view(torch.int16)))
+    ops = 4.0 * tokens * tokens * inner
+    return {"tokens": tokens, "capacity": cap, "ms": round(ms, 5),
+            "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+            "frac_int8_peak": round(ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+            "ms_synchronised_call": round(ms_sync, 5), "reps": reps, "output_finite": finite,
+            "output_nonzero": nonzero, "replays_bit_identical": stable}
+
+
+def ref_sweep(torch, H, budget_s: float) -> dict:
+    """The reference's attention sweep as one JSON line; each case gets about budget_s seconds
+    of timed launches (at least 3)."""
+    dev = torch.device("cuda:0")
+    rows = []
+    for tokens in SWEEP_TOKENS:
+        probe = sweep_case(torch, H, dev, tokens, 3)
+        reps = max(3, min(2000, int(budget_s * 1e3 / max(probe["ms"], 1e-3))))
+        row = sweep_case(torch, H, dev, tokens, reps)
+        print(f"# sweep tokens={tokens}: {row['ms']} ms, {row['tops']} TOPS", file=sys.stderr,
+              flush=True)
+        rows.append(row)
+        torch.cuda.empty_cache()
+    last = rows[-1]
+    return {"metric": "attention_i8qkhm TOPS over the reference's sweep (benches/kernels.rs:562-656)",
+            "value": last["tops"], "unit": "TOPS", "n_gpus": 1, "higher_is_better": True,
+            "dtype": "int8", "data": "synthetic (the reference bench's operand formulas)",
+            "config": {"workload": f"ref-sweep: attention_i8qkhm, H={SWEEP_HEADS}, D=128, "
+                                   "tokens " + ",".join(map(str, SWEEP_TOKENS)) +
+                                   "; value = TOPS at the last (37,977 tokens, 768p)",
+                       "heads": SWEEP_HEADS},
+            "sweep": rows}
+
 
 def copy_calibration(torch) -> None:
     """A plain device-to-device copy of COPY_BYTES (reads COPY_BYTES, writes COPY_BYTES). Under
@@ -411,7 +518,10 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + ["ref-sweep"],
+                    help="a BASELINE config, or ref-sweep: the reference's own attention sweep")
+    ap.add_argument("--sweep-seconds", type=float, default=1.0,
+                    help="ref-sweep: seconds of timed launches per case")
     ap.add_argument("--cpu-rows", type=int, default=32, help="query rows per head for the CPU leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-adjacent", action="store_true",
@@ -432,6 +542,10 @@ def main() -> None:
         return
 
     import h3attn as H
+
+    if args.workload == "ref-sweep":
+        print(json.dumps(ref_sweep(torch, H, args.sweep_seconds)), flush=True)
+        return
 
     dev = torch.device("cuda:0")
     tokens, heads, grid = WORKLOADS[args.workload]
@@ -465,10 +579,20 @@ def main() -> None:
     text = TextCross(torch, H, dev, tokens, heads, cap, qi, qs)
     with_text = args.workload == "c4"  # config 4 = joint self-attention + text cross-attention
 
+    # The three prepare launches are independent branches joined before the attention, as the
+    # reference records them (src/stack.rs:1751-1813) and h3_stack_attend_fused runs them: Q on
+    # the current stream, K and the V transpose on two side streams (default priority).
+    side_k, side_v = torch.cuda.Stream(), torch.cuda.Stream()
+
     def step(record: bool):
+        cur = torch.cuda.current_stream()
+        side_k.wait_stream(cur)
+        side_v.wait_stream(cur)
         H.prepare_qk_rope_i8hm(pq, tokens, fused_bf16, qnorm, cos_t, sin_t, qi, qs)
-        H.prepare_qk_rope_i8hm(pk, tokens, fused_bf16, knorm, cos_t, sin_t, ki, ks)
-        H.transpose_qkv_v_f16(tc, tokens, tokens, fused_bf16, vt)
+        H.prepare_qk_rope_i8hm(pk, tokens, fused_bf16, knorm, cos_t, sin_t, ki, ks, stream=side_k)
+        H.transpose_qkv_v_f16(tc, tokens, tokens, fused_bf16, vt, stream=side_v)
+        cur.wait_stream(side_k)
+        cur.wait_stream(side_v)
         if record:
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
@@ -527,8 +651,8 @@ def main() -> None:
             "heads": heads,
             "head_dim": 128,
             "capacity": cap,
-            "step": "prepare_qk_rope_i8hm(Q) + prepare_qk_rope_i8hm(K) + transpose_qkv_v_f16 "
-                    "+ attention_i8qkhm" + (" + text K/V^T prep + attention_i8qkhm_cross (512 text "
+            "step": "prepare_qk_rope_i8hm(Q) | prepare_qk_rope_i8hm(K) | transpose_qkv_v_f16 "
+                    "(three branches) -> attention_i8qkhm" + (" + text K/V^T prep + attention_i8qkhm_cross (512 text "
                                             "tokens, 8 KV heads, 20% padding masked)"
                                             if with_text else ""),
         },
@@ -567,6 +691,9 @@ def main() -> None:
             "ms": round(cross_ms, 4),
             "tops": round(text.ops / (cross_ms * 1e-3) / 1e12, 1),
             "frac_int8_peak": round(text.ops / (cross_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+        print("# smoothed route...", file=sys.stderr, flush=True)
+        line["adjacent_kernels"]["k_smoothing"] = smoothed_route(
+            torch, H, dev, tokens, heads, cap, fused_bf16, knorm, cos_t, sin_t)
         print("# platform attention...", file=sys.stderr, flush=True)
         line["adjacent_kernels"]["platform_flash_f16"] = platform_flash(torch, dev, tokens, heads,
                                                                         att_avg)

@@ -403,6 +403,7 @@ int h3_prepare_k_rope_smooth_i8hm(const h3_prepare_cfg* cfg, uint32_t tokens, h3
   hipError_t e = launch_rope_colmean(*cfg, tokens, x.ptr, static_cast<const float*>(weight.ptr),
                                      static_cast<const float*>(cos_t.ptr),
                                      static_cast<const float*>(sin_t.ptr),
+                                     static_cast<float*>(scales.ptr),
                                      static_cast<float*>(mean.ptr), s);
   if (e != hipSuccess) return launched(stage, e);
   return launched(stage, launch_prepare_qk_rope_mean(

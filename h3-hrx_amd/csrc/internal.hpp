@@ -55,9 +55,11 @@ hipError_t launch_rope_qknorm(const h3_rope_cfg& cfg, uint32_t tokens, const voi
                               uint16_t* v_out, hipStream_t stream);
 hipError_t launch_colmean(uint32_t width, uint32_t row_stride, uint32_t elem, uint32_t tokens,
                           const void* x, float* mean, hipStream_t stream);
+// Two launches: r of every K row into r_scratch ([heads][capacity] floats), then the column
+// chains; r_scratch may be the quantizer's scales binding, which the next pass overwrites.
 hipError_t launch_rope_colmean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
                                const float* weight, const float* cos_t, const float* sin_t,
-                               float* mean, hipStream_t stream);
+                               float* r_scratch, float* mean, hipStream_t stream);
 hipError_t launch_prepare_qk_rope_mean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
                                        const float* weight, const float* cos_t,
                                        const float* sin_t, const float* mean, int32_t* codes,

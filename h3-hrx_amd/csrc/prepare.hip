@@ -10,6 +10,9 @@
 // The arithmetic is built with -ffp-contract=off: every float operation below is one IEEE
 // operation in the order written, which is what makes the quantizer bit-exact with the
 // reference's fp32 op order (kernels/prepare_qk_i8.loom:63-188).
+#include <algorithm>
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace h3 {
@@ -184,12 +187,40 @@ __device__ __forceinline__ RopeLane rope_lane(int lane, const float* weight, con
   return t;
 }
 
-__device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const RopeLane& tab, float eps) {
+// o rounded to f16 (round to nearest even) and widened back. The empty asm keeps o a rounded f32
+// value first: without it the compiler may fold the multiply that produced o into a
+// mixed-precision FMA that rounds the exact product once, straight to f16 (v_fma_mixlo_f16),
+// which differs from rounding to f32 and then to f16 whenever the two roundings interact.
+__device__ __forceinline__ float f16_round(float o) {
+  asm("" : "+v"(o));
+  return (float)(_Float16)o;
+}
+
+// r = 1/sqrt(mean(v^2) + eps) of the 128-channel row held by a half-wave (four channels per lane).
+__device__ __forceinline__ float rms_inverse(v4f v, float eps) {
   float part = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
   part = half_sum(part);
   float ms = part * 0.0078125f;
   float me = ms + eps;
-  float r = 1.0f / __builtin_sqrtf(me);
+  return 1.0f / __builtin_sqrtf(me);
+}
+
+// One channel of rmsnorm_rope_f16 given its row's r: the same operations in the same order
+// (xn = (v*r)*w for the channel and for its rotation partner, then xn*cos -/+ partner*sin or xn
+// itself), rounded to f16 and widened, so the same bits.
+__device__ __forceinline__ float rope_channel(float v, float pv, float r, float w, float pw,
+                                              float c, float s, bool lo, bool pair) {
+  const float xn = (v * r) * w;
+  const float px = (pv * r) * pw;
+  const float a = xn * c;
+  const float b = px * s;
+  float o = lo ? (a - b) : (a + b);
+  o = pair ? o : xn;
+  return f16_round(o);
+}
+
+__device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const RopeLane& tab, float eps) {
+  const float r = rms_inverse(v, eps);
   const float4 w = tab.w;
   v4f xn;
   xn[0] = (v[0] * r) * w.x;
@@ -210,7 +241,7 @@ __device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const RopeLane&
     float b = px[j] * ss[j];
     float o = lo ? (a - b) : (a + b);
     o = pair ? o : xn[j];
-    out[j] = (float)(_Float16)o;
+    out[j] = f16_round(o);
   }
   return out;
 }
@@ -265,7 +296,7 @@ __device__ __forceinline__ void rmsnorm_rope_f16(float (&v)[8], int l, const Rop
     const float b = px * tab.s[j];
     float o = lo ? (a - b) : (a + b);
     o = pair ? o : xn[j];
-    v[j] = (float)(_Float16)o;
+    v[j] = f16_round(o);
   }
 }
 
@@ -475,39 +506,215 @@ __global__ __launch_bounds__(64) void k_colmean(const void* __restrict__ x,
   mean[c] = acc / (float)tokens;
 }
 
-// First pass of the fused K smoothing: the column mean of RMSNorm+RoPE(K) rounded to f16, over
-// all tokens, in sequential fp32 order per column. One workgroup per head: its eight half-waves
-// rotate 32 tokens of that head into LDS, then 128 lanes add their column in token order.
-__global__ __launch_bounds__(256) void k_rope_colmean(
-    const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, float* __restrict__ mean, uint32_t tokens,
-    uint32_t row_stride, uint32_t head_offset, float eps, uint32_t elem) {
-  constexpr int kStep = 32;
-  __shared__ float tile[kStep][128 + 4];
-  const uint32_t h = blockIdx.x;
+// The fused K smoothing's column mean: mean[c] = (sum_t rope(K)[t][c]) / tokens, where rope(K) is
+// RMSNorm+RoPE of K rounded to f16 (exactly what h3_rope_qknorm_f16 writes) and the sum runs in
+// token order in fp32, one dependent add per token (kernels/colmean_f32.loom in-file 30-40). The
+// add chain of each column is inherently sequential; everything feeding it is spread out.
+//
+// Pass 1 (k_rope_rms): r of every (token, head) row, one row per half-wave, head-major into a
+// float buffer [heads][capacity] (the scales binding, which the quantizer pass then overwrites).
+// Rows are taken head-major (row = h * tokens + t), so a workgroup's writes are contiguous; each
+// half-wave loads kRowsAhead rows before reducing any, and the grid strides over the rows.
+constexpr uint32_t kRmsRowsPerStep = kRowsPerBlock * kRowsAhead;  // 32 rows per workgroup step
+__global__ __launch_bounds__(256) void k_rope_rms(const void* __restrict__ x,
+                                                  float* __restrict__ r_out, uint32_t tokens,
+                                                  uint32_t heads, uint32_t row_stride,
+                                                  uint32_t head_offset, uint32_t capacity,
+                                                  float eps, uint32_t elem) {
   const int half = threadIdx.x >> 5, lane = threadIdx.x & 31;
-  const uint32_t col = head_offset + 128u * h + 4u * lane;
-  float acc = 0.0f;
-  for (uint32_t t0 = 0; t0 < tokens; t0 += kStep) {
+  const uint32_t rows = tokens * heads;
+  for (uint32_t base = blockIdx.x * kRmsRowsPerStep; base < rows;
+       base += gridDim.x * kRmsRowsPerStep) {
+    v4f v[kRowsAhead];
+    uint32_t row[kRowsAhead];
 #pragma unroll
-    for (int i = 0; i < kStep / kRowsPerBlock; ++i) {
-      const int tt = i * kRowsPerBlock + half;
-      const uint32_t t = t0 + tt;
-      if (t < tokens) {
-        v4f v = widen4(load4(x, (size_t)t * row_stride + col), elem);
-        v4f o = rmsnorm_rope_f16(v, lane, weight, cos_t + (size_t)t * 48,
-                                 sin_t + (size_t)t * 48, eps);
-        *reinterpret_cast<float4*>(&tile[tt][4 * lane]) = make_float4(o[0], o[1], o[2], o[3]);
+    for (int i = 0; i < kRowsAhead; ++i) {
+      row[i] = base + kRowsPerBlock * i + half;
+      const uint32_t rr = row[i] < rows ? row[i] : rows - 1;  // every lane stays in the butterfly
+      const uint32_t h = rr / tokens, t = rr - h * tokens;
+      v[i] = widen4(load4(x, (size_t)t * row_stride + head_offset + 128u * h + 4u * lane), elem);
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsAhead; ++i) {
+      const float r = rms_inverse(v[i], eps);
+      if (row[i] < rows && lane == 0) {
+        const uint32_t h = row[i] / tokens, t = row[i] - h * tokens;
+        r_out[(size_t)h * capacity + t] = r;
+      }
+    }
+  }
+}
+
+// Pass 2 (k_rope_colmean): one workgroup per 16 channels of one head (8 per head, 256 at 32
+// heads). Workgroups 0-5 of a head own rotation pairs: channels 8k..8k+7 and 48+8k..48+8k+7,
+// which are each other's RoPE partners and share cos/sin columns 8k..8k+7, so every input byte is
+// loaded once; workgroups 6 and 7 own channels 96-111 and 112-127 (not rotated). Eight waves:
+// lanes 0-15 of wave 0 each run one channel's add chain over an LDS tile; wave 4 (the other wave
+// on wave 0's SIMD) only joins the barriers, so the chain has its SIMD to itself; the six other
+// waves (384 producer threads, one token each per 384-token chunk) compute the f16 RoPE values
+// into the double-buffered tile. Producers keep three chunks of raw inputs in registers and load
+// each chunk two chunks ahead, so the chain (tokens dependent adds) stays the critical path. The
+// eight workgroups of a head are placed on one XCD so that the rows they read share an L2.
+constexpr int kSlab = 16;                        // channels per workgroup
+constexpr int kSlabs = 128 / kSlab;              // workgroups per head
+constexpr int kColmeanThreads = 512;
+constexpr int kChunk = 384;                      // tokens per chunk = producer threads
+constexpr int kChunkPad = kChunk + 4;            // floats per LDS column (a 16-byte multiple)
+constexpr int kRing = 3;                         // chunks of raw inputs held per producer
+
+struct PairToken {  // the raw inputs of one token for a workgroup's 16 channels
+  uint4 a, b;       // channels of the first and second group of eight (16-bit bit patterns)
+  float4 c[2], s[2];  // cos/sin of the pair's eight table columns (rotated workgroups only)
+  float r;
+};
+
+__device__ __forceinline__ void load_pair_token(PairToken& in, const void* x, const float* r_in,
+                                                const float* cos_t, const float* sin_t,
+                                                uint32_t t, uint32_t tokens, size_t col_a,
+                                                size_t col_b, uint32_t row_stride,
+                                                size_t r_base, uint32_t tab0, bool rotated) {
+  if (t >= tokens) return;  // past the sequence: never consumed
+  const uint16_t* row = reinterpret_cast<const uint16_t*>(x) + (size_t)t * row_stride;
+  in.a = *reinterpret_cast<const uint4*>(row + col_a);
+  in.b = *reinterpret_cast<const uint4*>(row + col_b);
+  in.r = r_in[r_base + t];
+  if (rotated) {
+    const float* ct = cos_t + (size_t)t * 48 + tab0;
+    const float* st = sin_t + (size_t)t * 48 + tab0;
+    in.c[0] = *reinterpret_cast<const float4*>(ct);
+    in.c[1] = *reinterpret_cast<const float4*>(ct + 4);
+    in.s[0] = *reinterpret_cast<const float4*>(st);
+    in.s[1] = *reinterpret_cast<const float4*>(st + 4);
+  }
+}
+
+__device__ __forceinline__ void unpack8(uint4 b, uint32_t elem, float (&v)[8]) {
+  const v4f lo = widen4(make_uint2(b.x, b.y), elem), hi = widen4(make_uint2(b.z, b.w), elem);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = lo[j];
+    v[4 + j] = hi[j];
+  }
+}
+
+__global__ __launch_bounds__(kColmeanThreads) void k_rope_colmean(
+    const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const float* __restrict__ r_in, float* __restrict__ mean,
+    uint32_t tokens, uint32_t row_stride, uint32_t head_offset, uint32_t capacity,
+    uint32_t total, uint32_t per_xcd, uint32_t elem) {
+  __shared__ __align__(16) float tile[2][kSlab][kChunkPad];
+  const uint32_t b = blockIdx.x;
+  const uint32_t logical = (b % 8) * per_xcd + b / 8;  // workgroup b runs on XCD b % 8
+  if (logical >= total) return;                       // whole workgroup, before any barrier
+  const uint32_t h = logical / kSlabs, k = logical % kSlabs;
+  const bool rotated = k < 6;
+  // channels of tile rows 0-7 and 8-15
+  const uint32_t ca = rotated ? 8 * k : 96 + 16 * (k - 6);
+  const uint32_t cb = rotated ? ca + 48 : ca + 8;
+  const size_t col_a = head_offset + 128u * h + ca, col_b = head_offset + 128u * h + cb;
+  const size_t r_base = (size_t)h * capacity;
+  const uint32_t chunks = (tokens + kChunk - 1) / kChunk;
+  const int wave = threadIdx.x >> 6;
+  const bool producer = wave != 0 && wave != 4;
+  const int p = (wave < 4 ? wave - 1 : wave - 2) * 64 + (threadIdx.x & 63);  // 0..383
+
+  float wa[8], wb[8];
+  PairToken ring[kRing];
+  auto load = [&](PairToken& in, uint32_t j) {
+    load_pair_token(in, x, r_in, cos_t, sin_t, j * kChunk + p, tokens, col_a, col_b, row_stride,
+                    r_base, 8 * k, rotated);
+  };
+  // Chunk j's values into tile buffer j % 2: the operations of rmsnorm_rope_f16, channel by
+  // channel (rope_channel), so the values are bit-identical to h3_rope_qknorm_f16's output.
+  auto store = [&](const PairToken& in, uint32_t j) {
+    if (j * kChunk + p >= tokens) return;
+    float (*dst)[kChunkPad] = tile[j & 1];
+    float va[8], vb[8];
+    unpack8(in.a, elem, va);
+    unpack8(in.b, elem, vb);
+    if (rotated) {
+      const float cc[8] = {in.c[0].x, in.c[0].y, in.c[0].z, in.c[0].w,
+                           in.c[1].x, in.c[1].y, in.c[1].z, in.c[1].w};
+      const float ss[8] = {in.s[0].x, in.s[0].y, in.s[0].z, in.s[0].w,
+                           in.s[1].x, in.s[1].y, in.s[1].z, in.s[1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dst[i][p] = rope_channel(va[i], vb[i], in.r, wa[i], wb[i], cc[i], ss[i], true, true);
+        dst[8 + i][p] = rope_channel(vb[i], va[i], in.r, wb[i], wa[i], cc[i], ss[i], false, true);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dst[i][p] = rope_channel(va[i], 0.0f, in.r, wa[i], 0.0f, 0.0f, 0.0f, false, false);
+        dst[8 + i][p] = rope_channel(vb[i], 0.0f, in.r, wb[i], 0.0f, 0.0f, 0.0f, false, false);
+      }
+    }
+  };
+
+  if (producer) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      wa[i] = weight[ca + i];
+      wb[i] = weight[cb + i];
+    }
+#pragma unroll
+    for (int i = 0; i < kRing; ++i)
+      if ((uint32_t)i < chunks) load(ring[i], i);
+    store(ring[0], 0);
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  const int lane = threadIdx.x;  // the chain lanes (wave 0, lanes 0-15)
+  // One chunk: producers store chunk j + 1 and load chunk j + 3 into the ring slot chunk j
+  // left; lanes 0-15 add chunk j. Slot indices are compile-time (the loop is unrolled by kRing).
+  auto chunk = [&](uint32_t j, auto slot) {
+    constexpr int kNext = (decltype(slot)::value + 1) % kRing;
+    if (producer && j + 1 < chunks) {
+      store(ring[kNext], j + 1);
+      if (j + kRing < chunks) load(ring[decltype(slot)::value], j + kRing);
+    }
+    if (threadIdx.x < kSlab) {
+      const float* col = tile[j & 1][lane];
+      const uint32_t n = min((uint32_t)kChunk, tokens - j * kChunk);
+      if (n == kChunk) {
+        float4 cur[8], nxt[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cur[i] = *reinterpret_cast<const float4*>(col + 4 * i);
+        for (int g = 0; g < kChunk / 32; ++g) {
+          if (g + 1 < kChunk / 32) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              nxt[i] = *reinterpret_cast<const float4*>(col + 32 * (g + 1) + 4 * i);
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            acc = acc + cur[i].x;
+            acc = acc + cur[i].y;
+            acc = acc + cur[i].z;
+            acc = acc + cur[i].w;
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+        }
+      } else {
+        for (uint32_t i = 0; i < n; ++i) acc = acc + col[i];
       }
     }
     __syncthreads();
-    if (threadIdx.x < 128) {
-      const uint32_t n = min((uint32_t)kStep, tokens - t0);
-      for (uint32_t i = 0; i < n; ++i) acc = acc + tile[i][threadIdx.x];
-    }
-    __syncthreads();
+  };
+  uint32_t j = 0;
+  for (; j + kRing <= chunks; j += kRing) {
+    chunk(j, std::integral_constant<int, 0>{});
+    chunk(j + 1, std::integral_constant<int, 1>{});
+    chunk(j + 2, std::integral_constant<int, 2>{});
   }
-  if (threadIdx.x < 128) mean[128u * h + threadIdx.x] = acc / (float)tokens;
+  if (j < chunks) chunk(j, std::integral_constant<int, 0>{});
+  if (j + 1 < chunks) chunk(j + 1, std::integral_constant<int, 1>{});
+  if (threadIdx.x < kSlab) {
+    const uint32_t c = lane < 8 ? ca + lane : cb + (lane - 8);
+    mean[128u * h + c] = acc / (float)tokens;
+  }
 }
 
 // ---------------------------------------------------------------- transposes
@@ -635,9 +842,19 @@ hipError_t launch_colmean(uint32_t width, uint32_t row_stride, uint32_t elem, ui
 
 hipError_t launch_rope_colmean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
                                const float* weight, const float* cos_t, const float* sin_t,
-                               float* mean, hipStream_t stream) {
-  hipLaunchKernelGGL(k_rope_colmean, dim3(cfg.heads), dim3(256), 0, stream, x, weight, cos_t,
-                     sin_t, mean, tokens, cfg.row_stride, cfg.head_offset, cfg.eps, cfg.elem);
+                               float* r_scratch, float* mean, hipStream_t stream) {
+  const uint32_t rows = tokens * cfg.heads;
+  const uint32_t rms_blocks = std::min(div_up(rows, kRmsRowsPerStep), 8192u);
+  hipLaunchKernelGGL(k_rope_rms, dim3(rms_blocks), dim3(256), 0, stream, x,
+                     r_scratch, tokens, cfg.heads, cfg.row_stride, cfg.head_offset,
+                     cfg.token_capacity, cfg.eps, cfg.elem);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const uint32_t total = cfg.heads * kSlabs, per_xcd = div_up(total, 8);
+  hipLaunchKernelGGL(k_rope_colmean, dim3(8 * per_xcd), dim3(kColmeanThreads), 0, stream, x,
+                     weight, cos_t,
+                     sin_t, r_scratch, mean, tokens, cfg.row_stride, cfg.head_offset,
+                     cfg.token_capacity, total, per_xcd, cfg.elem);
   return hipGetLastError();
 }
 

@@ -37,6 +37,13 @@ struct h3_stack {
   h3_transpose_cfg transpose{};
   // IntQk (src/stack.rs:229-238)
   h3_view qi{}, ki{}, qs{}, ks{}, kmean{}, zmean{}, vt{};
+  // The fused route's three independent prepare launches run as branches (the reference
+  // records prep_q, prep_k and the V transpose as separate graph branches joined before the
+  // attention, src/stack.rs:1751-1813): two side streams at the default priority, forked from
+  // and joined back into the caller's stream with events, so the pattern is stream-ordered and
+  // capturable.
+  hipStream_t side[2] = {nullptr, nullptr};
+  hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
 };
 
 namespace h3 {
@@ -45,6 +52,35 @@ namespace {
 void release(h3_stack* s) {
   for (h3_view* v : {&s->qi, &s->ki, &s->qs, &s->ks, &s->kmean, &s->zmean, &s->vt})
     if (v->ptr) (void)hipFree(v->ptr);
+  for (hipStream_t& st : s->side)
+    if (st) (void)hipStreamDestroy(st);
+  for (hipEvent_t* e : {&s->fork, &s->join[0], &s->join[1]})
+    if (*e) (void)hipEventDestroy(*e);
+}
+
+// Branch b of the fused route waits for everything the caller enqueued before the call.
+int fork_branches(h3_stack* s, hipStream_t caller) {
+  hipError_t e = hipEventRecord(s->fork, caller);
+  for (int b = 0; b < 2 && e == hipSuccess; ++b) e = hipStreamWaitEvent(s->side[b], s->fork, 0);
+  if (e != hipSuccess)
+    return set_error(H3_ERR_LAUNCH, "fused attention operands: forking the branches failed (%s)",
+                     hipGetErrorString(e));
+  return H3_OK;
+}
+
+// The caller's stream waits for both branches (also after a failed launch, so no branch is left
+// outside the caller's order).
+int join_branches(h3_stack* s, hipStream_t caller) {
+  hipError_t e = hipSuccess;
+  for (int b = 0; b < 2; ++b) {
+    hipError_t r = hipEventRecord(s->join[b], s->side[b]);
+    if (r == hipSuccess) r = hipStreamWaitEvent(caller, s->join[b], 0);
+    if (e == hipSuccess) e = r;
+  }
+  if (e != hipSuccess)
+    return set_error(H3_ERR_LAUNCH, "fused attention operands: joining the branches failed (%s)",
+                     hipGetErrorString(e));
+  return H3_OK;
 }
 
 }  // namespace
@@ -124,6 +160,18 @@ int h3_stack_build(const h3_stack_dims* dims, h3_stack** out) {
       return set_error(H3_ERR_NO_DEVICE, "stack: clearing %zu bytes failed", a.bytes);
     }
   }
+  if (s->fused) {
+    bool ok = true;
+    for (hipStream_t& st : s->side)
+      ok = ok && hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess;
+    for (hipEvent_t* e : {&s->fork, &s->join[0], &s->join[1]})
+      ok = ok && hipEventCreateWithFlags(e, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+      release(s);
+      delete s;
+      return set_error(H3_ERR_NO_DEVICE, "stack: creating the branch streams and events failed");
+    }
+  }
   *out = s;
   return H3_OK;
 }
@@ -181,17 +229,26 @@ int h3_stack_attend_fused(h3_stack* s, uint32_t t, h3_view fused, h3_view qnorm,
       (st = require(stage, 3, sin_t, rows * 48 * 4)) ||
       (st = require("attention", 5, out, rows * inner * 2)))
     return st;
-  if ((st = h3_prepare_qk_rope_i8hm(&s->prep_q, t, fused, qnorm, cos_t, sin_t, s->qi, s->qs,
-                                    stream)))
-    return st;
-  if (s->smooth)
-    st = h3_prepare_k_rope_smooth_i8hm(&s->prep_k, t, fused, knorm, cos_t, sin_t, s->kmean, s->ki,
-                                       s->ks, stream);
-  else
-    st = h3_prepare_qk_rope_i8hm(&s->prep_k, t, fused, knorm, cos_t, sin_t, s->ki, s->ks, stream);
-  if (st) return st;
+  // Three branches (src/stack.rs:1751-1813): Q on the caller's stream, K and the V transpose on
+  // the side streams, all joined before the attention.
+  hipStream_t caller = reinterpret_cast<hipStream_t>(stream);
+  if ((st = fork_branches(s, caller))) return st;
+  h3_stream k_branch = reinterpret_cast<h3_stream>(s->side[0]);
+  h3_stream v_branch = reinterpret_cast<h3_stream>(s->side[1]);
+  st = h3_prepare_qk_rope_i8hm(&s->prep_q, t, fused, qnorm, cos_t, sin_t, s->qi, s->qs, stream);
+  if (!st) {
+    if (s->smooth)
+      st = h3_prepare_k_rope_smooth_i8hm(&s->prep_k, t, fused, knorm, cos_t, sin_t, s->kmean,
+                                         s->ki, s->ks, k_branch);
+    else
+      st = h3_prepare_qk_rope_i8hm(&s->prep_k, t, fused, knorm, cos_t, sin_t, s->ki, s->ks,
+                                   k_branch);
+  }
   // "fused V transpose" (src/stack.rs:1599-1610): workload [t]
-  if ((st = h3_transpose_qkv_v_f16(&s->transpose, t, t, fused, s->vt, stream))) return st;
+  if (!st) st = h3_transpose_qkv_v_f16(&s->transpose, t, t, fused, s->vt, v_branch);
+  const int joined = join_branches(s, caller);
+  if (st) return st;
+  if (joined) return joined;
   return stack_attention(s, t, out, stream);
 }
 

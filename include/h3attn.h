@@ -537,14 +537,20 @@ typedef struct h3_stack h3_stack;
 /* Stack::build (src/stack.rs:260-987, INT8 branch): chooses the route (fused head-major operands,
  * head-major separate, or token-major below 4096 tokens), derives every kernel config
  * (src/stack.rs:597-766), and allocates the zero-filled IntQk operand buffers
- * (src/stack.rs:845-908). The only allocating call; attend/prepare never allocate. */
+ * (src/stack.rs:845-908); on the fused route it also creates two side streams (default
+ * priority) and three events for the branch fan-out below. The only allocating call;
+ * attend/prepare never allocate. */
 int h3_stack_build(const h3_stack_dims *dims, h3_stack **out);
 void h3_stack_destroy(h3_stack *stack);
 uint32_t h3_stack_capacity(const h3_stack *stack);
 
 /* Stack::prepare_fused_operands (src/stack.rs:1541-1616) followed by attention: reads the fused
  * QKV projection [t][3*heads*128], per-head norm weights, cos/sin [t][48]; writes the attention
- * output [t][heads*128] f16. */
+ * output [t][heads*128] f16. The Q quantizer, the K quantizer (smoothed or not) and the V
+ * transpose are three independent branches, as the reference records them
+ * (src/stack.rs:1751-1813): forked from `stream` onto the stack's side streams with an event and
+ * joined back before the attention, so the call stays ordered on `stream` and capturable. Calls
+ * on one stack must not overlap (they share its side streams and operand buffers). */
 int h3_stack_attend_fused(h3_stack *stack, uint32_t t, h3_view fused, h3_view qnorm,
                           h3_view knorm, h3_view cos_t, h3_view sin_t, h3_view out,
                           h3_stream stream);

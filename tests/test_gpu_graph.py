@@ -126,3 +126,23 @@ def test_vsa_attention_replays_from_a_graph(dev):
     print("graph: vsa attention, both forms", flush=True)
     replay_matches(torch, dev, run, [out, out_ws])
     assert np.array_equal(from_dev(out), from_dev(out_ws))
+
+
+@pytest.mark.parametrize("smooth", [False, True])
+def test_stack_fused_route_branches_replay_from_a_graph(dev, smooth):
+    """h3_stack_attend_fused forks the Q, K and V preparations onto the stack's side streams and
+    joins them before the attention; captured from the caller's stream, the branches join the
+    graph and every replay gives the eager output bit for bit."""
+    import torch
+
+    from test_gpu_stack import fused_inputs
+
+    tokens, heads = 4100, 2
+    rng = np.random.default_rng(41)
+    fused, qw, kw, cos_t, sin_t = fused_inputs(rng, tokens, heads)
+    st = H.Stack(heads, tokens, ksmooth=smooth, fused=True)
+    args = [to_dev(a, dev) for a in (fused, qw, kw, cos_t, sin_t)]
+    out = torch.zeros((tokens, heads * 128), dtype=torch.float16, device=dev)
+    print(f"graph: stack fused route, smooth={smooth}", flush=True)
+    replay_matches(torch, dev, lambda: st.attend_fused(tokens, *args, out), [out])
+    st.close()

@@ -9,6 +9,8 @@ Mirrors the reference's tests:
   - transposed_values_clear_reused_capacity (3373-3444)
 All through the C ABI.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -226,27 +228,45 @@ def test_fused_operands_are_byte_identical_to_separate_preparation(dev, tokens, 
     assert torch.equal(old, new)
 
 
-@pytest.mark.parametrize("tokens,heads", [(257, 4), (4097, 8)])
-def test_fused_k_smoothing_is_byte_identical_to_the_separate_route(dev, tokens, heads):
+@pytest.mark.parametrize("tokens,heads,bf16", [(1, 2, False), (257, 4, False), (383, 2, True),
+                                               (384, 4, False), (385, 2, False), (769, 2, True),
+                                               (4097, 8, False), (129024, 32, True)])
+def test_fused_k_smoothing_is_byte_identical_to_the_separate_route(dev, tokens, heads, bf16):
     """This build's fused K-mean + RoPE + quantize == rope_qknorm_f16 -> colmean_f32 ->
-    prepare_qk_i8hm(mean), the reference's smoothed route (src/stack.rs:1306-1326, 1727-1791)."""
+    prepare_qk_i8hm(mean), the reference's smoothed route (src/stack.rs:1306-1326, 1727-1791).
+    Lengths around the column-mean kernel's 384-token chunks, both input formats, and BASELINE
+    config 3's K (129,024 tokens x 32 heads) at full size; the oracle composition is checked up
+    to 4,097 tokens."""
     import torch
 
+    print(f"fused K smoothing tokens={tokens} heads={heads} bf16={bf16}", flush=True)
     width = heads * 128
     cap = O.capacity(tokens)
     rng = np.random.default_rng(tokens)
-    f = rng.standard_normal((tokens, 3 * width), np.float32)
-    f[:, width:2 * width] += rng.standard_normal(width).astype(np.float32) * np.float32(np.sqrt(2))
-    fused = O.f16_bits(f)
+    fmt, elem = (O.BF16, H.H3_ELEM_BF16) if bf16 else (O.F16, H.H3_ELEM_F16)
     kw = (1.0 + O.values(128, 0.1)).astype(np.float32)
     angles = rng.uniform(-3, 3, (tokens, 48)).astype(np.float32)
     cos_t, sin_t = np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
-    f_d, kw_d, c_d, s_d = (to_dev(a, dev) for a in (fused, kw, cos_t, sin_t))
+    kw_d, c_d, s_d = (to_dev(a, dev) for a in (kw, cos_t, sin_t))
+    if tokens <= 4097:
+        f = rng.standard_normal((tokens, 3 * width), np.float32)
+        f[:, width:2 * width] += (rng.standard_normal(width).astype(np.float32)
+                                  * np.float32(np.sqrt(2)))
+        fused = O.bf16_bits(f) if bf16 else O.f16_bits(f)
+        f_d = to_dev(fused, dev)
+    else:  # full size: generated on the device (the oracle composition is not run)
+        g = torch.Generator(device=dev)
+        g.manual_seed(tokens)
+        f = torch.randn((tokens, 3 * width), generator=g, device=dev)
+        f[:, width:2 * width] += torch.randn((width,), generator=g, device=dev) * math.sqrt(2.0)
+        f_d = f.to(torch.bfloat16 if bf16 else torch.float16).view(torch.int16)
+        del f
     # separate route
     k_rot = torch.zeros(tokens * width, dtype=torch.int16, device=dev)
     q_rot = torch.zeros(tokens * width, dtype=torch.int16, device=dev)
-    H.rope_qknorm_f16(H.RopeCfg(3 * width, heads, heads, width, 1e-5, 0, H.H3_ELEM_F16), tokens,
+    H.rope_qknorm_f16(H.RopeCfg(3 * width, heads, heads, width, 1e-5, 0, elem), tokens,
                       f_d, kw_d, kw_d, c_d, s_d, q_rot, k_rot, None)
+    del q_rot
     mean_sep = torch.zeros(width, dtype=torch.float32, device=dev)
     H.colmean_f32(width, tokens, k_rot, mean_sep)
     cfg = H.PrepareCfg(width, 0, heads, 1.0, cap, 1e-5, H.H3_ELEM_F16)
@@ -254,7 +274,7 @@ def test_fused_k_smoothing_is_byte_identical_to_the_separate_route(dev, tokens, 
     sep_s = torch.zeros(cap * heads, dtype=torch.float32, device=dev)
     H.prepare_qk_i8hm(cfg, tokens, k_rot, mean_sep, sep_c, sep_s)
     # fused route
-    cfg2 = H.PrepareCfg(3 * width, width, heads, 1.0, cap, 1e-5, H.H3_ELEM_F16)
+    cfg2 = H.PrepareCfg(3 * width, width, heads, 1.0, cap, 1e-5, elem)
     mean_f = torch.zeros(width, dtype=torch.float32, device=dev)
     fus_c = torch.zeros(cap * width, dtype=torch.uint8, device=dev)
     fus_s = torch.zeros(cap * heads, dtype=torch.float32, device=dev)
@@ -262,8 +282,10 @@ def test_fused_k_smoothing_is_byte_identical_to_the_separate_route(dev, tokens, 
     torch.cuda.synchronize()
     assert torch.equal(mean_sep.view(torch.int32), mean_f.view(torch.int32))
     assert torch.equal(sep_c, fus_c) and torch.equal(sep_s.view(torch.int32), fus_s.view(torch.int32))
+    if tokens > 4097:
+        return
     # and the oracle composition
-    roped = O.rope_qknorm_f16(fused, O.F16, tokens, 3 * width, width, heads, kw, cos_t, sin_t, 1e-5)
+    roped = O.rope_qknorm_f16(fused, fmt, tokens, 3 * width, width, heads, kw, cos_t, sin_t, 1e-5)
     mean = O.colmean(roped, O.F16, tokens, width, width)
     assert np.array_equal(mean_f.cpu().numpy().view(np.uint32), mean.view(np.uint32))
     want_w, _ = O.prepare_qk(roped, O.F16, mean, tokens, width, 0, heads, 1.0, True, cap)
