@@ -1338,6 +1338,11 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
 hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
                                   const int32_t* ki, const float* ks, const uint16_t* vt,
                                   const uint8_t* key_mask, uint16_t* out, hipStream_t stream) {
+  // Groups that divide a workgroup's eight waves run on the head-major kernel, whose workgroups
+  // hold every query head of one key/value head over the same staged K/V^T tiles.
+  const uint32_t group = cfg.q_heads / cfg.kv_heads;
+  if (8 % group == 0)
+    return launch_attention_hm_cross(cfg, qi, qs, ki, ks, vt, key_mask, out, stream);
   Args a{};
   a.qi = qi;
   a.qs = qs;

@@ -97,15 +97,22 @@ struct Geometry {
   const float* ks;
   const uint16_t* vt;
   uint16_t* out;
-  uint32_t tokens;       // keys (and readable query rows)
-  uint32_t rows;         // query rows written: min(token_count, tokens)
-  uint32_t capacity;
+  uint32_t tokens;       // keys (and, self-attention, readable query rows)
+  uint32_t rows;         // query rows written: min(token_count, tokens); cross: query tokens
+  uint32_t capacity;     // head-major row capacity of K / V^T (and, self-attention, of Q)
   uint32_t out_stride;
-  uint32_t q_blocks;     // ceil(token_count / 256)
+  uint32_t q_blocks;     // self: ceil(token_count / 256); cross: ceil(q_tokens / queries per head)
   uint32_t kv_head_limit;
   uint32_t head_limit;
-  uint32_t total;        // q_blocks * heads
+  uint32_t total;        // q_blocks * heads (cross: * kv_heads)
   uint32_t per_xcd;      // ceil(total / 8)
+  // cross-attention only: keys with key_mask == 0 are dead; the kv_group query heads of a key /
+  // value head share a workgroup, waves_per_head = 8 / kv_group waves each
+  const uint8_t* key_mask;
+  uint32_t q_tokens;
+  uint32_t q_capacity;
+  uint32_t kv_group;
+  uint32_t waves_per_head;
 };
 
 // Per-lane constants of the staging loads (the wave's share of each tile).
@@ -142,16 +149,20 @@ __device__ __forceinline__ Stager make_stager(const Geometry& g, int wave, int l
 // Staging of one stage (K tile at key kk0 with its scales, V^T tile at key vk0): buffer
 // descriptors that end at the last valid key (K, scales) or at the end of the head's V^T block.
 struct StepLoads {
-  __amdgpu_buffer_rsrc_t rk, rv, rs;
+  __amdgpu_buffer_rsrc_t rk, rv, rs, rm;
   char* kst;
   char* vst;
   float ks;
+  uint32_t keep;  // cross-attention: the key's mask byte (0 past the sequence)
 };
+template <bool kCross>
 __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_head, uint32_t kk0,
                                                char* kst, uint32_t vk0, char* vst) {
   StepLoads L;
   const uint32_t live = g.tokens > kk0 ? min(g.tokens - kk0, (uint32_t)kKeys) : 0u;
   L.rs = rsrc(g.ks + (size_t)kv_head * g.capacity + kk0, live * 4);
+  if (kCross) L.rm = rsrc(g.key_mask + kk0, live);
+  L.keep = 0;
   L.rk = rsrc(reinterpret_cast<const char*>(g.ki) + ((size_t)kv_head * g.capacity + kk0) * 128,
               live * 128);
   // V^T: columns past `tokens` inside the head's block are zero or belong to the next channel
@@ -164,11 +175,13 @@ __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_he
   L.ks = 0.0f;
   return L;
 }
-// Load `slot` of a step: 0 the key scale (into a register), then the K tile's LDS-DMA loads,
-// then the V^T tile's.
+// Load `slot` of a step: 0 the key scale (into a register; with cross-attention also the key's
+// mask byte), then the K tile's LDS-DMA loads, then the V^T tile's.
+template <bool kCross>
 __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int slot) {
   if (slot == 0) {
     L.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(L.rs, sg.skey * 4, 0, 0));
+    if (kCross) L.keep = __builtin_amdgcn_raw_buffer_load_b8(L.rm, sg.skey, 0, 0);
   } else if (slot <= kKLoads) {
     const int t = slot - 1;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -179,13 +192,15 @@ __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int s
         L.rv, (lds_void*)(L.vst + (sg.wave * kVLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
   }
 }
+template <bool kCross>
 __device__ __forceinline__ void issue_k(StepLoads& L, const Stager& sg) {
 #pragma unroll
-  for (int s = 0; s <= kKLoads; ++s) issue_load(L, sg, s);
+  for (int s = 0; s <= kKLoads; ++s) issue_load<kCross>(L, sg, s);
 }
+template <bool kCross>
 __device__ __forceinline__ void issue_v(StepLoads& L, const Stager& sg) {
 #pragma unroll
-  for (int s = kKLoads + 1; s < kLoadsPerStep; ++s) issue_load(L, sg, s);
+  for (int s = kKLoads + 1; s < kLoadsPerStep; ++s) issue_load<kCross>(L, sg, s);
 }
 
 // Scales of K tile k0 at their MFMA rows: ks, and c = -1.5*2^23*ks for a key inside the
@@ -204,6 +219,24 @@ __device__ __forceinline__ void store_scales(char* sst, const Stager& sg, float 
     sc[rot(sg.srow, 1)] = ks;
     sc[kKeys + rot(sg.srow, 2)] = k0 + sg.skey < tokens ? -(kMagic * ks) : -INFINITY;
   }
+}
+// Cross-attention: a key is live when its mask byte is nonzero (the mask's descriptor ends at the
+// last key, so keys past the sequence read 0).
+__device__ __forceinline__ void store_scales_masked(char* sst, const Stager& sg, float ks,
+                                                    uint32_t keep) {
+  if ((threadIdx.x & 63) < kSRows) {
+    float* sc = reinterpret_cast<float*>(sst);
+    sc[rot(sg.srow, 1)] = ks;
+    sc[kKeys + rot(sg.srow, 2)] = keep != 0 ? -(kMagic * ks) : -INFINITY;
+  }
+}
+template <bool kCross>
+__device__ __forceinline__ void store_stage_scales(char* sst, const Stager& sg, float ks,
+                                                   uint32_t keep, uint32_t k0, uint32_t tokens) {
+  if (kCross)
+    store_scales_masked(sst, sg, ks, keep);
+  else
+    store_scales(sst, sg, ks, k0, tokens);
 }
 
 // Barrier between steps: this wave's LDS writes, and its staging loads from before the current
@@ -566,6 +599,7 @@ __device__ __forceinline__ char* ring(int i, char* a0, char* a1, char* a2, char*
   return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : a3;
 }
 
+template <bool kCross>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2), amdgpu_num_vgpr(kOReg)))
 void k_attention_hm(Geometry g) {
@@ -583,15 +617,26 @@ void k_attention_hm(Geometry g) {
   const uint32_t b = blockIdx.x;
   const uint32_t logical = (b & 7u) * g.per_xcd + (b >> 3);
   if (logical >= g.total) return;
-  const uint32_t head_y = logical / g.q_blocks;
-  const uint32_t qb = logical % g.q_blocks;
-  const uint32_t kv_head = head_y % g.kv_head_limit;
-  const uint32_t head = kv_head % g.head_limit;
-
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
+  const uint32_t head_y = logical / g.q_blocks;
+  const uint32_t qb = logical % g.q_blocks;
+  uint32_t kv_head, head, q, q_limit, q_cap;
+  if (kCross) {  // block = (key/value head, query block); its kv_group query heads share it
+    kv_head = head_y;
+    head = kv_head * g.kv_group + (uint32_t)wave / g.waves_per_head;
+    q = (qb * g.waves_per_head + (uint32_t)wave % g.waves_per_head) * kTileQ + n;
+    q_limit = g.q_tokens;
+    q_cap = g.q_capacity;
+  } else {
+    kv_head = head_y % g.kv_head_limit;
+    head = kv_head % g.head_limit;
+    q = qb * kBlockQ + wave * kTileQ + n;
+    q_limit = g.tokens;
+    q_cap = g.capacity;
+  }
   const Stager sg = make_stager(g, wave, lane);
   const Lanes ln = make_lanes(n, half);
   // The QK bias 1.5*2^23, made opaque so that it stays in registers for the whole loop.
@@ -602,35 +647,34 @@ void k_attention_hm(Geometry g) {
   const uint32_t n_stages = (g.tokens + kKeys - 1) / kKeys;  // 64-key stages; 32-key tiles 2x
 
   // ---- prologue: K and scales of stages 0..2, V^T of stages 0 and 1 in flight
-  StepLoads L0 = plan_step(g, kv_head, 0, k0s, 0, v0s);
-  issue_k(L0, sg);
-  issue_v(L0, sg);
-  StepLoads L1 = plan_step(g, kv_head, kKeys, k1s, kKeys, v1s);
-  issue_k(L1, sg);
-  issue_v(L1, sg);
-  StepLoads L2 = plan_step(g, kv_head, 2 * kKeys, k2s, 0, nullptr);
-  issue_k(L2, sg);
+  StepLoads L0 = plan_step<kCross>(g, kv_head, 0, k0s, 0, v0s);
+  issue_k<kCross>(L0, sg);
+  issue_v<kCross>(L0, sg);
+  StepLoads L1 = plan_step<kCross>(g, kv_head, kKeys, k1s, kKeys, v1s);
+  issue_k<kCross>(L1, sg);
+  issue_v<kCross>(L1, sg);
+  StepLoads L2 = plan_step<kCross>(g, kv_head, 2 * kKeys, k2s, 0, nullptr);
+  issue_k<kCross>(L2, sg);
 
   Tile T;
-  const uint32_t q = qb * kBlockQ + wave * kTileQ + n;
   {
-    const uint32_t q_read = q < g.tokens ? q : g.tokens - 1;
-    const int32_t* src = g.qi + ((size_t)head * g.capacity + q_read) * 32;
+    const uint32_t q_read = q < q_limit ? q : q_limit - 1;
+    const int32_t* src = g.qi + ((size_t)head * q_cap + q_read) * 32;
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
-    T.qsl = g.qs[(size_t)head * g.capacity + q_read] * kLog2e;
+    T.qsl = g.qs[(size_t)head * q_cap + q_read] * kLog2e;
     T.negm = 1.0e30f;
     T.l = 0.0f;
   }
   zero_all(std::make_integer_sequence<int, 64>{});
-  store_scales(s0s, sg, L0.ks, 0, g.tokens);
-  store_scales(s1s, sg, L1.ks, kKeys, g.tokens);
+  store_stage_scales<kCross>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
+  store_stage_scales<kCross>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
   step_barrier<kWaitAll>();
 
   // ---- step -1: QK of key tiles 0 and 1, the probabilities of tile 0; K(3) and V(2) in flight
-  StepLoads Lm = plan_step(g, kv_head, 3 * kKeys, k3s, 2 * kKeys, v2s);
-  issue_k(Lm, sg);
-  issue_v(Lm, sg);
+  StepLoads Lm = plan_step<kCross>(g, kv_head, 3 * kKeys, k3s, 2 * kKeys, v2s);
+  issue_k<kCross>(Lm, sg);
+  issue_v<kCross>(Lm, sg);
   Pre pre;
 #pragma unroll
   for (int part = 0; part < 4; ++part) prefetch(pre, part, k0s, 0, s0s, 0, ln);
@@ -639,11 +683,12 @@ void k_attention_hm(Geometry g) {
     if (c >= 4 && c < 10) prefetch(next, c - 4, k0s, 1, s0s, 0, ln);
   });
   sub_step<1, true, false, true>(nullptr, s0s, 0, T, ln, half, magic, pre, [&](int c, Pre& next) {
-    if (c == 0) store_scales(s2s, sg, L2.ks, 2 * kKeys, g.tokens);
+    if (c == 0) store_stage_scales<kCross>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
     if (c == kBarrierChunk) step_barrier<kWaitPrevStep>();
     next_step_reads(c, next, k1s, s0s, ln);
   });
   float ks_held = Lm.ks;
+  uint32_t keep_held = Lm.keep;
 
   // Steady step j (stage j+1 exists), J = j % 4: sub-steps 2j and 2j+1 read K(j+1), V(j) and the
   // scales of tiles 2j+1 (stage j, block 1) and 2j+2 (stage j+1, block 0); the step stages K(j+4)
@@ -655,21 +700,24 @@ void k_attention_hm(Geometry g) {
   uint32_t j = 0;
   auto steady = [&](auto J_) {
     constexpr int J = decltype(J_)::value;
-    StepLoads L = plan_step(g, kv_head, (j + 4) * kKeys, kr(J), (j + 3) * kKeys, vr(J + 3));
+    StepLoads L = plan_step<kCross>(g, kv_head, (j + 4) * kKeys, kr(J), (j + 3) * kKeys, vr(J + 3));
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
     sub_step<0, true, true, true>(vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
-      if (c == 0) store_scales(sr(J + 3), sg, ks_held, (j + 3) * kKeys, g.tokens);
-      if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep) issue_load(L, sg, c / kLoadGap);
+      if (c == 0)
+        store_stage_scales<kCross>(sr(J + 3), sg, ks_held, keep_held, (j + 3) * kKeys, g.tokens);
+      if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep)
+        issue_load<kCross>(L, sg, c / kLoadGap);
       if (c >= 4 && c < 10) prefetch(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
     });
     sub_step<1, true, true, true>(vr(J), sr(J + 1), 0, T, ln, half, magic, pre,
                                   [&](int c, Pre& next) {
       const int slot = (c + 12) / kLoadGap;
-      if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load(L, sg, slot);
+      if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
       if (c == kBarrierChunk) step_barrier<kWaitTwoSteps>();
       next_step_reads(c, next, kr(J + 2), sr(J + 1), ln);
     });
     ks_held = L.ks;
+    keep_held = L.keep;
     ++j;
   };
   const uint32_t n_steady = n_stages - 1;  // steps j with stage j+1
@@ -733,7 +781,36 @@ hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count
   g.head_limit = cfg.out_stride / 128;
   g.total = g.q_blocks * heads;
   g.per_xcd = (g.total + 7) / 8;
-  hipLaunchKernelGGL(k_attention_hm, dim3(g.per_xcd * 8), dim3(kThreads), 0, stream, g);
+  hipLaunchKernelGGL(k_attention_hm<false>, dim3(g.per_xcd * 8), dim3(kThreads), 0, stream, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_hm_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
+                                     const int32_t* ki, const float* ks, const uint16_t* vt,
+                                     const uint8_t* key_mask, uint16_t* out, hipStream_t stream) {
+  Geometry g{};
+  g.qi = qi;
+  g.qs = qs;
+  g.ki = ki;
+  g.ks = ks;
+  g.vt = vt;
+  g.out = out;
+  g.tokens = cfg.kv_tokens;
+  g.rows = cfg.q_tokens;
+  g.capacity = cfg.kv_capacity;
+  g.out_stride = cfg.out_stride;
+  g.key_mask = key_mask;
+  g.q_tokens = cfg.q_tokens;
+  g.q_capacity = cfg.q_capacity;
+  g.kv_group = cfg.q_heads / cfg.kv_heads;
+  g.waves_per_head = kWaves / g.kv_group;
+  const uint32_t per_block = g.waves_per_head * kTileQ;  // queries of each head per block
+  g.q_blocks = (cfg.q_tokens + per_block - 1) / per_block;
+  g.kv_head_limit = cfg.kv_heads;
+  g.head_limit = cfg.q_heads;
+  g.total = g.q_blocks * cfg.kv_heads;
+  g.per_xcd = (g.total + 7) / 8;
+  hipLaunchKernelGGL(k_attention_hm<true>, dim3(g.per_xcd * 8), dim3(kThreads), 0, stream, g);
   return hipGetLastError();
 }
 

@@ -80,12 +80,17 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream);
-// attention_i8qkhm: the head-major INT8 kernel of attention_hm.hip (one wave per SIMD, two query
-// tiles per wave). Shapes are validated by the caller.
+// attention_i8qkhm: the head-major INT8 kernel of attention_hm.hip (eight waves of 32 queries,
+// two per SIMD). Shapes are validated by the caller.
 hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count, uint32_t heads,
                                const int32_t* qi, const float* qs, const int32_t* ki,
                                const float* ks, const uint16_t* vt, uint16_t* out,
                                hipStream_t stream);
+// The same kernel as cross-attention with a key mask and grouped heads; q_heads / kv_heads must
+// divide 8 (each workgroup holds all query heads of one key/value head).
+hipError_t launch_attention_hm_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
+                                     const int32_t* ki, const float* ks, const uint16_t* vt,
+                                     const uint8_t* key_mask, uint16_t* out, hipStream_t stream);
 // Bytes of the head-major key-scale copy the token-major attention kernels read when a caller
 // lends a workspace: (kv_stride / 128) * tokens f32.
 size_t scales_workspace_bytes(const h3_attention_cfg& cfg);
