@@ -100,7 +100,17 @@ def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
                                                                 ks, vt, out, ws), 2)
     skip_tm_ms = time_launches(torch, lambda: H.attention_i4qks(sc, tokens, heads, qi, qs, ki, ks,
                                                                 vt, out), 2)
+    # the same token-major kernel on int8 codes (attention_i8qk, _ws form): what int4 costs over
+    # int8 in one kernel design
+    del qi, ki
+    qi8 = torch.zeros((cap, width // 4), dtype=torch.int32, device=dev)
+    ki8 = torch.zeros_like(qi8)
+    H.prepare_qk_i8(pq, tokens, fused, None, qi8, qs)
+    H.prepare_qk_i8(pk, tokens, fused, None, ki8, ks)
+    i8_ms = time_launches(torch, lambda: H.attention_i8qk_ws(ac, tokens, heads, qi8, qs, ki8, ks,
+                                                             vt, out, ws), 2)
     return {"prepare_qk_i4_x2_ms": round(prep_ms, 4),
+            "attention_i8qk_token_major_ws_ms": round(i8_ms, 3),
             "attention_i4qk_ms": round(att_ms, 3),
             "attention_i4qk_tops": round(ops / (att_ms * 1e-3) / 1e12, 1),
             "attention_i4qk_token_major_scales_ms": round(att_tm_ms, 3),

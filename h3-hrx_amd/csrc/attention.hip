@@ -380,8 +380,14 @@ __device__ __forceinline__ v4i widen_i4(uint32_t x0, uint32_t x1) {
                  (int)((x1 << 4) & 0xF0F0F0F0u), (int)(x1 & 0xF0F0F0F0u)};
   return r;
 }
-// K operands of MFMA chunks (bb, 2p) and (bb, 2p + 1) from an int4 stage (64-byte rows, chunks
-// swizzled by (row/4)%4; row 32bb + n, with (n/4)%4 = g).
+// The packed int4 codes of MFMA chunks (bb, 2p) (words x, y) and (bb, 2p + 1) (words z, w) from
+// an int4 stage (64-byte rows, chunks swizzled by (row/4)%4; row 32bb + n, with (n/4)%4 = g).
+__device__ __forceinline__ uint4 k_raw_i4(const char* kst, int n, int half, uint32_t g, int bb,
+                                          int p) {
+  return *reinterpret_cast<const uint4*>(kst + (32 * bb + n) * kI4RowBytes +
+                                         16 * ((2 * p + half) ^ g));
+}
+// K operands of MFMA chunks (bb, 2p) and (bb, 2p + 1) from an int4 stage, widened.
 __device__ __forceinline__ void k_pair_i4(const char* kst, int n, int half, uint32_t g, int bb,
                                           int p, v4i& even, v4i& odd) {
   const uint4 w = *reinterpret_cast<const uint4*>(kst + (32 * bb + n) * kI4RowBytes +
@@ -464,15 +470,17 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
   v16i s[2];
   v8h pb[4];
   v4i kop[8];
+  uint4 kraw[4];  // int4: the packed codes of MFMA chunks (bb, 2p) and (bb, 2p + 1), p = i / 2
   v8h vop[16];
   float4 k4[8], c4[8];
 
   // ---- phase A: QK(j+1) || probabilities of slots 0..15 (block 0)
   constexpr bool kI4 = isI4(kMode);
   if (do_qk) {
-    if constexpr (kI4) {  // chunks 0..3 now, 4..7 two MFMAs ahead of their use
-      k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 0, kop[0], kop[2]);
-      k_pair_i4(kst, n, half, (n >> 2) & 3, 1, 0, kop[1], kop[3]);
+    if constexpr (kI4) {  // codes of chunks 0..3 now, 4..7 two MFMAs ahead of their use; each
+                          // chunk is widened just before its MFMA (half the registers held)
+      kraw[0] = k_raw_i4(kst, n, half, (n >> 2) & 3, 0, 0);
+      kraw[1] = k_raw_i4(kst, n, half, (n >> 2) & 3, 1, 0);
     } else {
 #pragma unroll
       for (int w = 0; w < kPf; ++w)
@@ -484,8 +492,12 @@ __device__ __forceinline__ void step(const char* kst, const char* vst, const v4i
     const int bb = c & 1, dc = c >> 1;
     if constexpr (kI4) {
       if (do_qk && c == 2) {
-        k_pair_i4(kst, n, half, (n >> 2) & 3, 0, 1, kop[4], kop[6]);
-        k_pair_i4(kst, n, half, (n >> 2) & 3, 1, 1, kop[5], kop[7]);
+        kraw[2] = k_raw_i4(kst, n, half, (n >> 2) & 3, 0, 1);
+        kraw[3] = k_raw_i4(kst, n, half, (n >> 2) & 3, 1, 1);
+      }
+      if (do_qk) {
+        const uint4 w = kraw[(c >> 2) * 2 + (c & 1)];
+        kop[c] = (c >> 1) & 1 ? widen_i4(w.z, w.w) : widen_i4(w.x, w.y);
       }
     } else if (do_qk && c + kPf < 8) {
       const int w = c + kPf;
