@@ -1268,7 +1268,7 @@ void k_attention_cross(Args a) {
 }  // namespace
 
 // CUs of the current device (cached per device).
-static uint32_t device_cus() {
+uint32_t device_cus() {
   static std::atomic<int> cus[64] = {};  // per device, once known (host threads may race to fill)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

@@ -67,9 +67,18 @@ constexpr int kLoadsPerStep = kKLoads + kVLoads + 1;
 constexpr int kLoadGap = 6;                       // chunks between a step's staging loads
 // s_waitcnt fields (gfx9 layout): vmcnt <= the loads of one or two steps, expcnt untouched,
 // lgkmcnt 0; or vmcnt 0.
-constexpr int kWaitPrevStep = kLoadsPerStep | (7 << 4) | (0 << 8);
-constexpr int kWaitTwoSteps = (2 * kLoadsPerStep) | (7 << 4) | (0 << 8);
+// Memory loads a wave issues per step: the key scale, its K and V^T LDS-DMA loads, and with
+// cross-attention also the key's mask byte (a second load in the scale's slot).
+template <bool kCross>
+constexpr int kVmemPerStep = kLoadsPerStep + (kCross ? 1 : 0);
+template <bool kCross>
+constexpr int kWaitPrevStep = kVmemPerStep<kCross> | (7 << 4) | (0 << 8);
+template <bool kCross>
+constexpr int kWaitTwoSteps = (2 * kVmemPerStep<kCross>) | (7 << 4) | (0 << 8);
 constexpr int kWaitAll = 0 | (7 << 4) | (0 << 8);
+// LDS work only: vmcnt at its maximum (63: low bits 3:0 and high bits 15:14), lgkmcnt 0.
+constexpr int kWaitLds = 0xF | (7 << 4) | (0 << 8) | (3 << 14);
+static_assert(2 * kVmemPerStep<true> < 16, "the vmcnt field's low four bits hold the count");
 constexpr int kPf = 4;                            // V^T operands read this many chunks ahead
 constexpr int kKBias = 65536;                     // see Lanes
 constexpr int kBarrierChunk = 8;                  // chunk of a step's second sub-step with its barrier
@@ -80,6 +89,7 @@ constexpr float kSumLimit = 256.0f;               // a lane's tile sum above thi
 constexpr int kRsrcWord3 = 0x00020000;            // gfx9 raw buffer: 32-bit data, no swizzle
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
   return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
@@ -105,7 +115,8 @@ struct Geometry {
   uint32_t kv_head_limit;
   uint32_t head_limit;
   uint32_t total;        // q_blocks * heads (cross: * kv_heads)
-  uint32_t per_xcd;      // ceil(total / 8)
+  uint32_t per_xcd;      // ceil(total / 8): blocks per XCD
+  uint32_t wpx;          // persistent workgroups per XCD (at most per_xcd)
   // cross-attention only: keys with key_mask == 0 are dead; the kv_group query heads of a key /
   // value head share a workgroup, waves_per_head = 8 / kv_group waves each
   const uint8_t* key_mask;
@@ -449,8 +460,12 @@ __device__ __forceinline__ void raise_exact(Tile& T, int par, const float* kss, 
   const float m_new = fmaxf(m_old, tmax * T.qsl);
   const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);
   // The tile's PV MFMAs of this sub-step were issued before; the waits on both sides of the
-  // rescale cover them and the next MFMA that reads the accumulators.
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  // rescale cover them and the next MFMA that reads the accumulators. alpha is an input of the
+  // first wait, so it (a transcendental result, which a dependent instruction may read only after
+  // a wait state) is complete before the waits begin; the compiler does not see the rescale's
+  // inline-asm reads of it and would otherwise place the exponential right before them.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" :: "v"(alpha)
+               : "memory");
   scale_all(alpha, std::make_integer_sequence<int, 64>{});
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
   T.negm = -m_new;
@@ -612,31 +627,18 @@ void k_attention_hm(Geometry g) {
   auto vr = [&](int i) { return ring(i & 3, v0s, v1s, v2s, v3s); };
   auto sr = [&](int i) { return ring(i & 3, s0s, s1s, s2s, s3s); };
 
-  // XCD-aware remap: hardware hands block b to XCD b % 8; give each XCD a contiguous range of
-  // (head, query block) work so its resident blocks share one head's K/V^T stream in L2.
-  const uint32_t b = blockIdx.x;
-  const uint32_t logical = (b & 7u) * g.per_xcd + (b >> 3);
-  if (logical >= g.total) return;
+  // Persistent workgroups, XCD-aware: the hardware hands workgroup b to XCD b % 8, and each XCD
+  // owns a contiguous range of per_xcd (head, query block) blocks, which its wpx workgroups take
+  // in turn (workgroup i of the XCD: blocks i, i + wpx, i + 2 wpx, ...). At any moment the
+  // XCD's resident workgroups hold wpx consecutive blocks, which share one head's K/V^T stream
+  // through the XCD's L2, and a workgroup's next block is usually of the same key/value head.
+  const uint32_t xcd = blockIdx.x & 7u;
+  uint32_t local = blockIdx.x >> 3;
+  if (local >= g.per_xcd || xcd * g.per_xcd + local >= g.total) return;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
-  const uint32_t head_y = logical / g.q_blocks;
-  const uint32_t qb = logical % g.q_blocks;
-  uint32_t kv_head, head, q, q_limit, q_cap;
-  if (kCross) {  // block = (key/value head, query block); its kv_group query heads share it
-    kv_head = head_y;
-    head = kv_head * g.kv_group + (uint32_t)wave / g.waves_per_head;
-    q = (qb * g.waves_per_head + (uint32_t)wave % g.waves_per_head) * kTileQ + n;
-    q_limit = g.q_tokens;
-    q_cap = g.q_capacity;
-  } else {
-    kv_head = head_y % g.kv_head_limit;
-    head = kv_head % g.head_limit;
-    q = qb * kBlockQ + wave * kTileQ + n;
-    q_limit = g.tokens;
-    q_cap = g.capacity;
-  }
   const Stager sg = make_stager(g, wave, lane);
   const Lanes ln = make_lanes(n, half);
   // The QK bias 1.5*2^23, made opaque so that it stays in registers for the whole loop.
@@ -645,34 +647,93 @@ void k_attention_hm(Geometry g) {
   for (int r = 0; r < 16; ++r) magic[r] = kMagicBits;
   asm volatile("" : "+v"(magic));
   const uint32_t n_stages = (g.tokens + kKeys - 1) / kKeys;  // 64-key stages; 32-key tiles 2x
-
-  // ---- prologue: K and scales of stages 0..2, V^T of stages 0 and 1 in flight
-  StepLoads L0 = plan_step<kCross>(g, kv_head, 0, k0s, 0, v0s);
-  issue_k<kCross>(L0, sg);
-  issue_v<kCross>(L0, sg);
-  StepLoads L1 = plan_step<kCross>(g, kv_head, kKeys, k1s, kKeys, v1s);
-  issue_k<kCross>(L1, sg);
-  issue_v<kCross>(L1, sg);
-  StepLoads L2 = plan_step<kCross>(g, kv_head, 2 * kKeys, k2s, 0, nullptr);
-  issue_k<kCross>(L2, sg);
-
-  Tile T;
-  {
-    const uint32_t q_read = q < q_limit ? q : q_limit - 1;
-    const int32_t* src = g.qi + ((size_t)head * q_cap + q_read) * 32;
+  // Chaining: when the next block reads the same K/V^T stream and the stage count is a multiple
+  // of the ring length, this block's last steady steps stage the next block's first stages
+  // (K 0-2, V^T 0-1 and their scales) into the ring slots they would have had anyway, so the
+  // next block starts without a prologue.
+  const bool chain_ok = n_stages % 4 == 0;
+  auto kv_head_of = [&](uint32_t logical) {
+    const uint32_t head_y = logical / g.q_blocks;
+    return kCross ? head_y : head_y % g.kv_head_limit;
+  };
+  // This wave's part of block `logical`: key/value head, query head, first query row of its tile.
+  struct WaveBlock {
+    uint32_t kv_head, head, q0;
+  };
+  auto wave_block = [&](uint32_t logical) {
+    const uint32_t head_y = logical / g.q_blocks;
+    const uint32_t qb = logical % g.q_blocks;
+    WaveBlock w;
+    if (kCross) {  // block = (key/value head, query block); its kv_group query heads share it
+      w.kv_head = head_y;
+      w.head = w.kv_head * g.kv_group + (uint32_t)wave / g.waves_per_head;
+      w.q0 = (qb * g.waves_per_head + (uint32_t)wave % g.waves_per_head) * kTileQ;
+    } else {
+      w.kv_head = head_y % g.kv_head_limit;
+      w.head = w.kv_head % g.head_limit;
+      w.q0 = qb * kBlockQ + wave * kTileQ;
+    }
+    return w;
+  };
+  const uint32_t q_limit = kCross ? g.q_tokens : g.tokens;  // readable query rows
+  const uint32_t q_cap = kCross ? g.q_capacity : g.capacity;
+  // The Q^T operand and scale of this lane's query in block `w`.
+  auto load_q = [&](Tile& T, const WaveBlock& w) {
+    const uint32_t qq = w.q0 + n;
+    const uint32_t q_read = qq < q_limit ? qq : q_limit - 1;
+    const int32_t* src = g.qi + ((size_t)w.head * q_cap + q_read) * 32;
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
-    T.qsl = g.qs[(size_t)head * q_cap + q_read] * kLog2e;
-    T.negm = 1.0e30f;
-    T.l = 0.0f;
+    T.qsl = g.qs[(size_t)w.head * q_cap + q_read] * kLog2e;
+  };
+
+  bool chained = false;  // this block's first stages were staged by the previous block
+  bool have_q = false;   // this block's Q was loaded by the previous block
+  float ks_carry = 0.0f;
+  uint32_t keep_carry = 0;
+  Tile T;
+
+  for (;;) {
+  const uint32_t logical = xcd * g.per_xcd + local;
+  const uint32_t next_local = local + g.wpx;
+  const bool has_next = next_local < g.per_xcd && xcd * g.per_xcd + next_local < g.total;
+  const WaveBlock wb = wave_block(logical);
+  const uint32_t kv_head = wb.kv_head, head = wb.head, q = wb.q0 + n;
+  const bool wrap = chain_ok && has_next && kv_head_of(xcd * g.per_xcd + next_local) == kv_head;
+  // stage index of a load: past the last stage it is the next block's (chained) or out of range
+  auto stage_of = [&](uint32_t st) { return wrap && st >= n_stages ? st - n_stages : st; };
+
+  // ---- prologue: K and scales of stages 0..2, V^T of stages 0 and 1 in flight (unless chained)
+  StepLoads L0 = plan_step<kCross>(g, kv_head, 0, k0s, 0, v0s);
+  StepLoads L1 = plan_step<kCross>(g, kv_head, kKeys, k1s, kKeys, v1s);
+  StepLoads L2 = plan_step<kCross>(g, kv_head, 2 * kKeys, k2s, 0, nullptr);
+  if (!chained) {
+    issue_k<kCross>(L0, sg);
+    issue_v<kCross>(L0, sg);
+    issue_k<kCross>(L1, sg);
+    issue_v<kCross>(L1, sg);
+    issue_k<kCross>(L2, sg);
+  } else {
+    L2.ks = ks_carry;
+    L2.keep = keep_carry;
   }
+
+  if (!have_q) load_q(T, wb);
+  T.negm = 1.0e30f;
+  T.l = 0.0f;
   zero_all(std::make_integer_sequence<int, 64>{});
-  store_stage_scales<kCross>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
-  store_stage_scales<kCross>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
-  step_barrier<kWaitAll>();
+  if (!chained) {
+    store_stage_scales<kCross>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
+    store_stage_scales<kCross>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
+    step_barrier<kWaitAll>();
+  } else {
+    // The first stages landed before the previous block's last barrier; the previous block's
+    // output stores stay in flight (only LDS work is waited for).
+    step_barrier<kWaitLds>();
+  }
 
   // ---- step -1: QK of key tiles 0 and 1, the probabilities of tile 0; K(3) and V(2) in flight
-  StepLoads Lm = plan_step<kCross>(g, kv_head, 3 * kKeys, k3s, 2 * kKeys, v2s);
+  StepLoads Lm = plan_step<kCross>(g, kv_head, stage_of(3) * kKeys, k3s, 2 * kKeys, v2s);
   issue_k<kCross>(Lm, sg);
   issue_v<kCross>(Lm, sg);
   Pre pre;
@@ -684,7 +745,7 @@ void k_attention_hm(Geometry g) {
   });
   sub_step<1, true, false, true>(nullptr, s0s, 0, T, ln, half, magic, pre, [&](int c, Pre& next) {
     if (c == 0) store_stage_scales<kCross>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
-    if (c == kBarrierChunk) step_barrier<kWaitPrevStep>();
+    if (c == kBarrierChunk) step_barrier<kWaitPrevStep<kCross>>();
     next_step_reads(c, next, k1s, s0s, ln);
   });
   float ks_held = Lm.ks;
@@ -696,15 +757,18 @@ void k_attention_hm(Geometry g) {
   // scales of stage j+3 (loaded one step earlier) into S(j-1)'s. Every load has three steps to
   // land. The step's barrier comes once its last read of K(j+1) and V(j) is issued (chunk
   // kBarrierChunk of its second sub-step), after a wait for this wave's loads of two steps
-  // before; the reads for the next step's first sub-step follow it.
+  // before; the reads for the next step's first sub-step follow it. Stages past the last are the
+  // next block's first ones when the blocks chain.
   uint32_t j = 0;
   auto steady = [&](auto J_) {
     constexpr int J = decltype(J_)::value;
-    StepLoads L = plan_step<kCross>(g, kv_head, (j + 4) * kKeys, kr(J), (j + 3) * kKeys, vr(J + 3));
+    StepLoads L = plan_step<kCross>(g, kv_head, stage_of(j + 4) * kKeys, kr(J),
+                                    stage_of(j + 3) * kKeys, vr(J + 3));
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
     sub_step<0, true, true, true>(vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
       if (c == 0)
-        store_stage_scales<kCross>(sr(J + 3), sg, ks_held, keep_held, (j + 3) * kKeys, g.tokens);
+        store_stage_scales<kCross>(sr(J + 3), sg, ks_held, keep_held, stage_of(j + 3) * kKeys,
+                                   g.tokens);
       if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep)
         issue_load<kCross>(L, sg, c / kLoadGap);
       if (c >= 4 && c < 10) prefetch(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
@@ -713,7 +777,7 @@ void k_attention_hm(Geometry g) {
                                   [&](int c, Pre& next) {
       const int slot = (c + 12) / kLoadGap;
       if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
-      if (c == kBarrierChunk) step_barrier<kWaitTwoSteps>();
+      if (c == kBarrierChunk) step_barrier<kWaitTwoSteps<kCross>>();
       next_step_reads(c, next, kr(J + 2), sr(J + 1), ln);
     });
     ks_held = L.ks;
@@ -736,16 +800,26 @@ void k_attention_hm(Geometry g) {
   // (its scales came in `pre`; its K reads there are unused)
   sub_step<0, false, true, true>(vr(j), sr(j), 1, T, ln, half, magic, pre, [](int, Pre&) {});
   sub_step<1, false, true, false>(vr(j), nullptr, 0, T, ln, half, magic, pre, [](int, Pre&) {});
-  step_barrier<kWaitAll>();  // no staging load outlives the workgroup
+  step_barrier<kWaitAll>();  // no staging load outlives the block (chained ones have landed)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // the last PV MFMAs have landed
 
-  // ---- normalise and store rows < min(token_count, tokens)
-  float o[64];
-  read_all(o, std::make_integer_sequence<int, 64>{});
-  const float l_tot = T.l + __shfl_xor(T.l, 32);
-  const float inv = 1.0f / l_tot;
-  if (q < g.rows) {
-    uint16_t* dst = g.out + (size_t)q * g.out_stride + head * 128;
+  // The next block's Q, loaded now (this block's QK is done) so that it lands during the
+  // epilogue and ahead of the stores below.
+  const float l_here = T.l;
+  if (has_next) load_q(T, wave_block(xcd * g.per_xcd + next_local));
+
+  // ---- normalise and store rows < min(token_count, tokens): every lane stores through a buffer
+  // descriptor that ends at the last valid row of the wave's tile (the hardware drops stores past
+  // it), so the stores are the same instructions for every wave and nothing waits for them
+  {
+    float o[64];
+    read_all(o, std::make_integer_sequence<int, 64>{});
+    const float l_tot = l_here + __shfl_xor(l_here, 32);
+    const float inv = 1.0f / l_tot;
+    const uint32_t live = g.rows > wb.q0 ? min(g.rows - wb.q0, (uint32_t)kTileQ) : 0u;
+    const __amdgpu_buffer_rsrc_t ro =
+        rsrc(g.out + (size_t)wb.q0 * g.out_stride, live * g.out_stride * 2);
+    const uint32_t row_off = (n * g.out_stride + head * 128 + 4 * half) * 2;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -753,9 +827,17 @@ void k_attention_hm(Geometry g) {
         const float* r = o + 16 * db + 4 * i;
         v4h h = {(_Float16)(r[0] * inv), (_Float16)(r[1] * inv), (_Float16)(r[2] * inv),
                  (_Float16)(r[3] * inv)};
-        *reinterpret_cast<v4h*>(dst + 32 * db + 8 * i + 4 * half) = h;
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, h), ro,
+                                              row_off + (32 * db + 8 * i) * 2, 0, 0);
       }
     }
+  }
+  if (!has_next) break;
+  have_q = true;
+  chained = wrap;
+  ks_carry = ks_held;
+  keep_carry = keep_held;
+  local = next_local;
   }
 }
 
@@ -781,7 +863,8 @@ hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count
   g.head_limit = cfg.out_stride / 128;
   g.total = g.q_blocks * heads;
   g.per_xcd = (g.total + 7) / 8;
-  hipLaunchKernelGGL(k_attention_hm<false>, dim3(g.per_xcd * 8), dim3(kThreads), 0, stream, g);
+  g.wpx = std::min(g.per_xcd, std::max(1u, device_cus() / 8));  // one workgroup per CU
+  hipLaunchKernelGGL(k_attention_hm<false>, dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
   return hipGetLastError();
 }
 
@@ -810,7 +893,8 @@ hipError_t launch_attention_hm_cross(const h3_cross_cfg& cfg, const int32_t* qi,
   g.head_limit = cfg.q_heads;
   g.total = g.q_blocks * cfg.kv_heads;
   g.per_xcd = (g.total + 7) / 8;
-  hipLaunchKernelGGL(k_attention_hm<true>, dim3(g.per_xcd * 8), dim3(kThreads), 0, stream, g);
+  g.wpx = std::min(g.per_xcd, std::max(1u, device_cus() / 8));  // one workgroup per CU
+  hipLaunchKernelGGL(k_attention_hm<true>, dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
   return hipGetLastError();
 }
 

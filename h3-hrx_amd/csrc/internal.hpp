@@ -80,6 +80,8 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream);
+// Compute units of the current device (cached per device; 256 if the query fails).
+uint32_t device_cus();
 // attention_i8qkhm: the head-major INT8 kernel of attention_hm.hip (eight waves of 32 queries,
 // two per SIMD). Shapes are validated by the caller.
 hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count, uint32_t heads,
