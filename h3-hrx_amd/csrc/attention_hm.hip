@@ -78,10 +78,13 @@ constexpr int kWaitTwoSteps = (2 * kVmemPerStep<kCross>) | (7 << 4) | (0 << 8);
 constexpr int kWaitAll = 0 | (7 << 4) | (0 << 8);
 // LDS work only: vmcnt at its maximum (63: low bits 3:0 and high bits 15:14), lgkmcnt 0.
 constexpr int kWaitLds = 0xF | (7 << 4) | (0 << 8) | (3 << 14);
+constexpr int kWaitLdsWrites = kWaitLds;  // the same wait, named for its use in the epilogue
 static_assert(2 * kVmemPerStep<true> < 16, "the vmcnt field's low four bits hold the count");
 constexpr int kPf = 4;                            // V^T operands read this many chunks ahead
 constexpr int kKBias = 65536;                     // see Lanes
-constexpr int kBarrierChunk = 8;                  // chunk of a step's second sub-step with its barrier
+constexpr int kBarrierChunk = 8;
+constexpr int kOStage = kTileQ * 64 * 2;          // 4 KiB: 32 output rows x 64 channels of f16
+static_assert(4 * kOStage == kVStage, "four waves' output stages fill one V^T stage");                  // chunk of a step's second sub-step with its barrier
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMagic = 12582912.0f;             // 1.5 * 2^23, the QK accumulators' bias
 constexpr int kMagicBits = 0x4B400000;            // its bit pattern
@@ -89,7 +92,7 @@ constexpr float kSumLimit = 256.0f;               // a lane's tile sum above thi
 constexpr int kRsrcWord3 = 0x00020000;            // gfx9 raw buffer: 32-bit data, no swizzle
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
   return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
@@ -614,7 +617,7 @@ __device__ __forceinline__ char* ring(int i, char* a0, char* a1, char* a2, char*
   return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : a3;
 }
 
-template <bool kCross>
+template <bool kCross, bool kChain>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2), amdgpu_num_vgpr(kOReg)))
 void k_attention_hm(Geometry g) {
@@ -651,7 +654,7 @@ void k_attention_hm(Geometry g) {
   // of the ring length, this block's last steady steps stage the next block's first stages
   // (K 0-2, V^T 0-1 and their scales) into the ring slots they would have had anyway, so the
   // next block starts without a prologue.
-  const bool chain_ok = n_stages % 4 == 0;
+  const bool chain_ok = kChain && n_stages % 4 == 0;
   auto kv_head_of = [&](uint32_t logical) {
     const uint32_t head_y = logical / g.q_blocks;
     return kCross ? head_y : head_y % g.kv_head_limit;
@@ -696,9 +699,10 @@ void k_attention_hm(Geometry g) {
   for (;;) {
   const uint32_t logical = xcd * g.per_xcd + local;
   const uint32_t next_local = local + g.wpx;
-  const bool has_next = next_local < g.per_xcd && xcd * g.per_xcd + next_local < g.total;
+  const bool has_next =
+      kChain && next_local < g.per_xcd && xcd * g.per_xcd + next_local < g.total;
   const WaveBlock wb = wave_block(logical);
-  const uint32_t kv_head = wb.kv_head, head = wb.head, q = wb.q0 + n;
+  const uint32_t kv_head = wb.kv_head, head = wb.head;
   const bool wrap = chain_ok && has_next && kv_head_of(xcd * g.per_xcd + next_local) == kv_head;
   // stage index of a load: past the last stage it is the next block's (chained) or out of range
   auto stage_of = [&](uint32_t st) { return wrap && st >= n_stages ? st - n_stages : st; };
@@ -808,9 +812,12 @@ void k_attention_hm(Geometry g) {
   const float l_here = T.l;
   if (has_next) load_q(T, wave_block(xcd * g.per_xcd + next_local));
 
-  // ---- normalise and store rows < min(token_count, tokens): every lane stores through a buffer
+  // ---- normalise and store rows < min(token_count, tokens). O^T gives each lane one query and
+  // 8-byte pieces of its channels, so the rows are first transposed through the wave's LDS stage
+  // (64 channels at a time, 16-byte chunks XOR-swizzled by row % 8): each store then writes 128
+  // contiguous bytes of eight rows instead of 16 bytes of 32 rows. The stores go through a buffer
   // descriptor that ends at the last valid row of the wave's tile (the hardware drops stores past
-  // it), so the stores are the same instructions for every wave and nothing waits for them
+  // it), so they are the same instructions for every wave and nothing waits for them.
   {
     float o[64];
     read_all(o, std::make_integer_sequence<int, 64>{});
@@ -819,17 +826,35 @@ void k_attention_hm(Geometry g) {
     const uint32_t live = g.rows > wb.q0 ? min(g.rows - wb.q0, (uint32_t)kTileQ) : 0u;
     const __amdgpu_buffer_rsrc_t ro =
         rsrc(g.out + (size_t)wb.q0 * g.out_stride, live * g.out_stride * 2);
-    const uint32_t row_off = (n * g.out_stride + head * 128 + 4 * half) * 2;
+    // The stage: a quarter of V^T stage 2 or 3. Neither holds anything live between the last
+    // step's barrier (after which no wave reads them) and the next block's first barrier (before
+    // which nothing is staged into them; a chained block's early stages are K 0-2 and V^T 0-1).
+    char* ow = (wave < 4 ? v2s : v3s) + (wave & 3) * kOStage;
+    const uint32_t sr = lane >> 3, sj = lane & 7;  // store: rows 8k + sr, chunk sj
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float* r = o + 16 * db + 4 * i;
-        v4h h = {(_Float16)(r[0] * inv), (_Float16)(r[1] * inv), (_Float16)(r[2] * inv),
-                 (_Float16)(r[3] * inv)};
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, h), ro,
-                                              row_off + (32 * db + 8 * i) * 2, 0, 0);
+      for (int dbl = 0; dbl < 2; ++dbl) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float* r = o + 16 * (2 * pass + dbl) + 4 * i;
+          const v4h h = {(_Float16)(r[0] * inv), (_Float16)(r[1] * inv), (_Float16)(r[2] * inv),
+                         (_Float16)(r[3] * inv)};
+          const int chunk = 4 * dbl + i;  // channel 64 pass + 8 chunk + 4 half
+          *reinterpret_cast<v4h*>(ow + n * 128 + 16 * (chunk ^ (n & 7)) + 8 * half) = h;
+        }
       }
+      __builtin_amdgcn_s_waitcnt(kWaitLdsWrites);  // this wave's pieces are in the stage
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t row = 8 * k + sr;
+        const v4u v = *reinterpret_cast<const v4u*>(ow + row * 128 + 16 * (sj ^ (row & 7)));
+        __builtin_amdgcn_raw_buffer_store_b128(
+            v, ro, (row * g.out_stride + head * 128 + 64 * pass + 8 * sj) * 2, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitLdsWrites);  // the stage is read before it is rewritten
+      __builtin_amdgcn_wave_barrier();
     }
   }
   if (!has_next) break;
@@ -839,6 +864,21 @@ void k_attention_hm(Geometry g) {
   keep_carry = keep_held;
   local = next_local;
   }
+}
+
+// Short key sequences (at most kPersistMaxStages 64-key stages) run one persistent workgroup per
+// CU that chains its blocks, since their per-block fill and drain is a large share of a block;
+// long ones run one workgroup per block (the loop compiled out), so that the hardware's dispatch
+// hands blocks to whichever CU is free. At 129,024 keys the chaining build was 5-6 % slower, from
+// a static split of the blocks over CUs that run at different speeds and from the extra
+// per-step work of the stage wrap.
+constexpr uint32_t kPersistMaxStages = 64;
+bool chain_blocks(const Geometry& g) {
+  return (g.tokens + kKeys - 1) / kKeys <= kPersistMaxStages;
+}
+uint32_t workgroups_per_xcd(const Geometry& g) {
+  if (!chain_blocks(g)) return g.per_xcd;
+  return std::min(g.per_xcd, std::max(1u, device_cus() / 8));  // one workgroup per CU
 }
 
 }  // namespace
@@ -863,8 +903,11 @@ hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count
   g.head_limit = cfg.out_stride / 128;
   g.total = g.q_blocks * heads;
   g.per_xcd = (g.total + 7) / 8;
-  g.wpx = std::min(g.per_xcd, std::max(1u, device_cus() / 8));  // one workgroup per CU
-  hipLaunchKernelGGL(k_attention_hm<false>, dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
+  g.wpx = workgroups_per_xcd(g);
+  if (chain_blocks(g))
+    hipLaunchKernelGGL((k_attention_hm<false, true>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
+  else
+    hipLaunchKernelGGL((k_attention_hm<false, false>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
   return hipGetLastError();
 }
 
@@ -893,8 +936,11 @@ hipError_t launch_attention_hm_cross(const h3_cross_cfg& cfg, const int32_t* qi,
   g.head_limit = cfg.q_heads;
   g.total = g.q_blocks * cfg.kv_heads;
   g.per_xcd = (g.total + 7) / 8;
-  g.wpx = std::min(g.per_xcd, std::max(1u, device_cus() / 8));  // one workgroup per CU
-  hipLaunchKernelGGL(k_attention_hm<true>, dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
+  g.wpx = workgroups_per_xcd(g);
+  if (chain_blocks(g))
+    hipLaunchKernelGGL((k_attention_hm<true, true>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
+  else
+    hipLaunchKernelGGL((k_attention_hm<true, false>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
   return hipGetLastError();
 }
 
