@@ -27,6 +27,7 @@ sys.path.insert(0, str(ROOT / "h3-hrx_amd"))
 
 METRIC = "INT8 attn TOPS + ms/call at S=129k,H=32,D=128; % of gfx950 int8 MFMA peak"
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s (at the 2.4 GHz spec clock)
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA, TFLOP/s (at the 2.4 GHz spec clock)
 BOX_CPU_SHARE = 16       # host threads a one-GPU box grants a job
 WORKLOADS = {
     # name: (tokens, heads, rope grid (t, h, w))
@@ -292,6 +293,15 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
     useful = float(((r @ ln) * ln).sum().item())             # live (query, key) pairs kept
     executed = float(r.sum().item()) * 64 * 64               # pairs the MFMAs run (whole cubes)
     ops_dense = 4.0 * tokens * tokens * heads * 128
+    # The f16 form (Runtime::new with bits 16, kernels/vsa_attention_16.loom): the same plan and
+    # inputs, the sparse attention on the gathered f16 q, k, v.
+    vsa16 = H.Vsa(src, inverse, lengths, prefix, heads, bits=16)
+    run16_ms = time_launches(torch, lambda: vsa16.attend(0, q, k, v, out), 3)
+    b16 = vsa16.buffers(0)
+    att16_ms = time_launches(torch, lambda: H.vsa_attention_f16(
+        b16.attention, b16.attention.tokens, heads, b16.q, b16.k, b16.v, b16.out, b16.routes,
+        b16.lengths), 3)
+    vsa16.close()
     res = {
         "workload": f"config 5b shape: S={tokens} H={heads}, grid {nt}x{nh}x{nw} in {nb} cubes, "
                     "keep 10% + diagonal +-1 (reference defaults), int8 QK, f16 PV, synthetic "
@@ -307,6 +317,11 @@ def vsa_path(torch, H, dev, tokens, heads, grid, fused, dense_ms):
                                          / PEAK_INT8_TOPS, 4),
         "dense_equivalent_tops": round(ops_dense / (run_ms * 1e-3) / 1e12, 1),
         "speedup_vs_dense_attention": round(dense_ms / run_ms, 2),
+        "f16_runtime_ms": round(run16_ms, 3),
+        "f16_sparse_attention_ms": round(att16_ms, 3),
+        "f16_executed_tflops": round(4.0 * 128 * executed / (att16_ms * 1e-3) / 1e12, 1),
+        "f16_executed_frac_f16_peak": round(4.0 * 128 * executed / (att16_ms * 1e-3) / 1e12
+                                            / PEAK_F16_TFLOPS, 4),
     }
     vsa.close()
     return res

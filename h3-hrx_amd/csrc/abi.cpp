@@ -165,13 +165,10 @@ int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
 // Operand layouts of the attention kernels (attention.hip's modes).
 enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2, kModeTokenI4Skip = 3, kModeTokenI8Vsa = 4 };
 
-int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
-                     uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
-                     h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f,
-                     h3_view routes = {}, h3_view lengths = {}, h3_view workspace = {}) {
-  const bool head_major = mode == kModeHeadI8;
-  const bool vsa = mode == kModeTokenI8Vsa;
-  const size_t code_div = (mode == kModeTokenI4 || mode == kModeTokenI4Skip) ? 2 : 1;
+// The attention config (kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17 and the same
+// declarations in vsa_attention_16.loom) and the launch arguments every attention form shares.
+int check_attention_cfg(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
+                        uint32_t heads) {
   if (!cfg) return set_error(H3_ERR_ARGUMENT, "%s: null config", stage);
   // kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17
   if (!in_range(cfg->q_stride, 128, 32768, 128))
@@ -196,11 +193,24 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
                 cfg->tokens);
   if (heads < 1 || heads > 65535)
     return set_error(H3_ERR_ARGUMENT, "%s: heads %u outside [1, 65535]", stage, heads);
-  const size_t cap = cfg->token_capacity;
-  const size_t head_limit = cfg->out_stride / 128, kv_head_limit = cfg->kv_stride / 128;
+  const size_t head_limit = cfg->out_stride / 128;
   if (cfg->q_stride / 128 < head_limit)
     return set_error(H3_ERR_CONFIG, "%s: q_stride %u holds fewer heads than out_stride %u", stage,
                 cfg->q_stride, cfg->out_stride);
+  return H3_OK;
+}
+
+int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
+                     uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                     h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f,
+                     h3_view routes = {}, h3_view lengths = {}, h3_view workspace = {}) {
+  const bool head_major = mode == kModeHeadI8;
+  const bool vsa = mode == kModeTokenI8Vsa;
+  const size_t code_div = (mode == kModeTokenI4 || mode == kModeTokenI4Skip) ? 2 : 1;
+  int st = check_attention_cfg(stage, cfg, token_count, heads);
+  if (st) return st;
+  const size_t cap = cfg->token_capacity;
+  const size_t head_limit = cfg->out_stride / 128, kv_head_limit = cfg->kv_stride / 128;
   // The extents the kernel addresses: head-major views [head_limit*cap][32] i32 and
   // [head_limit][cap] f32 (attention_i8qkhm...loom:394-401); token-major views
   // [cap][q_stride/4] i32 and [cap][head_limit] f32 (attention_i8qk_family.loom:117-121).
@@ -219,7 +229,7 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   need[4] = (size_t)cfg->kv_stride * cap * 2;
   need[5] = (size_t)token_count * cfg->out_stride * 2;
   h3_view views[6] = {qi, qs, ki, ks, vt, out};
-  int st = check_bindings(stage, views, need, 6);
+  st = check_bindings(stage, views, need, 6);
   if (st) return st;
   // A workspace (token-major operands) receives a head-major copy of the key scales, which the
   // kernel then reads; without one it reads them token-major. Nothing is allocated either way.
@@ -812,6 +822,38 @@ int h3_vsa_attention_i8(const h3_attention_cfg* cfg, uint32_t token_count, uint3
   return attention_common("VSA attention", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI8Vsa, 0.0f, routes,
                           lengths);
+}
+
+int h3_vsa_attention_f16(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                         h3_view q, h3_view k, h3_view v, h3_view out, h3_view routes,
+                         h3_view lengths, h3_stream stream) {
+  const char* stage = "VSA attention f16";
+  int st = check_attention_cfg(stage, cfg, token_count, heads);
+  if (st) return st;
+  // kernels/vsa_attention_16.loom:113-123, 584-587: blocks = tokens / 64 query cubes, routes
+  // [out_stride/128][blocks][blocks] i32, lengths [blocks] i32; q [token_capacity][q_stride],
+  // k and v [token_capacity][kv_stride], out [token_count][out_stride], all f16.
+  if (cfg->tokens % 64 != 0 || cfg->tokens / 64 > 16384)
+    return set_error(H3_ERR_CONFIG, "%s: tokens %u is not 64 * blocks with blocks <= 16384",
+                     stage, cfg->tokens);
+  const size_t cap = cfg->token_capacity, blocks = cfg->tokens / 64;
+  const size_t head_limit = cfg->out_stride / 128;
+  h3_view views[6] = {q, k, v, out, routes, lengths};
+  size_t need[6] = {cap * cfg->q_stride * 2,
+                    cap * cfg->kv_stride * 2,
+                    cap * cfg->kv_stride * 2,
+                    (size_t)token_count * cfg->out_stride * 2,
+                    head_limit * blocks * blocks * 4,
+                    blocks * 4};
+  if ((st = check_bindings(stage, views, need, 6))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_attention_vsa_f16(
+                             *cfg, token_count, heads, static_cast<const uint16_t*>(q.ptr),
+                             static_cast<const uint16_t*>(k.ptr),
+                             static_cast<const uint16_t*>(v.ptr), static_cast<uint16_t*>(out.ptr),
+                             static_cast<const int32_t*>(routes.ptr),
+                             static_cast<const int32_t*>(lengths.ptr),
+                             reinterpret_cast<hipStream_t>(stream)));
 }
 
 int h3_vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,

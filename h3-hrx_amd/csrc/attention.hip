@@ -50,6 +50,7 @@
 #include <algorithm>
 
 #include <atomic>
+#include <type_traits>
 
 #include "internal.hpp"
 
@@ -127,6 +128,7 @@ struct Args {
   const int32_t* lengths;  // k_attention_vsa: live keys of each 64-key cube
   uint32_t blocks;         // k_attention_vsa: tokens / 64
   uint32_t base;           // k_attention_vsa: first (head, cube) item of this launch
+  float scale;             // k_attention_vsa<·, true>: the score scale of the f16 operands
 };
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
@@ -740,14 +742,30 @@ constexpr int kVsaVLoads = kVsaVStage / 1024 / kVsaWaves; // 4
 constexpr int kVsaSRows = kVsaKeys / kVsaWaves;           // scale rows stored per wave: 16
 constexpr int kVsaWaitPrevStep = (kVsaKLoads + kVsaVLoads + 1) | (7 << 4) | (0 << 8);
 constexpr int kVsaListMax = 512;                          // list entries per run of the key loop
+// The f16 form (kernels/vsa_attention_16.loom): K and V token-major f16, [tokens][kv_stride].
+// A K stage holds 32 rows of 256 bytes (one head's 128 channels) and the keys' masks c (0 for a
+// live key, -inf for a dead one); a V stage holds the 32 keys' rows of V as they lie in memory,
+// and the PV operand is read from it with the LDS transposed read (ds_read_b64_tr_b16).
+constexpr int kVsaF16RowBytes = 256;
+constexpr int kVsaF16KRows = kVsaKeys * kVsaF16RowBytes;          // 8192
+constexpr int kVsaF16KStage = kVsaF16KRows + kVsaKeys * 4;        // + c[32]: 8320
+constexpr int kVsaF16VStage = kVsaKeys * kVsaF16RowBytes;         // 8192
+constexpr int kVsaF16KLoads = kVsaF16KRows / 1024 / kVsaWaves;    // 4
+constexpr int kVsaF16VLoads = kVsaF16VStage / 1024 / kVsaWaves;   // 4
+constexpr int kVsaF16WaitPrevStep = (kVsaF16KLoads + kVsaF16VLoads) | (7 << 4) | (0 << 8);
+static_assert(kVsaF16VStage == kVsaVStage, "the V stages of both forms are 8 KiB");
+constexpr int kVsaKLoadsMax = kVsaF16KLoads > kVsaKLoads ? kVsaF16KLoads : kVsaKLoads;
+constexpr int kVsaVLoadsMax = kVsaF16VLoads > kVsaVLoads ? kVsaF16VLoads : kVsaVLoads;
+template <bool kF16> constexpr int vsa_kstage() { return kF16 ? kVsaF16KStage : kVsaKStage; }
 constexpr int kVsaPf = 1;  // MFMA operands and key scales read from LDS one chunk ahead (2: +1 %)
 // entry: cube (14 bits) | half << 14 | live keys of the half (1..32) << 16
 constexpr uint32_t kEntryCube = 0x3fffu;
 static_assert(kVsaSRows <= 64 && (kVsaSRows & (kVsaSRows - 1)) == 0, "scale rows per wave");
 
 struct VsaStager {
-  uint32_t koff[kVsaKLoads];  // byte offset inside a K tile of this lane's 16 bytes, per load
-  uint32_t voff[kVsaVLoads];  // byte offset inside a V^T tile (from the head block base + 2*k0)
+  uint32_t koff[kVsaKLoadsMax];  // byte offset inside a K tile of this lane's 16 bytes, per load
+  uint32_t voff[kVsaVLoadsMax];  // byte offset inside a V^T tile (from the head block base + 2*k0)
+                                 // or, f16, inside a V tile (from the tile's first row)
   uint32_t soff;              // ks element offset (bytes) of this lane's scale row
   uint32_t srow;              // MFMA row whose scales this lane stores (lanes below kVsaSRows)
   int wave;
@@ -756,10 +774,33 @@ struct VsaStager {
 // K stage: as in k_attention (128-byte rows, chunks swizzled by (row/2)%8, row m holds key
 // swap23(m)). V^T stage: 64-byte rows (one channel, 32 keys), byte o holds row o/64, logical
 // chunk ((o/16)%4) ^ ((row/4)%4), so the sixteen rows a quarter-wave reads fall on distinct banks.
-template <bool kHmScales>
+//
+// f16 stages (kF16): K byte o holds row o/256, logical chunk ((o/16)%16) ^ (row%16), row m holding
+// key swap23(m) as above, so the sixteen rows a quarter-wave reads with one 16-byte load fall on
+// distinct banks. V byte o holds key o/256 (natural order), logical chunk ((o/16)%16) ^
+// (4*(key%4)): a transposed read takes 4 keys x 32 bytes per 16 lanes and 8 keys x 64 bytes per
+// 32 lanes (one LDS cycle), and the swizzle puts those 16 chunks on distinct banks.
+template <bool kHmScales, bool kF16 = false>
 __device__ __forceinline__ VsaStager make_vsa_stager(const Args& a, int wave, int lane) {
   VsaStager s;
   s.wave = wave;
+  if constexpr (kF16) {
+#pragma unroll
+    for (int t = 0; t < kVsaF16KLoads; ++t) {
+      const uint32_t o = (wave * kVsaF16KLoads + t) * 1024 + 16 * lane;
+      const uint32_t row = o >> 8, chunk = ((o >> 4) & 15) ^ (row & 15);
+      s.koff[t] = swap23(row) * a.kv_bytes + 16 * chunk;
+    }
+#pragma unroll
+    for (int t = 0; t < kVsaF16VLoads; ++t) {
+      const uint32_t o = (wave * kVsaF16VLoads + t) * 1024 + 16 * lane;
+      const uint32_t key = o >> 8, chunk = ((o >> 4) & 15) ^ (4 * (key & 3));
+      s.voff[t] = key * a.kv_bytes + 16 * chunk;
+    }
+    s.srow = kVsaSRows * wave + (lane & (kVsaSRows - 1));
+    s.soff = 0;
+    return s;
+  }
 #pragma unroll
   for (int t = 0; t < kVsaKLoads; ++t) {
     const uint32_t o = (wave * kVsaKLoads + t) * 1024 + 16 * lane;
@@ -779,9 +820,20 @@ __device__ __forceinline__ VsaStager make_vsa_stager(const Args& a, int wave, in
 
 // LDS-DMA of the `live` keys of K tile k0 into stage `kst` (rows from `live` on load as zero),
 // and the load of this lane's key scale (head-major or token-major scales).
-template <bool kHmScales>
+template <bool kHmScales, bool kF16 = false>
 __device__ __forceinline__ float stage_k_vsa(const Args& a, const VsaStager& sg, uint32_t kv_head,
                                              uint32_t k0, uint32_t live, char* kst) {
+  if constexpr (kF16) {  // f16 rows: no scales
+    const char* base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes +
+                       kv_head * kVsaF16RowBytes;
+    const __amdgpu_buffer_rsrc_t rk =
+        rsrc(base, live ? (live - 1) * a.kv_bytes + kVsaF16RowBytes : 0u);
+#pragma unroll
+    for (int t = 0; t < kVsaF16KLoads; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (lds_void*)(kst + (sg.wave * kVsaF16KLoads + t) * 1024), 16, sg.koff[t], 0, 0, 0);
+    return 1.0f;
+  }
   const char* base = reinterpret_cast<const char*>(a.ki) + (size_t)k0 * a.kv_bytes + kv_head * 128;
   const __amdgpu_buffer_rsrc_t rk = rsrc(base, live ? (live - 1) * a.kv_bytes + 128 : 0u);
 #pragma unroll
@@ -796,9 +848,23 @@ __device__ __forceinline__ float stage_k_vsa(const Args& a, const VsaStager& sg,
                                                                          sg.soff, 0, 0));
 }
 
-// LDS-DMA of V^T tile k0 (32 columns of every channel row of this head's block).
+// LDS-DMA of V^T tile k0 (32 columns of every channel row of this head's block); f16: the `live`
+// rows of V from key k0 (rows from `live` on load as zero, so a dead key's V is finite).
+template <bool kF16 = false>
 __device__ __forceinline__ void stage_v_vsa(const Args& a, const VsaStager& sg, uint32_t kv_head,
-                                            uint32_t k0, char* vst) {
+                                            uint32_t k0, uint32_t live, char* vst) {
+  if constexpr (kF16) {
+    const char* base = reinterpret_cast<const char*>(a.vt) + (size_t)k0 * a.kv_bytes +
+                       kv_head * kVsaF16RowBytes;
+    const __amdgpu_buffer_rsrc_t rv =
+        rsrc(base, live ? (live - 1) * a.kv_bytes + kVsaF16RowBytes : 0u);
+#pragma unroll
+    for (int t = 0; t < kVsaF16VLoads; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (lds_void*)(vst + (sg.wave * kVsaF16VLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
+    return;
+  }
+  (void)live;
   const uint32_t blk = 128 * a.capacity;
   const char* base = reinterpret_cast<const char*>(a.vt) + ((size_t)kv_head * blk + k0) * 2;
   const __amdgpu_buffer_rsrc_t rv = rsrc(base, k0 < blk ? (blk - k0) * 2 : 0u);
@@ -808,9 +874,17 @@ __device__ __forceinline__ void stage_v_vsa(const Args& a, const VsaStager& sg, 
         rv, (lds_void*)(vst + (sg.wave * kVsaVLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
 }
 
-// Scales of a staged tile: (ks, -1.5*2^23*ks) for a live key, (ks, -inf) for a dead one.
+// Scales of a staged tile: (ks, -1.5*2^23*ks) for a live key, (ks, -inf) for a dead one; f16:
+// the mask c alone (0 live, -inf dead).
+template <bool kF16 = false>
 __device__ __forceinline__ void store_scales_vsa(char* kst, const VsaStager& sg, float ks,
                                                  uint32_t live) {
+  if constexpr (kF16) {
+    if ((threadIdx.x & 63) < kVsaSRows)
+      reinterpret_cast<float*>(kst + kVsaF16KRows)[sg.srow] =
+          swap23(sg.srow) < live ? 0.0f : -INFINITY;
+    return;
+  }
   if ((threadIdx.x & 63) < kVsaSRows) {
     float* sc = reinterpret_cast<float*>(kst + kVsaKRows);
     sc[sg.srow] = ks;
@@ -939,16 +1013,140 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
   if (!kNext) st.l += tile_sum_vsa(pb);
 }
 
+// ---- the f16 form's per-tile work (kernels/vsa_attention_16.loom: f16 QK in f32, times the
+// config scale, softmax, f16 PV): S^T = K Q^T on v_mfma_f32_32x32x16_f16, eight MFMAs per 32-key
+// tile, Q (32 queries x 128 channels) held as the B operands; the scores need no dequantisation,
+// only the dead-key mask c, so u = S + c; the softmax and PV are those of the int8 form.
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+// K operand of QK chunk c (channels 16c .. 16c+15): row n, logical chunk 2c + half.
+__device__ __forceinline__ v8h k_op_f16(const char* kst, int n, int half, int c) {
+  return *reinterpret_cast<const v8h*>(kst + n * kVsaF16RowBytes + 16 * ((2 * c + half) ^ (n & 15)));
+}
+
+// PV operand w (channel block w%4, key half w/4) from a V stage: lane l needs
+// V[16*(w/4) + 8*(l/32) + i][32*(w%4) + l%32] for i = 0..7 (the A operand of
+// v_mfma_f32_32x32x16_f16). The transposed read gives, in each group of 16 lanes, lane i element e
+// of the 8-byte piece lane 4e + i/4 points at, element i%4; with lane j pointing at key k0 + j/4,
+// channels c0 + 4*(j%4) .. +3, lane i receives V[k0 + e][c0 + i], e = 0..3. Two reads (keys k0 and
+// k0 + 4) make the eight keys.
+__device__ __forceinline__ v8h v_op_f16(const char* vst, int lane, int w) {
+  const int db = w & 3, kh = w >> 2;
+  const int g = lane >> 4, j = lane & 15;
+  const int key = 16 * kh + 8 * (g >> 1) + (j >> 2);               // key % 4 == j / 4
+  const int chunk = 4 * db + 2 * (g & 1) + ((j & 3) >> 1);
+  const int off = key * kVsaF16RowBytes + 16 * (chunk ^ (4 * (j >> 2))) + 8 * (j & 1);
+  const v4h lo = __builtin_bit_cast(
+      v4h, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vst + off)));
+  const v4h hi = __builtin_bit_cast(
+      v4h, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vst + off + 4 * kVsaF16RowBytes)));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Slots 4i..4i+3 of a fresh tile: u = S + c (c = 0 live, -inf dead), folded into the tile max.
+__device__ __forceinline__ void dequant_f16(const v16f& s, int i, float4 c4, float (&u)[16],
+                                            float& tmax) {
+  u[4 * i + 0] = s[4 * i + 0] + c4.x;
+  u[4 * i + 1] = s[4 * i + 1] + c4.y;
+  u[4 * i + 2] = s[4 * i + 2] + c4.z;
+  u[4 * i + 3] = s[4 * i + 3] + c4.w;
+  tmax = max3(tmax, max3(u[4 * i], u[4 * i + 1], u[4 * i + 2]), u[4 * i + 3]);
+}
+
+// The probability of slot r into pb[r/8].
+__device__ __forceinline__ void exp_one_vsa(const float (&u)[16], int r, float qsl, float negm,
+                                            v8h (&pb)[2]) {
+  pb[r / 8][r % 8] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qsl, negm));
+}
+
+__device__ __forceinline__ void first_tile_f16(const char* kst, const v8h (&qop)[8], float qsl,
+                                               State& st, float (&u)[16], int n, int half) {
+  const float* kc = reinterpret_cast<const float*>(kst + kVsaF16KRows);
+  v16f s = {};
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k_op_f16(kst, n, half, c), qop[c], s, 0, 0, 0);
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    dequant_f16(s, i, *reinterpret_cast<const float4*>(kc + 8 * i + 4 * half), u, tmax);
+  raise_max(tmax, qsl, st);
+}
+
+// One pipeline step of the f16 form, in the order of step_vsa:
+//   phase A  QK(j+1): 8 f16 MFMAs  with  the probabilities of tile j's slots 0..7 (one a chunk)
+//   phase B  PV(j):   8 f16 MFMAs  with  slots 8..15, then the mask + max of tile j+1 and the
+//                                        raise of m
+template <bool kNext>
+__device__ __forceinline__ void step_f16(const char* kst, const char* vst, const v8h (&qop)[8],
+                                         float qsl, State& st, float (&u)[16], int lane) {
+  const int n = lane & 31, half = lane >> 5;
+  if (__any(st.alpha != 1.0f)) {  // the rescale owed by the last raise of m
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[db][r] *= st.alpha;
+    st.alpha = 1.0f;
+  }
+  const float negm = -st.m;
+  const float* kc = reinterpret_cast<const float*>(kst + kVsaF16KRows);
+  v16f s = {};
+  v8h pb[2];
+  v8h kop[8];
+  v8h vop[8];
+  float4 c4[4];
+
+  // ---- phase A: QK(j+1) || probabilities of slots 0..7
+  if (kNext) kop[0] = k_op_f16(kst, n, half, 0);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    if (kNext && c + 1 < 8) kop[c + 1] = k_op_f16(kst, n, half, c + 1);
+    if (c == 7) vop[0] = v_op_f16(vst, lane, 0);
+    if (kNext) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop[c], qop[c], s, 0, 0, 0);
+    exp_one_vsa(u, c, qsl, negm, pb);
+    H3_CHUNK_END();
+  }
+
+  // ---- phase B: PV(j) || probabilities of slots 8..15, then mask + max of tile j+1
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    if (c + 1 < 8) vop[c + 1] = v_op_f16(vst, lane, c + 1);
+    if (kNext && c >= 2 && c < 6) c4[c - 2] = *reinterpret_cast<const float4*>(kc + 8 * (c - 2) + 4 * half);
+    st.acc[c & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[c], pb[c >> 2], st.acc[c & 3], 0, 0, 0);
+    if (c < 4) exp_pair_vsa(u, 8 + 2 * c, qsl, negm, pb);
+    if (kNext && c >= 3 && c < 7) dequant_f16(s, c - 3, c4[c - 3], u, tmax);
+    if (kNext && c == 7) {
+      st.l += tile_sum_vsa(pb);
+      raise_max(tmax, qsl, st);
+    }
+    H3_CHUNK_END();
+  }
+  if (!kNext) st.l += tile_sum_vsa(pb);
+}
+
+template <bool kF16, bool kNext, class QOp>
+__device__ __forceinline__ void vsa_step(const char* kst, const char* vst, const QOp& qop,
+                                         float qsl, State& st, float (&u)[16], int lane) {
+  if constexpr (kF16)
+    step_f16<kNext>(kst, vst, qop, qsl, st, u, lane);
+  else
+    step_vsa<kNext>(kst, vst, qop, qsl, st, u, lane & 31, lane >> 5);
+}
+
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // kHmScales: a.ks is head-major, [kv_head_limit][tokens]; otherwise token-major as the
-// operands' producer writes it, [tokens][kv_head_limit].
-template <bool kHmScales>
+// operands' producer writes it, [tokens][kv_head_limit]. kF16: the f16 form (a.qi, a.ki, a.vt
+// are the token-major f16 q, k, v; a.q_row and a.kv_bytes their row pitches in bytes; scores
+// times a.scale), with three workgroups per CU (51.6 KB of LDS each).
+template <bool kHmScales, bool kF16 = false>
 __global__ __launch_bounds__(kVsaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention_vsa(Args a) {
-  __shared__ __attribute__((aligned(16))) char k0s[kVsaKStage];
-  __shared__ __attribute__((aligned(16))) char k1s[kVsaKStage];
-  __shared__ __attribute__((aligned(16))) char k2s[kVsaKStage];
+  __shared__ __attribute__((aligned(16))) char k0s[vsa_kstage<kF16>()];
+  __shared__ __attribute__((aligned(16))) char k1s[vsa_kstage<kF16>()];
+  __shared__ __attribute__((aligned(16))) char k2s[vsa_kstage<kF16>()];
   __shared__ __attribute__((aligned(16))) char v0s[kVsaVStage];
   __shared__ __attribute__((aligned(16))) char v1s[kVsaVStage];
   __shared__ __attribute__((aligned(16))) char v2s[kVsaVStage];
@@ -973,14 +1171,21 @@ void k_attention_vsa(Args a) {
   const uint32_t q = cube * 64 + wave * kQueriesPerWave + n;
   const uint32_t q_read = q < a.tokens ? q : a.tokens - 1;
 
-  const VsaStager sg = make_vsa_stager<kHmScales>(a, wave, lane);
-  v4i qop[4];
-  {
+  const VsaStager sg = make_vsa_stager<kHmScales, kF16>(a, wave, lane);
+  std::conditional_t<kF16, v8h[8], v4i[4]> qop;
+  float qsl;
+  if constexpr (kF16) {
+    const char* src = reinterpret_cast<const char*>(a.qi) + (size_t)q_read * a.q_row +
+                      head * kVsaF16RowBytes;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) qop[c] = *reinterpret_cast<const v8h*>(src + 32 * c + 16 * half);
+    qsl = a.scale * kLog2e;
+  } else {
     const int32_t* src = a.qi + (size_t)q_read * (a.q_row / 4) + head * 32;
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) qop[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
+    qsl = a.qs[(size_t)q_read * a.head_limit + head] * kLog2e;
   }
-  const float qsl = a.qs[(size_t)q_read * a.head_limit + head] * kLog2e;
 
   State st;
 #pragma unroll
@@ -1052,31 +1257,35 @@ void k_attention_vsa(Args a) {
     uint32_t e2 = entry(2), e3 = entry(3);
     {
       const uint32_t e0 = entry(0), e1 = entry(1);
-      const float ks0 = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
-      const float ks1 = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
-      stage_v_vsa(a, sg, kv_head, k0_of(e0), v0s);
-      stage_v_vsa(a, sg, kv_head, k0_of(e1), v1s);
-      store_scales_vsa(k0s, sg, ks0, live_of(e0));
-      store_scales_vsa(k1s, sg, ks1, live_of(e1));
+      const float ks0 = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
+      const float ks1 = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
+      stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), v0s);
+      stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), v1s);
+      store_scales_vsa<kF16>(k0s, sg, ks0, live_of(e0));
+      store_scales_vsa<kF16>(k1s, sg, ks1, live_of(e1));
     }
-    float ks_held = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
+    float ks_held = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
     step_barrier<kWaitAll>();
-    first_tile_vsa(k0s, qop, qsl, st, u, n, half);
+    if constexpr (kF16)
+      first_tile_f16(k0s, qop, qsl, st, u, n, half);
+    else
+      first_tile_vsa(k0s, qop, qsl, st, u, n, half);
     step_barrier<kWaitAll>();
 
     // One step j: K(j+3) -> kc, V(j+2) -> vn2; QK(j+1) from kn, PV(j) from vc; then the scales
     // of K(j+2) into kn2.
 #define H3_VSA_STEP(kc, kn, kn2, vc, vn2)                                                      \
   {                                                                                          \
-    const float ks_new = stage_k_vsa<kHmScales>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);       \
-    stage_v_vsa(a, sg, kv_head, k0_of(e2), vn2);                                             \
+    const float ks_new =                                                                     \
+        stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
+    stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e2), live_of(e2), vn2);                          \
     const uint32_t e4 = entry(j + 4);                                                        \
-    step_vsa<true>(kn, vc, qop, qsl, st, u, n, half);                                        \
-    store_scales_vsa(kn2, sg, ks_held, live_of(e2));                                         \
+    vsa_step<kF16, true>(kn, vc, qop, qsl, st, u, lane);                                     \
+    store_scales_vsa<kF16>(kn2, sg, ks_held, live_of(e2));                                   \
     ks_held = ks_new;                                                                        \
     e2 = e3;                                                                                 \
     e3 = e4;                                                                                 \
-    step_barrier<kVsaWaitPrevStep>();                                                        \
+    step_barrier<kF16 ? kVsaF16WaitPrevStep : kVsaWaitPrevStep>();                           \
     ++j;                                                                                     \
   }
     const uint32_t steady = count - 1;
@@ -1091,7 +1300,7 @@ void k_attention_vsa(Args a) {
 #undef H3_VSA_STEP
     {  // the last tile's PV (stage j % 3)
       const uint32_t r = j % 3;
-      step_vsa<false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, n, half);
+      vsa_step<kF16, false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, lane);
     }
     step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
   }
@@ -1429,6 +1638,42 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
       hipLaunchKernelGGL(k_attention_vsa<true>, dim3(a.per_xcd * 8), dim3(kVsaThreads), 0, stream, a);
     else
       hipLaunchKernelGGL(k_attention_vsa<false>, dim3(a.per_xcd * 8), dim3(kVsaThreads), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_vsa_f16(const h3_attention_cfg& cfg, uint32_t token_count,
+                                    uint32_t heads, const uint16_t* q, const uint16_t* k,
+                                    const uint16_t* v, uint16_t* out, const int32_t* routes,
+                                    const int32_t* lengths, hipStream_t stream) {
+  Args a{};
+  a.qi = reinterpret_cast<const int32_t*>(q);
+  a.ki = reinterpret_cast<const int32_t*>(k);
+  a.vt = v;
+  a.out = out;
+  a.tokens = cfg.tokens;
+  a.token_count = token_count;
+  a.capacity = cfg.token_capacity;
+  a.q_row = cfg.q_stride * 2;
+  a.kv_bytes = cfg.kv_stride * 2;
+  a.out_stride = cfg.out_stride;
+  a.q_blocks = (token_count + 63) / 64;
+  a.heads = heads;
+  a.kv_head_limit = cfg.kv_stride / 128;
+  a.head_limit = cfg.out_stride / 128;
+  a.routes = routes;
+  a.lengths = lengths;
+  a.blocks = cfg.tokens / 64;
+  a.scale = cfg.scale;
+  // Generations of resident workgroups as in launch_attention_vsa, three per CU here (LDS).
+  const uint32_t items = a.q_blocks * heads;
+  const uint32_t gen = std::max(1u, 3u * device_cus());
+  for (uint32_t base = 0; base < items; base += gen) {
+    a.base = base;
+    a.total = std::min(gen, items - base);
+    a.per_xcd = (a.total + 7) / 8;
+    hipLaunchKernelGGL((k_attention_vsa<false, true>), dim3(a.per_xcd * 8), dim3(kVsaThreads), 0,
+                       stream, a);
   }
   return hipGetLastError();
 }

@@ -110,6 +110,11 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
                                 const int32_t* ki, const float* ks, const uint16_t* vt,
                                 uint16_t* out, const int32_t* routes, const int32_t* lengths,
                                 void* workspace, hipStream_t stream);
+// The f16 VSA attention (attention.hip): token-major f16 q, k, v; scores times cfg.scale.
+hipError_t launch_attention_vsa_f16(const h3_attention_cfg& cfg, uint32_t token_count,
+                                    uint32_t heads, const uint16_t* q, const uint16_t* k,
+                                    const uint16_t* v, uint16_t* out, const int32_t* routes,
+                                    const int32_t* lengths, hipStream_t stream);
 // h3_vsa_attention_i8 with a caller's workspace of at least scales_workspace_bytes(*cfg) bytes
 // (abi.cpp); with an empty view it reads the token-major scales as the public entry point does.
 int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,

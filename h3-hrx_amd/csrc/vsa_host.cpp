@@ -32,6 +32,7 @@ struct h3_vsa {
   h3_prepare_cfg prep_q{}, prep_k{};
   h3_transpose_cfg transpose{};
   uint32_t layers = 0;
+  uint32_t bits = 8;  // the attention's operands: 8 (INT8 QK) or 16 (f16 q, k, v)
   // plan (uploaded) and scratch shared by the layers (src/vsa/device.rs:7-46)
   h3_view src{}, inverse{}, lengths{};
   h3_view q{}, k{}, v{}, qm{}, km{}, vm{}, coarse{}, scores{}, routes{}, out{};
@@ -179,11 +180,23 @@ const char* h3_vsa_dense_reason(const h3_vsa_options* o, uint32_t tokens, float 
 int h3_vsa_build(const int32_t* src, const int32_t* inverse, const int32_t* lengths,
                  uint32_t blocks, uint32_t seq_len, uint32_t prefix_blocks,
                  const h3_vsa_options* options, uint32_t heads, uint32_t layers, h3_vsa** out) {
+  return h3_vsa_build_bits(src, inverse, lengths, blocks, seq_len, prefix_blocks, options, heads,
+                           8, layers, out);
+}
+
+int h3_vsa_build_bits(const int32_t* src, const int32_t* inverse, const int32_t* lengths,
+                      uint32_t blocks, uint32_t seq_len, uint32_t prefix_blocks,
+                      const h3_vsa_options* options, uint32_t heads, uint32_t bits,
+                      uint32_t layers, h3_vsa** out) {
   if (!src || !inverse || !lengths || !options || !out)
     return set_error(H3_ERR_ARGUMENT, "VSA build: null argument");
   *out = nullptr;
-  int st = h3_vsa_validate(options, 8);
+  int st = h3_vsa_validate(options, bits);
   if (st) return st;
+  // src/vsa/device.rs:86 names the attention vsa_attention_{bits}; the INT8 operands exist only
+  // for bits 8 (device.rs:104-158).
+  if (bits != 8 && bits != 16)
+    return set_error(H3_ERR_ARGUMENT, "VSA build: attention bits %u is neither 8 nor 16", bits);
   if (blocks < 1 || blocks > 16384 || seq_len < 1 || seq_len > 1048576 || prefix_blocks > blocks ||
       heads < 1 || heads > 256 || layers < 1)
     return set_error(H3_ERR_ARGUMENT,
@@ -202,6 +215,7 @@ int h3_vsa_build(const int32_t* src, const int32_t* inverse, const int32_t* leng
   r->prep_k.extra_scale = 1.0f;
   r->transpose = {width, n, H3_ELEM_F16};  // device.rs:120-128
   r->layers = layers;
+  r->bits = bits;
   const size_t nw2 = (size_t)n * width * 2, bw4 = (size_t)blocks * width * 4,
                hbb4 = (size_t)heads * blocks * blocks * 4;
   struct {
@@ -220,16 +234,31 @@ int h3_vsa_build(const int32_t* src, const int32_t* inverse, const int32_t* leng
                 {&r->coarse, bw4, nullptr},
                 {&r->scores, hbb4, nullptr},
                 {&r->routes, hbb4, nullptr},
-                {&r->out, nw2, nullptr},
-                {&r->qi, (size_t)n * width, nullptr},
-                {&r->ki, (size_t)n * width, nullptr},
-                {&r->qs, (size_t)n * heads * 4, nullptr},
-                {&r->ks, (size_t)n * heads * 4, nullptr},
-                {&r->vt, nw2, nullptr},
-                {&r->zero, (size_t)width * 4, nullptr},
-                {&r->ws, scales_workspace_bytes(r->attention), nullptr}};
+                {&r->out, nw2, nullptr}};
+  struct {
+    h3_view* v;
+    size_t bytes;
+  } integer[] = {{&r->qi, (size_t)n * width},
+                 {&r->ki, (size_t)n * width},
+                 {&r->qs, (size_t)n * heads * 4},
+                 {&r->ks, (size_t)n * heads * 4},
+                 {&r->vt, nw2},
+                 {&r->zero, (size_t)width * 4},
+                 {&r->ws, scales_workspace_bytes(r->attention)}};
   for (auto& a : allocs) {
     if ((st = allocate(a.v, a.bytes, a.upload))) {
+      release(r);
+      delete r;
+      return st;
+    }
+  }
+  if (bits == 16) {
+    *out = r;
+    set_error(H3_OK, "%s", "");
+    return H3_OK;
+  }
+  for (auto& a : integer) {
+    if ((st = allocate(a.v, a.bytes))) {
       release(r);
       delete r;
       return st;
@@ -283,17 +312,24 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
       (st = h3_vsa_scores(c, r->qm, r->km, r->scores, stream)) ||
       (st = h3_vsa_route(c, r->scores, r->routes, stream)))
     return st;
-  // 290-333: INT8 operands (K centred on the layer's previous mean), V^T, sparse attention
-  h3_view& mean = r->means[layer];
-  if ((st = h3_prepare_qk_i8(&r->prep_q, c->padded, r->q, r->zero, r->qi, r->qs, stream)) ||
-      (st = h3_prepare_qk_i8(&r->prep_k, c->padded, r->k, mean, r->ki, r->ks, stream)) ||
-      (st = h3_transpose_f16(&r->transpose, c->padded, c->padded, r->v, r->vt, stream)) ||
-      (st = vsa_attention_i8_ws(&r->attention, c->padded, c->heads, r->qi, r->qs, r->ki, r->ks,
-                                r->vt, r->out, r->routes, r->lengths, r->ws,
-                                reinterpret_cast<hipStream_t>(stream))))
-    return st;
-  // 334-346: this call's mean of the block K means, for the layer's next call
-  if ((st = h3_vsa_kmean(c->width, c->blocks, r->km, mean, stream))) return st;
+  if (r->bits == 16) {
+    // 362-386: the f16 attention reads the gathered q, k, v as they are
+    if ((st = h3_vsa_attention_f16(&r->attention, c->padded, c->heads, r->q, r->k, r->v, r->out,
+                                   r->routes, r->lengths, stream)))
+      return st;
+  } else {
+    // 290-333: INT8 operands (K centred on the layer's previous mean), V^T, sparse attention
+    h3_view& mean = r->means[layer];
+    if ((st = h3_prepare_qk_i8(&r->prep_q, c->padded, r->q, r->zero, r->qi, r->qs, stream)) ||
+        (st = h3_prepare_qk_i8(&r->prep_k, c->padded, r->k, mean, r->ki, r->ks, stream)) ||
+        (st = h3_transpose_f16(&r->transpose, c->padded, c->padded, r->v, r->vt, stream)) ||
+        (st = vsa_attention_i8_ws(&r->attention, c->padded, c->heads, r->qi, r->qs, r->ki, r->ks,
+                                  r->vt, r->out, r->routes, r->lengths, r->ws,
+                                  reinterpret_cast<hipStream_t>(stream))))
+      return st;
+    // 334-346: this call's mean of the block K means, for the layer's next call
+    if ((st = h3_vsa_kmean(c->width, c->blocks, r->km, mean, stream))) return st;
+  }
   if (gate.ptr) {
     // 372-434: value means, coarse attention, gated scatter
     if ((st = h3_vsa_pool(c, r->lengths, r->v, r->vm, stream)) ||
@@ -308,7 +344,8 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
 int h3_vsa_inspect(const h3_vsa* r, uint32_t layer, h3_vsa_buffers* out) {
   if (!r || !out || layer >= r->layers) return set_error(H3_ERR_ARGUMENT, "VSA inspect: bad argument");
   *out = {r->src, r->inverse, r->lengths, r->q, r->k, r->v, r->qm, r->km, r->scores, r->routes,
-          r->qi, r->ki, r->qs, r->ks, r->vt, r->out, r->means[layer], r->cfg, r->attention};
+          r->qi, r->ki, r->qs, r->ks, r->vt, r->out,
+          layer < r->means.size() ? r->means[layer] : h3_view{}, r->cfg, r->attention};
   set_error(H3_OK, "%s", "");
   return H3_OK;
 }

@@ -309,6 +309,9 @@ extern "C" {
                                   qi: H3View, qs: H3View, ki: H3View, ks: H3View, vt: H3View,
                                   out: H3View, routes: H3View, lengths: H3View,
                                   workspace: H3View, stream: H3Stream) -> c_int;
+    pub fn h3_vsa_attention_f16(cfg: *const H3AttentionCfg, token_count: u32, heads: u32,
+                                q: H3View, k: H3View, v: H3View, out: H3View, routes: H3View,
+                                lengths: H3View, stream: H3Stream) -> c_int;
     pub fn h3_vsa_plan_blocks(segments: *const H3VsaSegment, n_segments: u32, nt: u32, nh: u32,
                               nw: u32, blocks: *mut u32) -> c_int;
     pub fn h3_vsa_plan(segments: *const H3VsaSegment, n_segments: u32, seq_len: u32, nt: u32,
@@ -321,6 +324,10 @@ extern "C" {
     pub fn h3_vsa_build(src: *const i32, inverse: *const i32, lengths: *const i32, blocks: u32,
                         seq_len: u32, prefix_blocks: u32, options: *const H3VsaOptions,
                         heads: u32, layers: u32, out: *mut *mut h3_vsa) -> c_int;
+    pub fn h3_vsa_build_bits(src: *const i32, inverse: *const i32, lengths: *const i32,
+                             blocks: u32, seq_len: u32, prefix_blocks: u32,
+                             options: *const H3VsaOptions, heads: u32, bits: u32, layers: u32,
+                             out: *mut *mut h3_vsa) -> c_int;
     pub fn h3_vsa_destroy(vsa: *mut h3_vsa);
     pub fn h3_vsa_reset(vsa: *mut h3_vsa, stream: H3Stream) -> c_int;
     pub fn h3_vsa_attend(vsa: *mut h3_vsa, layer: u32, q: H3View, k: H3View, v: H3View,

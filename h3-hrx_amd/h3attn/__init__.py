@@ -217,6 +217,9 @@ SIGNATURES = {
     "h3_vsa_attention_i8": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, View, _S], ctypes.c_int),
+    "h3_vsa_attention_f16": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         _S], ctypes.c_int),
     "h3_vsa_attention_i8_ws": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, View, View, _S], ctypes.c_int),
@@ -248,6 +251,10 @@ SIGNATURES = {
         [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
          ctypes.c_uint32, _P(VsaOptionsC), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p],
         ctypes.c_int),
+    "h3_vsa_build_bits": (
+        [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+         ctypes.c_uint32, _P(VsaOptionsC), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+         ctypes.c_void_p], ctypes.c_int),
     "h3_vsa_destroy": ([ctypes.c_void_p], None),
     "h3_vsa_reset": ([ctypes.c_void_p, _S], ctypes.c_int),
     "h3_vsa_attend": (
@@ -564,6 +571,15 @@ def vsa_attention_i8(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki
                                     view(lengths), stream_ptr(stream)))
 
 
+def vsa_attention_f16(cfg: AttentionCfg, token_count: int, heads: int, q, k, v, out, routes,
+                      lengths, stream=None) -> None:
+    """h3_vsa_attention_16 (kernels/vsa_attention_16.loom): token-major f16 q, k, v; scores
+    (q . k) * cfg.scale over the kept cubes' live keys."""
+    check(lib().h3_vsa_attention_f16(ctypes.byref(cfg), token_count, heads, view(q), view(k),
+                                     view(v), view(out), view(routes), view(lengths),
+                                     stream_ptr(stream)))
+
+
 def scales_workspace_bytes(cfg) -> int:
     """Bytes of the head-major key-scale copy the _ws attention forms need for `cfg`."""
     if isinstance(cfg, AttentionSkipCfg):
@@ -653,11 +669,12 @@ def vsa_plan(segments, seq_len: int, nt: int, nh: int, nw: int):
 
 
 class Vsa:
-    """vsa::device::Runtime (src/vsa/device.rs) for INT8 attention: build once per plan, then
-    attend(layer, q, k, v, out, gate=None) per DiT block; reset() clears the per-layer K means."""
+    """vsa::device::Runtime (src/vsa/device.rs): build once per plan, then
+    attend(layer, q, k, v, out, gate=None) per DiT block; reset() clears the per-layer K means.
+    bits 8: INT8 attention (the K means centre the K operand); bits 16: f16 attention."""
 
     def __init__(self, src, inverse, lengths, prefix_blocks: int, heads: int,
-                 options: Optional[VsaOptions] = None, layers: int = 1):
+                 options: Optional[VsaOptions] = None, layers: int = 1, bits: int = 8):
         import numpy as np
 
         self.options = options or VsaOptions()
@@ -666,9 +683,11 @@ class Vsa:
         lengths = np.ascontiguousarray(lengths, np.int32)
         handle = ctypes.c_void_p()
         opt = self.options.c()
-        check(lib().h3_vsa_build(src.ctypes.data, inverse.ctypes.data, lengths.ctypes.data,
-                                 len(lengths), len(inverse), prefix_blocks, ctypes.byref(opt),
-                                 heads, layers, ctypes.byref(handle)))
+        check(lib().h3_vsa_build_bits(src.ctypes.data, inverse.ctypes.data, lengths.ctypes.data,
+                                      len(lengths), len(inverse), prefix_blocks,
+                                      ctypes.byref(opt), heads, bits, layers,
+                                      ctypes.byref(handle)))
+        self.bits = bits
         self.handle = handle
         self.layers = layers
 

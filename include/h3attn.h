@@ -439,6 +439,16 @@ int h3_vsa_attention_i8_ws(const h3_attention_cfg *cfg, uint32_t token_count, ui
                            h3_stream stream);
 
 
+/* h3_vsa_attention_f16 (kernels/vsa_attention_16.loom, h3_vsa_attention_16): the f16 form over
+ * the same gathered layout: query row t of head h attends to the keys 64kb + j with
+ * routes[h][t/64][kb] != 0 and j < lengths[kb], with scores (q . k) * cfg->scale in f32, a
+ * softmax, and f16 probabilities times f16 V. q [token_capacity][q_stride], k and v
+ * [token_capacity][kv_stride] f16 token-major (V is not transposed), out [token_count][out_stride]
+ * f16; cfg->tokens = padded (a multiple of 64, blocks <= 16384). Allocates nothing. */
+int h3_vsa_attention_f16(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                         h3_view q, h3_view k, h3_view v, h3_view out, h3_view routes,
+                         h3_view lengths, h3_stream stream);
+
 /* ---- VSA host policy (src/vsa.rs), no device work */
 
 /* A prefix segment of the sequence: rows row0 .. row0+rows-1 (text, a reference, audio). */
@@ -493,6 +503,14 @@ typedef struct h3_vsa h3_vsa;
 int h3_vsa_build(const int32_t *src, const int32_t *inverse, const int32_t *lengths,
                  uint32_t blocks, uint32_t seq_len, uint32_t prefix_blocks,
                  const h3_vsa_options *options, uint32_t heads, uint32_t layers, h3_vsa **out);
+/* Runtime::new with its `bits` argument (device.rs:49-58, 86): 8 as h3_vsa_build, or 16 for the
+ * f16 attention (h3_vsa_attention_f16 on the gathered q, k, v): no INT8 operands, V^T or K means
+ * are allocated, and h3_vsa_attend runs gather, pool, scores, route, the f16 attention and the
+ * (gated) scatter (device.rs:362-386). */
+int h3_vsa_build_bits(const int32_t *src, const int32_t *inverse, const int32_t *lengths,
+                      uint32_t blocks, uint32_t seq_len, uint32_t prefix_blocks,
+                      const h3_vsa_options *options, uint32_t heads, uint32_t bits,
+                      uint32_t layers, h3_vsa **out);
 void h3_vsa_destroy(h3_vsa *vsa);
 /* Runtime::reset (device.rs:189-196): zero every layer's K-mean vector. */
 int h3_vsa_reset(h3_vsa *vsa, h3_stream stream);
@@ -505,7 +523,8 @@ int h3_vsa_reset(h3_vsa *vsa, h3_stream stream);
 int h3_vsa_attend(h3_vsa *vsa, uint32_t layer, h3_view q, h3_view k, h3_view v, h3_view out,
                   h3_view gate, h3_stream stream);
 /* Device buffers of the runtime, for inspection: the plan, gathered q/k/v, block means,
- * scores and routes, the INT8 operands, V^T, the gathered output, and layer `layer`'s K mean. */
+ * scores and routes, the INT8 operands, V^T, the gathered output, and layer `layer`'s K mean
+ * (the INT8 operands, V^T and the K mean are empty views in a bits-16 runtime). */
 typedef struct {
   h3_view src, inverse, lengths, q, k, v, qm, km, scores, routes, qi, ki, qs, ks, vt, out,
       kmean;

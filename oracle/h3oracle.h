@@ -216,6 +216,12 @@ int h3o_vsa_attention_f64(const int8_t *qc, const float *qs, const int8_t *kc, c
                           const uint16_t *vt, int tokens, int capacity, int heads,
                           const int32_t *routes, const int32_t *lengths, const int *rows,
                           int n_rows, double *out, int threads);
+/* kernels/vsa_attention_16.loom in f64: f16 q, k, v token-major [capacity][heads*128], logits
+ * (q . k) * scale, natural softmax over the kept cubes' live keys. */
+int h3o_vsa_attention_f16_f64(const uint16_t *q, const uint16_t *k, const uint16_t *v, int tokens,
+                              int heads, double scale, const int32_t *routes,
+                              const int32_t *lengths, const int *rows, int n_rows, double *out,
+                              int threads);
 
 int h3o_max_threads(void);
 

@@ -264,3 +264,65 @@ int h3o_vsa_attention_f64(const int8_t *qc, const float *qs, const int8_t *kc, c
   }
   return 0;
 }
+
+/* kernels/vsa_attention_16.loom (body 1-555) in f64, as the reference's own test states it
+ * (src/vsa/device.rs:565-600): query row i (cube i/64) of head h attends to the keys j of every
+ * cube kb with routes[h][i/64][kb] != 0 and j % 64 < lengths[kb], logits (q . k) * scale over the
+ * f16 values, natural softmax, out = sum_j p_j v[j] / sum_j p_j.
+ *   q, k, v  f16 bits token-major [capacity][heads*128]
+ *   rows     the query rows to evaluate; out f64 [n_rows][heads][128]. */
+int h3o_vsa_attention_f16_f64(const uint16_t *q, const uint16_t *k, const uint16_t *v, int tokens,
+                              int heads, double scale, const int32_t *routes,
+                              const int32_t *lengths, const int *rows, int n_rows, double *out,
+                              int threads) {
+  const int d = 128, width = heads * d, blocks = tokens / 64;
+  long total = (long)n_rows * heads;
+#ifdef _OPENMP
+  if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel num_threads(threads)
+#endif
+  {
+    double *score = (double *)malloc(sizeof(double) * (size_t)tokens);
+    int *key = (int *)malloc(sizeof(int) * (size_t)tokens);
+    double qrow[128];
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+    for (long job = 0; job < total; ++job) {
+      const int ri = (int)(job / heads), h = (int)(job % heads);
+      const int row = rows[ri], qb = row / 64;
+      for (int c = 0; c < d; ++c)
+        qrow[c] = (double)h3o_half_to_float(q[(size_t)row * width + h * d + c]);
+      int nk = 0;
+      double top = -INFINITY;
+      for (int kb = 0; kb < blocks; ++kb) {
+        if (!routes[((size_t)h * blocks + qb) * blocks + kb]) continue;
+        for (int jj = 0; jj < lengths[kb] && jj < 64; ++jj) {
+          const int j = 64 * kb + jj;
+          const uint16_t *kr = k + (size_t)j * width + h * d;
+          double dot = 0.0;
+          for (int c = 0; c < d; ++c) dot += qrow[c] * (double)h3o_half_to_float(kr[c]);
+          const double s = dot * scale;
+          score[nk] = s;
+          key[nk++] = j;
+          if (s > top) top = s;
+        }
+      }
+      double sum = 0.0;
+      for (int t = 0; t < nk; ++t) {
+        score[t] = exp(score[t] - top);
+        sum += score[t];
+      }
+      double *o = out + ((size_t)ri * heads + h) * d;
+      for (int c = 0; c < d; ++c) {
+        double a = 0.0;
+        for (int t = 0; t < nk; ++t)
+          a += score[t] * (double)h3o_half_to_float(v[(size_t)key[t] * width + h * d + c]);
+        o[c] = a / sum;
+      }
+    }
+    free(score);
+    free(key);
+  }
+  return 0;
+}

@@ -114,6 +114,9 @@ def lib():
         L.h3o_vsa_attention_f64.argtypes = [i8, f32, i8, f32, u16, c_int, c_int, c_int, i32, i32,
                                             ip, c_int, f64, c_int]
         L.h3o_vsa_attention_f64.restype = c_int
+        L.h3o_vsa_attention_f16_f64.argtypes = [u16, u16, u16, c_int, c_int, ctypes.c_double,
+                                                i32, i32, ip, c_int, f64, c_int]
+        L.h3o_vsa_attention_f16_f64.restype = c_int
         L.h3o_max_threads.argtypes = []
         L.h3o_max_threads.restype = c_int
         _lib = L
@@ -409,6 +412,21 @@ def vsa_kmean(x):
     x = np.ascontiguousarray(x, np.float32)
     out = np.zeros(x.shape[1], np.float32)
     lib().h3o_vsa_kmean(x, x.shape[0], x.shape[1], out)
+    return out
+
+
+def vsa_attention_f16_f64(q, k, v, tokens, heads, scale, routes, lengths, rows, threads=0):
+    """f16 bits q, k, v token-major [>= tokens][heads*128], logits (q . k) * scale, routes
+    [heads][blocks][blocks], lengths [blocks]; f64 [len(rows)][heads][128]."""
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros((len(rows), heads, 128), np.float64)
+    lib().h3o_vsa_attention_f16_f64(np.ascontiguousarray(q, np.uint16).reshape(-1),
+                                    np.ascontiguousarray(k, np.uint16).reshape(-1),
+                                    np.ascontiguousarray(v, np.uint16).reshape(-1), tokens, heads,
+                                    float(scale),
+                                    np.ascontiguousarray(routes, np.int32).reshape(-1),
+                                    np.ascontiguousarray(lengths, np.int32), rows, len(rows), out,
+                                    threads)
     return out
 
 

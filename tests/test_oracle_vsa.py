@@ -258,6 +258,63 @@ def test_sparse_attention_masks_unrouted_blocks_and_dead_keys():
     assert not np.allclose(got[0, 0], vt.view(np.float16).astype(np.float64)[:, keys_bad].mean(1))
 
 
+def f16_operands(rng, heads, n, scale=1.0):
+    q, k, v = (O.f16_bits(rng.standard_normal((n, heads * 128)) * scale).reshape(n, heads * 128)
+               for _ in range(3))
+    return q, k, v
+
+
+def test_f16_sparse_attention_with_every_block_routed_is_dense_softmax_attention():
+    """With every cube kept and full, the f16 form is plain softmax attention, computed here
+    independently with numpy matrix products on the same f16 values."""
+    rng = np.random.default_rng(31)
+    heads, blocks = 2, 4
+    n = 64 * blocks
+    q, k, v = f16_operands(rng, heads, n)
+    routes = np.ones((heads, blocks, blocks), np.int32)
+    lengths = np.full(blocks, 64, np.int32)
+    rows = np.arange(0, n, 3, dtype=np.int32)
+    scale = 1 / math.sqrt(128)
+    got = O.vsa_attention_f16_f64(q, k, v, n, heads, scale, routes, lengths, rows)
+    f = lambda x: x.view(np.float16).astype(np.float64).reshape(n, heads, 128)
+    qf, kf, vf = f(q), f(k), f(v)
+    for h in range(heads):
+        lg = qf[rows, h] @ kf[:, h].T * scale
+        pr = np.exp(lg - lg.max(1, keepdims=True))
+        pr /= pr.sum(1, keepdims=True)
+        assert np.allclose(got[:, h], pr @ vf[:, h], atol=1e-12)
+    # a planted scale mistake (the 1/sqrt(128) dropped) is far outside that agreement
+    bad = O.vsa_attention_f16_f64(q, k, v, n, heads, 1.0, routes, lengths, rows)
+    assert np.abs(bad - got).max() > 1e-2
+
+
+def test_f16_sparse_attention_masks_unrouted_blocks_and_dead_keys():
+    rng = np.random.default_rng(32)
+    heads, blocks = 1, 5
+    n = 64 * blocks
+    q, k, v = f16_operands(rng, heads, n)
+    q[:] = 0  # every logit 0: uniform weights over the kept live keys
+    routes = np.zeros((heads, blocks, blocks), np.int32)
+    routes[0, 2, [0, 3]] = 1
+    lengths = np.array([10, 64, 64, 33, 64], np.int32)
+    got = O.vsa_attention_f16_f64(q, k, v, n, heads, 0.09, routes, lengths,
+                                  np.array([130, 140], np.int32))
+    keys = np.r_[np.arange(0, 10), np.arange(192, 225)]
+    want = v.view(np.float16).astype(np.float64)[keys].mean(0)
+    assert np.allclose(got[0, 0], want, atol=1e-12) and np.allclose(got[1, 0], want, atol=1e-12)
+    keys_bad = np.r_[np.arange(0, 11), np.arange(192, 225)]
+    assert not np.allclose(got[0, 0], v.view(np.float16).astype(np.float64)[keys_bad].mean(0))
+    # one live key in the only kept cube: the output is that key's V row exactly
+    routes[:] = 0
+    routes[0, 2, 4] = 1
+    lengths[4] = 1
+    q2, k2, _ = f16_operands(rng, heads, n, 3.0)
+    one = O.vsa_attention_f16_f64(q2, k2, v, n, heads, 0.09, routes, lengths,
+                                  np.array([128, 191], np.int32))
+    assert np.array_equal(one[:, 0], np.repeat(v.view(np.float16).astype(np.float64)[256][None],
+                                               2, 0))
+
+
 # --------------------------------------------------------------------- whole pipeline
 
 def reference_device_inputs():
@@ -355,6 +412,26 @@ def oracle_pipeline(heads, src, inverse, lengths, prefix, keep, data, gates, kme
     return out, gated, routes, O.vsa_kmean(km)
 
 
+def oracle_pipeline_f16(heads, src, inverse, lengths, prefix, keep, data, gates):
+    """The bits-16 runtime sequence (src/vsa/device.rs:200-263, 362-446): gather, routes, the f16
+    attention on the gathered q, k, v, (gated) scatter."""
+    t = len(inverse)
+    n = len(src)
+    width = heads * 128
+    nb = len(lengths)
+    q, k, v = (O.vsa_gather(src, t, d) for d in data)
+    qm, km = O.vsa_pool(lengths, q), O.vsa_pool(lengths, k)
+    scores = O.vsa_scores(qm, km, heads)
+    routes = O.vsa_route(scores, prefix, O.vsa_topk(keep, nb - prefix))
+    att = O.vsa_attention_f16_f64(q, k, v, n, heads, O.config_f32(1 / math.sqrt(128)), routes,
+                                  lengths, np.arange(n, dtype=np.int32))
+    fine = O.f16_bits(att.reshape(n, width).astype(np.float32)).reshape(n, width)
+    out = O.vsa_scatter(inverse, fine)
+    coarse = O.vsa_coarse_f64(scores, O.vsa_pool(lengths, v)).astype(np.float32)
+    gated = O.vsa_gated_scatter(inverse, fine, gates, coarse)
+    return out, gated, routes
+
+
 def nrmse(actual_bits, expected):
     a = actual_bits.view(np.float16).astype(np.float64)
     return math.sqrt(((a - expected) ** 2).sum() / (expected ** 2).sum())
@@ -373,6 +450,19 @@ def test_pipeline_matches_the_reference_device_oracle():
     zero = [np.zeros_like(data[0])] + data[1:]
     *_, routes0 = oracle_pipeline(heads, src, inverse, lengths, prefix, keep, zero, gates)[:3]
     assert np.all(routes0 == 1)
+
+
+def test_f16_pipeline_matches_the_reference_device_oracle():
+    """The reference's device test with bits 16 (src/vsa/device.rs:672-700): normalised RMSE
+    against its masked f32-math attention below 0.01, plain and gated."""
+    heads, src, inverse, lengths, prefix, keep, data, gates = reference_device_inputs()
+    expected, gated_expected, want_routes = independent_expected(heads, src, lengths, prefix, keep,
+                                                                 data, gates)
+    out, gated, routes = oracle_pipeline_f16(heads, src, inverse, lengths, prefix, keep, data,
+                                             gates)
+    assert np.array_equal(routes, want_routes)
+    assert nrmse(out, expected) < 0.01
+    assert nrmse(gated, gated_expected) < 0.01
 
 
 def test_pipeline_planted_route_mistake_is_caught():
