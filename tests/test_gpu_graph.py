@@ -128,6 +128,47 @@ def test_vsa_attention_replays_from_a_graph(dev):
     assert np.array_equal(from_dev(out), from_dev(out_ws))
 
 
+def test_f16_vsa_attention_and_runtime_replay_from_a_graph(dev):
+    """The f16 VSA attention alone, and the bits-16 runtime (gather, pool, scores, route, the f16
+    attention, gated scatter) on the reference's device-test inputs, as the reference's test
+    replays its graph (src/vsa/device.rs:701-719)."""
+    import torch
+
+    from test_gpu_vsa import random_routes, torch_f16
+    from test_gpu_vsa_f16 import f16_sparse_operands
+    from test_oracle_vsa import reference_device_inputs
+
+    rng = np.random.default_rng(13)
+    heads = 2
+    lengths = np.array([64, 40, 64, 64, 9, 64, 64, 33, 64], np.int32)
+    blocks = len(lengths)
+    n, w = 64 * blocks, heads * 128
+    q, k, v = (to_dev(x, dev) for x in f16_sparse_operands(rng, heads, lengths))
+    routes = to_dev(random_routes(rng, heads, blocks, 1, 0.4), dev)
+    ln = to_dev(lengths, dev)
+    cfg = H.AttentionCfg(w, w, w, n, n, H.config_f32(1 / math.sqrt(128)))
+    out = torch.zeros((n, w), dtype=torch.float16, device=dev)
+    print("graph: f16 vsa attention", flush=True)
+    replay_matches(torch, dev, lambda: H.vsa_attention_f16(cfg, n, heads, q, k, v, out, routes, ln),
+                   [out])
+
+    heads, src, inverse, lengths, prefix, keep, data, gates = reference_device_inputs()
+    t, w = len(inverse), heads * 128
+    vsa = H.Vsa(src, inverse, lengths, prefix, heads, H.VsaOptions(keep_percent=keep), bits=16)
+    qd, kd, vd = (torch_f16(d, dev) for d in data)
+    gate = torch_f16(gates, dev)
+    rout = torch.zeros((t * w,), dtype=torch.int16, device=dev)
+    gout = torch.zeros_like(rout)
+
+    def run():
+        vsa.attend(0, qd, kd, vd, rout)
+        vsa.attend(0, qd, kd, vd, gout, gate=gate)
+
+    print("graph: bits-16 vsa runtime", flush=True)
+    replay_matches(torch, dev, run, [rout, gout])
+    vsa.close()
+
+
 @pytest.mark.parametrize("smooth", [False, True])
 def test_stack_fused_route_branches_replay_from_a_graph(dev, smooth):
     """h3_stack_attend_fused forks the Q, K and V preparations onto the stack's side streams and
