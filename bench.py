@@ -101,6 +101,13 @@ def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
                                                                 ks, vt, out, ws), 2)
     skip_tm_ms = time_launches(torch, lambda: H.attention_i4qks(sc, tokens, heads, qi, qs, ki, ks,
                                                                 vt, out), 2)
+    # the FP6 form: the int4 codes converted into a lent workspace as the E2M3 values c/2, QK on
+    # the f8f6f4 MFMA inside the head-major kernel (conversion included in the time)
+    ws6 = torch.empty(H.fp6_workspace_bytes(ac), dtype=torch.uint8, device=dev)
+    fp6_ms = time_launches(torch, lambda: H.attention_i4qk_fp6(ac, tokens, heads, qi, qs, ki, ks,
+                                                               vt, out, ws6), 2)
+    fp6_finite = bool(torch.isfinite(out).all())
+    del ws6
     # the same token-major kernel on int8 codes (attention_i8qk, _ws form): what int4 costs over
     # int8 in one kernel design
     del qi, ki
@@ -117,8 +124,13 @@ def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
             "attention_i4qk_token_major_scales_ms": round(att_tm_ms, 3),
             "attention_i4qks_tau2_ms": round(skip_ms, 3),
             "attention_i4qks_tau2_token_major_scales_ms": round(skip_tm_ms, 3),
-            "note": "no int4 MFMA on gfx950: codes are widened to int8 in registers; _ms figures "
-                    "use the _ws forms (key scales copied head-major into a lent workspace)"}
+            "attention_i4qk_fp6_ms": round(fp6_ms, 3),
+            "attention_i4qk_fp6_tops": round(ops / (fp6_ms * 1e-3) / 1e12, 1),
+            "attention_i4qk_fp6_output_finite": fp6_finite,
+            "note": "no int4 MFMA on gfx950: attention_i4qk widens codes to int8 in registers "
+                    "(its _ms figures use the _ws forms, key scales copied head-major into a lent "
+                    "workspace); attention_i4qk_fp6 runs QK on the FP6 f8f6f4 MFMA over codes "
+                    "converted into a lent workspace, the conversion included"}
 
 
 def adjacent_kernels(torch, H, dev, tokens, width, out):

@@ -23,7 +23,7 @@ OUT = HERE / "libh3attn.so"
 OBJ = HERE / "_build"
 SOURCES = ["prepare.hip", "plain.hip", "attention.hip", "attention_hm.hip", "noalloc.hip", "gemm.hip",
            "abi.cpp", "stack.cpp",
-           "tables.cpp", "vsa.hip", "vsa_host.cpp"]
+           "tables.cpp", "vsa.hip", "vsa_host.cpp", "fp6.hip"]
 ARCH = "gfx950"
 
 

@@ -163,7 +163,14 @@ int rope_bindings(const char* stage, const h3_prepare_cfg* cfg, uint32_t tokens,
 }
 
 // Operand layouts of the attention kernels (attention.hip's modes).
-enum { kModeTokenI8 = 0, kModeHeadI8 = 1, kModeTokenI4 = 2, kModeTokenI4Skip = 3, kModeTokenI8Vsa = 4 };
+enum {
+  kModeTokenI8 = 0,
+  kModeHeadI8 = 1,
+  kModeTokenI4 = 2,
+  kModeTokenI4Skip = 3,
+  kModeTokenI8Vsa = 4,
+  kModeTokenI4Fp6 = 5
+};
 
 // The attention config (kernels/attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:7-17 and the same
 // declarations in vsa_attention_16.loom) and the launch arguments every attention form shares.
@@ -206,7 +213,8 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
                      h3_view routes = {}, h3_view lengths = {}, h3_view workspace = {}) {
   const bool head_major = mode == kModeHeadI8;
   const bool vsa = mode == kModeTokenI8Vsa;
-  const size_t code_div = (mode == kModeTokenI4 || mode == kModeTokenI4Skip) ? 2 : 1;
+  const bool fp6 = mode == kModeTokenI4Fp6;
+  const size_t code_div = (mode == kModeTokenI4 || mode == kModeTokenI4Skip || fp6) ? 2 : 1;
   int st = check_attention_cfg(stage, cfg, token_count, heads);
   if (st) return st;
   const size_t cap = cfg->token_capacity;
@@ -234,7 +242,7 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   // A workspace (token-major operands) receives a head-major copy of the key scales, which the
   // kernel then reads; without one it reads them token-major. Nothing is allocated either way.
   if (workspace.ptr) {
-    const size_t ws_need = scales_workspace_bytes(*cfg);
+    const size_t ws_need = fp6 ? fp6_layout(*cfg).bytes : scales_workspace_bytes(*cfg);
     if (workspace.bytes < ws_need)
       return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
                        stage, workspace.bytes, ws_need);
@@ -262,6 +270,15 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
                                                 workspace.ptr, stream));
   }
   if ((st = device_ready(stage))) return st;
+  if (fp6)
+    return launched(stage, launch_attention_i4_fp6(*cfg, token_count, heads,
+                                                   static_cast<const int32_t*>(qi.ptr),
+                                                   static_cast<const float*>(qs.ptr),
+                                                   static_cast<const int32_t*>(ki.ptr),
+                                                   static_cast<const float*>(ks.ptr),
+                                                   static_cast<const uint16_t*>(vt.ptr),
+                                                   static_cast<uint16_t*>(out.ptr), workspace.ptr,
+                                                   stream));
   return launched(stage, launch_attention(*cfg, mode, skip_tau, token_count, heads,
                                           static_cast<const int32_t*>(qi.ptr),
                                           static_cast<const float*>(qs.ptr),
@@ -627,6 +644,19 @@ int h3_attention_i4qk_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint
   if (!workspace.ptr) return null_workspace("attention_i4qk");
   return attention_common("attention_i4qk", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI4, 0.0f, {}, {},
+                          workspace);
+}
+
+size_t h3_fp6_workspace_bytes(const h3_attention_cfg* cfg) {
+  return cfg ? fp6_layout(*cfg).bytes : 0;
+}
+
+int h3_attention_i4qk_fp6(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                          h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                          h3_view workspace, h3_stream stream) {
+  if (!workspace.ptr) return null_workspace("attention_i4qk_fp6");
+  return attention_common("attention_i4qk_fp6", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                          reinterpret_cast<hipStream_t>(stream), kModeTokenI4Fp6, 0.0f, {}, {},
                           workspace);
 }
 

@@ -18,8 +18,15 @@
 //        8g..8g+7 are keys 16g + 8(l/32) + 0..7 of the block: the B operand of a 16-key f16 MFMA
 //        step with V^T in natural key order, and P never leaves its registers.
 //   dequant  accumulators start from the bit pattern of 1.5*2^23, so each ends as the float
-//        1.5*2^23 + S exactly and one FMA gives u = S*ks: u = acc*ks + c with c = -1.5*2^23*ks
-//        staged per key, or c = -inf for a key past the sequence (masking costs nothing).
+//        1.5*2^23 + S exactly and one FMA gives u = acc*ks + c with c = -1.5*2^23*ks staged per
+//        key (rounded to f32, so u is S*ks to within 0.75*ks plus the FMA's rounding: less than
+//        one unit of S), or c = -inf for a key past the sequence (masking costs nothing).
+//   FP6 form (kFp6, h3_attention_i4qk_fp6): int4 codes c, converted beforehand to the FP6 e2m3
+//        values c/2 (exact for every signed nibble, -8 included) in head-major rows laid out
+//        for the f8f6f4 MFMA, and the key scales folded with the factor 4. QK is two
+//        v_mfma_f32_32x32x64_f8f6f4 per 32 keys (64 channels each, at the int8 instruction's
+//        cost), accumulating S/4 exactly in f32 from zero, so u = acc*(4ks) + c with c = 0 is
+//        S*ks rounded once.
 //   softmax  base 2 on y = u*qs*log2e - m with no per-tile max: the running max m is kept from
 //        earlier tiles and a tile whose probabilities could exceed 2^8 is caught by its row sum
 //        (every p >= 0, so the sum of a lane's 16 probabilities bounds each of them; f16
@@ -93,6 +100,8 @@ constexpr int kRsrcWord3 = 0x00020000;            // gfx9 raw buffer: 32-bit dat
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v6i __attribute__((ext_vector_type(6)));  // an FP6 MFMA operand: 32 six-bit codes
 
 __device__ __forceinline__ uint32_t swap23(uint32_t m) {
   return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
@@ -226,12 +235,13 @@ __device__ __forceinline__ void issue_v(StepLoads& L, const Stager& sg) {
 __device__ __forceinline__ uint32_t rot(uint32_t r, uint32_t by) {
   return (r & ~3u) | ((r + by) & 3u);
 }
+template <bool kFp6 = false>
 __device__ __forceinline__ void store_scales(char* sst, const Stager& sg, float ks, uint32_t k0,
                                              uint32_t tokens) {
   if ((threadIdx.x & 63) < kSRows) {
     float* sc = reinterpret_cast<float*>(sst);
     sc[rot(sg.srow, 1)] = ks;
-    sc[kKeys + rot(sg.srow, 2)] = k0 + sg.skey < tokens ? -(kMagic * ks) : -INFINITY;
+    sc[kKeys + rot(sg.srow, 2)] = k0 + sg.skey < tokens ? (kFp6 ? 0.0f : -(kMagic * ks)) : -INFINITY;
   }
 }
 // Cross-attention: a key is live when its mask byte is nonzero (the mask's descriptor ends at the
@@ -244,13 +254,13 @@ __device__ __forceinline__ void store_scales_masked(char* sst, const Stager& sg,
     sc[kKeys + rot(sg.srow, 2)] = keep != 0 ? -(kMagic * ks) : -INFINITY;
   }
 }
-template <bool kCross>
+template <bool kCross, bool kFp6 = false>
 __device__ __forceinline__ void store_stage_scales(char* sst, const Stager& sg, float ks,
                                                    uint32_t keep, uint32_t k0, uint32_t tokens) {
   if (kCross)
     store_scales_masked(sst, sg, ks, keep);
   else
-    store_scales(sst, sg, ks, k0, tokens);
+    store_scales<kFp6>(sst, sg, ks, k0, tokens);
 }
 
 // Barrier between steps: this wave's LDS writes, and its staging loads from before the current
@@ -267,6 +277,7 @@ struct Tile {
   v16i s[2];    // S^T of the 32-key tiles of each parity
   v8h p[2][2];  // probabilities of the 32-key tiles of each parity, packed f16 (16 keys each)
   v4i q[4];     // Q^T operand: 4 chunks of 32 channels
+  v6i qf[2];    // FP6 form: the Q^T operand, 2 chunks of 64 channels
   float qsl;    // qs * log2(e)
   float negm;   // minus the running max (log2 units)
   float l;      // this lane's share of the row sum
@@ -289,12 +300,17 @@ struct Lanes {
   uint32_t v[4];
   uint32_t s;
 };
+// FP6 form: a 128-byte K row holds 32-byte blocks b (channels 32b .. 32b+31, 24 bytes of codes
+// and 8 of padding), so the operand of QK chunk x (channels 64x ..) for lane half h is block
+// 2x + h: 16-byte chunks 4x + 2h (k[2x]) and 4x + 2h + 1 (first 8 bytes, k[2x+1]).
+template <bool kFp6 = false>
 __device__ __forceinline__ Lanes make_lanes(int n, int half) {
   Lanes L;
   const uint32_t sw = (n >> 1) & 7;
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
-    L.k[x] = kKBias + n * kRowBytes + chunk_off(x, half, sw);
+    L.k[x] = kKBias + n * kRowBytes +
+             (kFp6 ? 16 * ((4 * (x >> 1) + 2 * half + (x & 1)) ^ sw) : chunk_off(x, half, sw));
     L.v[x] = n * kRowBytes + chunk_off(x, half, sw);
     asm volatile("" : "+v"(L.k[x]));
     asm volatile("" : "+v"(L.v[x]));
@@ -362,6 +378,17 @@ __device__ __forceinline__ void read_all(float (&o)[64], std::integer_sequence<i
 template <int... kR>
 __device__ __forceinline__ void zero_all(std::integer_sequence<int, kR...>) {
   (zero_acc<kR>(), ...);
+}
+
+// FP6 form: QK chunk x of a tile on the f8f6f4 MFMA (both operands FP6 e2m3), from zero or
+// accumulating.
+__device__ __forceinline__ v16i qk_fp6_first(v6i k, v6i q) {
+  v16i d;
+  asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0 cbsz:2 blgp:2" : "=&v"(d) : "v"(k), "v"(q));
+  return d;
+}
+__device__ __forceinline__ void qk_fp6_next(v16i& d, v6i k, v6i q) {
+  asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0 cbsz:2 blgp:2" : "+v"(d) : "v"(k), "v"(q));
 }
 
 // The first QK MFMA of a tile accumulates onto the bias 1.5*2^23 (`magic`, kept in registers).
@@ -491,14 +518,31 @@ __device__ __forceinline__ void raise_exact(Tile& T, int par, const float* kss, 
 // its QK and the scales of its first two quarters.
 struct Pre {
   v4i k[4];
+  v6i kf[2];  // FP6 form: the two K chunks
   float4 k4[2], c4[2];
 };
 // Part `part` (0-5) of the reads of `pre` for a sub-step that reads block `kb` of K stage `kst`
 // and block `sb` of scale stage `sst`: parts 0-3 the K chunks, 4-5 the scales of quarters 0-1.
+// FP6 form: parts 0-3 are the 16-byte and 8-byte halves of the two K chunks.
+template <bool kFp6 = false>
 __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, int kb,
                                          const char* sst, int sb, const Lanes& ln) {
   if (part < 4) {
-    pre.k[part] = *reinterpret_cast<const v4i*>(kst + (32 * kb * kRowBytes - kKBias) + ln.k[part]);
+    const char* a = kst + (32 * kb * kRowBytes - kKBias) + ln.k[part];
+    if constexpr (kFp6) {
+      v6i& d = pre.kf[part >> 1];
+      if ((part & 1) == 0) {
+        const v4i lo = *reinterpret_cast<const v4i*>(a), hi = __builtin_shufflevector(d, d, 4, 5, -1, -1);
+        d = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5);
+      } else {
+        const v2i h2 = *reinterpret_cast<const v2i*>(a);
+        const v4i lo = __builtin_shufflevector(d, d, 0, 1, 2, 3),
+                  hi = __builtin_shufflevector(h2, h2, 0, 1, -1, -1);
+        d = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5);
+      }
+    } else {
+      pre.k[part] = *reinterpret_cast<const v4i*>(a);
+    }
   } else {
     const float* kss = reinterpret_cast<const float*>(sst);
     pre.k4[part - 4] = scale4(kss, sb, part - 4, ln.s);
@@ -521,13 +565,14 @@ __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, in
 // exponentials), with the scales of quarters 2 and 3 read two quarters ahead. Each quarter adds
 // its probabilities to the lane's tile sum right away (f32 dot products), so the overflow check
 // after the last chunk waits on two instructions only.
-template <int kPar, bool kQK, bool kPV, bool kSM, typename Stage>
+template <int kPar, bool kQK, bool kPV, bool kSM, bool kFp6, typename Stage>
 __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int sb, Tile& T,
                                          const Lanes& ln, int half, const v16i& magic, Pre& pre,
                                          Stage&& stage) {
   constexpr int kSm = 1 - kPar;  // parity of the tile whose probabilities are computed
   const float* kss = reinterpret_cast<const float*>(sst);
   v4i kop[4];
+  v6i kopf[2];
   v8h vop[8];
   float4 k4[4], c4[4];
   float u[4];
@@ -544,8 +589,13 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
     k4[i] = scale4(kss, sb, i, ln.s);
     c4[i] = scale4(kss + kKeys, sb, i, ln.s);
   };
+  if constexpr (kFp6) {
+    kopf[0] = pre.kf[0];
+    kopf[1] = pre.kf[1];
+  } else {
 #pragma unroll
-  for (int o = 0; o < 4; ++o) kop[o] = pre.k[o];
+    for (int o = 0; o < 4; ++o) kop[o] = pre.k[o];
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     k4[i] = pre.k4[i];
@@ -557,10 +607,16 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
   for (int c = 0; c < 12; ++c) {
     if (c < 4) {
       if (kQK) {
-        if (c == 0)
+        if constexpr (kFp6) {  // chunks 1 and 3 carry no MFMA: their vector work stays
+          if (c == 0)
+            T.s[kPar] = qk_fp6_first(kopf[0], T.qf[0]);
+          else if (c == 2)
+            qk_fp6_next(T.s[kPar], kopf[1], T.qf[1]);
+        } else if (c == 0) {
           T.s[kPar] = qk_first(kop[0], T.q[0], magic);
-        else
+        } else {
           qk_next(T.s[kPar], kop[c], T.q[c]);
+        }
       }
     } else if (kPV) {
       const int v = c - 4;
@@ -597,17 +653,18 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
 
 // The reads of the next step's first `Pre` (K stage `kst` block 0, scale stage `sst` block 1) in
 // the chunks after the step barrier of a step's second sub-step.
+template <bool kFp6>
 __device__ __forceinline__ void next_step_reads(int c, Pre& next, const char* kst, const char* sst,
                                                 const Lanes& ln) {
   if (c == kBarrierChunk + 1) {
-    prefetch(next, 0, kst, 0, sst, 1, ln);
-    prefetch(next, 4, kst, 0, sst, 1, ln);
+    prefetch<kFp6>(next, 0, kst, 0, sst, 1, ln);
+    prefetch<kFp6>(next, 4, kst, 0, sst, 1, ln);
   } else if (c == kBarrierChunk + 2) {
-    prefetch(next, 1, kst, 0, sst, 1, ln);
-    prefetch(next, 5, kst, 0, sst, 1, ln);
+    prefetch<kFp6>(next, 1, kst, 0, sst, 1, ln);
+    prefetch<kFp6>(next, 5, kst, 0, sst, 1, ln);
   } else if (c == kBarrierChunk + 3) {
-    prefetch(next, 2, kst, 0, sst, 1, ln);
-    prefetch(next, 3, kst, 0, sst, 1, ln);
+    prefetch<kFp6>(next, 2, kst, 0, sst, 1, ln);
+    prefetch<kFp6>(next, 3, kst, 0, sst, 1, ln);
   }
 }
 
@@ -617,7 +674,7 @@ __device__ __forceinline__ char* ring(int i, char* a0, char* a1, char* a2, char*
   return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : a3;
 }
 
-template <bool kCross, bool kChain>
+template <bool kCross, bool kChain, bool kFp6 = false>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2), amdgpu_num_vgpr(kOReg)))
 void k_attention_hm(Geometry g) {
@@ -643,12 +700,14 @@ void k_attention_hm(Geometry g) {
   const int n = lane & 31;
   const int half = lane >> 5;
   const Stager sg = make_stager(g, wave, lane);
-  const Lanes ln = make_lanes(n, half);
+  const Lanes ln = make_lanes<kFp6>(n, half);
   // The QK bias 1.5*2^23, made opaque so that it stays in registers for the whole loop.
-  v16i magic;
+  v16i magic = {};  // the int8 form's accumulator bias (the FP6 form starts QK from zero)
+  if constexpr (!kFp6) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) magic[r] = kMagicBits;
-  asm volatile("" : "+v"(magic));
+    for (int r = 0; r < 16; ++r) magic[r] = kMagicBits;
+    asm volatile("" : "+v"(magic));
+  }
   const uint32_t n_stages = (g.tokens + kKeys - 1) / kKeys;  // 64-key stages; 32-key tiles 2x
   // Chaining: when the next block reads the same K/V^T stream and the stage count is a multiple
   // of the ring length, this block's last steady steps stage the next block's first stages
@@ -685,8 +744,19 @@ void k_attention_hm(Geometry g) {
     const uint32_t qq = w.q0 + n;
     const uint32_t q_read = qq < q_limit ? qq : q_limit - 1;
     const int32_t* src = g.qi + ((size_t)w.head * q_cap + q_read) * 32;
+    if constexpr (kFp6) {  // blocks 2x + half of the row: 24 bytes of codes each
+      const char* b = reinterpret_cast<const char*>(src) + 32 * half;
 #pragma unroll
-    for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
+      for (int x = 0; x < 2; ++x) {
+        const v2i h2 = *reinterpret_cast<const v2i*>(b + 64 * x + 16);
+        T.qf[x] = __builtin_shufflevector(*reinterpret_cast<const v4i*>(b + 64 * x),
+                                          __builtin_shufflevector(h2, h2, 0, 1, -1, -1), 0, 1, 2,
+                                          3, 4, 5);
+      }
+    } else {
+#pragma unroll
+      for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
+    }
     T.qsl = g.qs[(size_t)w.head * q_cap + q_read] * kLog2e;
   };
 
@@ -727,8 +797,8 @@ void k_attention_hm(Geometry g) {
   T.l = 0.0f;
   zero_all(std::make_integer_sequence<int, 64>{});
   if (!chained) {
-    store_stage_scales<kCross>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
-    store_stage_scales<kCross>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
+    store_stage_scales<kCross, kFp6>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
+    store_stage_scales<kCross, kFp6>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
     step_barrier<kWaitAll>();
   } else {
     // The first stages landed before the previous block's last barrier; the previous block's
@@ -742,15 +812,15 @@ void k_attention_hm(Geometry g) {
   issue_v<kCross>(Lm, sg);
   Pre pre;
 #pragma unroll
-  for (int part = 0; part < 4; ++part) prefetch(pre, part, k0s, 0, s0s, 0, ln);
-  sub_step<0, true, false, false>(nullptr, nullptr, 0, T, ln, half, magic, pre,
+  for (int part = 0; part < 4; ++part) prefetch<kFp6>(pre, part, k0s, 0, s0s, 0, ln);
+  sub_step<0, true, false, false, kFp6>(nullptr, nullptr, 0, T, ln, half, magic, pre,
                                   [&](int c, Pre& next) {
-    if (c >= 4 && c < 10) prefetch(next, c - 4, k0s, 1, s0s, 0, ln);
+    if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, k0s, 1, s0s, 0, ln);
   });
-  sub_step<1, true, false, true>(nullptr, s0s, 0, T, ln, half, magic, pre, [&](int c, Pre& next) {
-    if (c == 0) store_stage_scales<kCross>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
+  sub_step<1, true, false, true, kFp6>(nullptr, s0s, 0, T, ln, half, magic, pre, [&](int c, Pre& next) {
+    if (c == 0) store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
     if (c == kBarrierChunk) step_barrier<kWaitPrevStep<kCross>>();
-    next_step_reads(c, next, k1s, s0s, ln);
+    next_step_reads<kFp6>(c, next, k1s, s0s, ln);
   });
   float ks_held = Lm.ks;
   uint32_t keep_held = Lm.keep;
@@ -769,20 +839,20 @@ void k_attention_hm(Geometry g) {
     StepLoads L = plan_step<kCross>(g, kv_head, stage_of(j + 4) * kKeys, kr(J),
                                     stage_of(j + 3) * kKeys, vr(J + 3));
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
-    sub_step<0, true, true, true>(vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
+    sub_step<0, true, true, true, kFp6>(vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
       if (c == 0)
-        store_stage_scales<kCross>(sr(J + 3), sg, ks_held, keep_held, stage_of(j + 3) * kKeys,
+        store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_held, keep_held, stage_of(j + 3) * kKeys,
                                    g.tokens);
       if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep)
         issue_load<kCross>(L, sg, c / kLoadGap);
-      if (c >= 4 && c < 10) prefetch(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
+      if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
     });
-    sub_step<1, true, true, true>(vr(J), sr(J + 1), 0, T, ln, half, magic, pre,
+    sub_step<1, true, true, true, kFp6>(vr(J), sr(J + 1), 0, T, ln, half, magic, pre,
                                   [&](int c, Pre& next) {
       const int slot = (c + 12) / kLoadGap;
       if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
       if (c == kBarrierChunk) step_barrier<kWaitTwoSteps<kCross>>();
-      next_step_reads(c, next, kr(J + 2), sr(J + 1), ln);
+      next_step_reads<kFp6>(c, next, kr(J + 2), sr(J + 1), ln);
     });
     ks_held = L.ks;
     keep_held = L.keep;
@@ -802,8 +872,8 @@ void k_attention_hm(Geometry g) {
 
   // ---- last step (j = n_stages - 1): PV of tiles 2j and 2j+1, the probabilities of 2j+1 between
   // (its scales came in `pre`; its K reads there are unused)
-  sub_step<0, false, true, true>(vr(j), sr(j), 1, T, ln, half, magic, pre, [](int, Pre&) {});
-  sub_step<1, false, true, false>(vr(j), nullptr, 0, T, ln, half, magic, pre, [](int, Pre&) {});
+  sub_step<0, false, true, true, kFp6>(vr(j), sr(j), 1, T, ln, half, magic, pre, [](int, Pre&) {});
+  sub_step<1, false, true, false, kFp6>(vr(j), nullptr, 0, T, ln, half, magic, pre, [](int, Pre&) {});
   step_barrier<kWaitAll>();  // no staging load outlives the block (chained ones have landed)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // the last PV MFMAs have landed
 
@@ -908,6 +978,36 @@ hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count
     hipLaunchKernelGGL((k_attention_hm<false, true>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
   else
     hipLaunchKernelGGL((k_attention_hm<false, false>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_hm_fp6(const h3_attention_cfg& cfg, uint32_t token_count,
+                                   uint32_t heads, const void* qf, const float* qs, const void* kf,
+                                   const float* ks, const uint16_t* vt, uint16_t* out,
+                                   hipStream_t stream) {
+  Geometry g{};
+  g.qi = static_cast<const int32_t*>(qf);
+  g.qs = qs;
+  g.ki = static_cast<const int32_t*>(kf);
+  g.ks = ks;
+  g.vt = vt;
+  g.out = out;
+  g.tokens = cfg.tokens;
+  g.rows = std::min(token_count, cfg.tokens);
+  g.capacity = cfg.token_capacity;
+  g.out_stride = cfg.out_stride;
+  g.q_blocks = (token_count + kBlockQ - 1) / kBlockQ;
+  g.kv_head_limit = cfg.kv_stride / 128;
+  g.head_limit = cfg.out_stride / 128;
+  g.total = g.q_blocks * heads;
+  g.per_xcd = (g.total + 7) / 8;
+  g.wpx = workgroups_per_xcd(g);
+  if (chain_blocks(g))
+    hipLaunchKernelGGL((k_attention_hm<false, true, true>), dim3(g.wpx * 8), dim3(kThreads), 0,
+                       stream, g);
+  else
+    hipLaunchKernelGGL((k_attention_hm<false, false, true>), dim3(g.wpx * 8), dim3(kThreads), 0,
+                       stream, g);
   return hipGetLastError();
 }
 

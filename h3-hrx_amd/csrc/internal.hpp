@@ -80,6 +80,22 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                             uint32_t heads, const int32_t* qi, const float* qs, const int32_t* ki,
                             const float* ks, const uint16_t* vt, uint16_t* out, void* workspace,
                             hipStream_t stream);
+// The FP6 form of the int4 attention (fp6.hip): byte offsets in its lent workspace of the FP6
+// Q and K rows ([heads][capacity][128 B]) and the head-major scales (the key scales times 4).
+struct Fp6Layout {
+  size_t q, k, qs, ks, bytes;
+};
+Fp6Layout fp6_layout(const h3_attention_cfg& cfg);
+// Converts the token-major int4 operands into the workspace, then runs the head-major kernel's
+// FP6 form (launch_attention_hm_fp6) on them.
+hipError_t launch_attention_i4_fp6(const h3_attention_cfg& cfg, uint32_t token_count,
+                                   uint32_t heads, const int32_t* qi, const float* qs,
+                                   const int32_t* ki, const float* ks, const uint16_t* vt,
+                                   uint16_t* out, void* workspace, hipStream_t stream);
+hipError_t launch_attention_hm_fp6(const h3_attention_cfg& cfg, uint32_t token_count,
+                                   uint32_t heads, const void* qf, const float* qs, const void* kf,
+                                   const float* ks, const uint16_t* vt, uint16_t* out,
+                                   hipStream_t stream);
 // Compute units of the current device (cached per device; 256 if the query fails).
 uint32_t device_cus();
 // attention_i8qkhm: the head-major INT8 kernel of attention_hm.hip (eight waves of 32 queries,

@@ -276,6 +276,10 @@ extern "C" {
     /// `h3_attention_i8qk_ws` with the library's static 8 MiB device array as the workspace:
     /// allocates nothing, for callers that cannot; (kv_stride/128)·tokens ≤ 2,097,152, and
     /// calls that overlap on one GPU race on the array.
+    pub fn h3_attention_i4qk_fp6(cfg: *const H3AttentionCfg, token_count: u32, heads: u32,
+                                 qi: H3View, qs: H3View, ki: H3View, ks: H3View, vt: H3View,
+                                 out: H3View, workspace: H3View, stream: H3Stream) -> c_int;
+    pub fn h3_fp6_workspace_bytes(cfg: *const H3AttentionCfg) -> usize;
     pub fn h3_attention_i8qk_static(cfg: *const H3AttentionCfg, token_count: u32, heads: u32,
                                     qi: H3View, qs: H3View, ki: H3View, ks: H3View, vt: H3View,
                                     out: H3View, stream: H3Stream) -> c_int;

@@ -224,6 +224,10 @@ SIGNATURES = {
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, View, View, _S], ctypes.c_int),
     "h3_scales_workspace_bytes": ([_P(AttentionCfg)], ctypes.c_size_t),
+    "h3_fp6_workspace_bytes": ([_P(AttentionCfg)], ctypes.c_size_t),
+    "h3_attention_i4qk_fp6": (
+        [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
+         View, _S], ctypes.c_int),
     "h3_attention_i8qk_ws": (
         [_P(AttentionCfg), ctypes.c_uint32, ctypes.c_uint32, View, View, View, View, View, View,
          View, _S], ctypes.c_int),
@@ -578,6 +582,20 @@ def vsa_attention_f16(cfg: AttentionCfg, token_count: int, heads: int, q, k, v, 
     check(lib().h3_vsa_attention_f16(ctypes.byref(cfg), token_count, heads, view(q), view(k),
                                      view(v), view(out), view(routes), view(lengths),
                                      stream_ptr(stream)))
+
+
+def fp6_workspace_bytes(cfg: AttentionCfg) -> int:
+    """Bytes of the workspace h3_attention_i4qk_fp6 converts the int4 operands into."""
+    return lib().h3_fp6_workspace_bytes(ctypes.byref(cfg))
+
+
+def attention_i4qk_fp6(cfg: AttentionCfg, token_count: int, heads: int, qi, qs, ki, ks, vt, out,
+                       workspace, stream=None) -> None:
+    """h3_attention_i4qk on the FP6 MFMA: the int4 operands converted into `workspace`
+    (fp6_workspace_bytes(cfg) bytes), then the head-major kernel's FP6 form."""
+    check(lib().h3_attention_i4qk_fp6(ctypes.byref(cfg), token_count, heads, view(qi), view(qs),
+                                      view(ki), view(ks), view(vt), view(out), view(workspace),
+                                      stream_ptr(stream)))
 
 
 def scales_workspace_bytes(cfg) -> int:

@@ -318,6 +318,19 @@ int h3_attention_i4qks_ws(const h3_attention_skip_cfg *cfg, uint32_t token_count
                           h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                           h3_view out, h3_view workspace, h3_stream stream);
 
+/* h3_attention_i4qk_fp6: h3_attention_i4qk (the same bindings, token-major int4 operands and
+ * scales as h3_prepare_qk_i4 writes them) computed on gfx950's FP6 matrix instructions, with a
+ * lent workspace of h3_fp6_workspace_bytes(cfg) bytes (1.09 GB at 129,024 tokens and 32 heads).
+ * No counterpart in the reference: every int4 code c (-8..7) is converted into the workspace as
+ * the FP6 e2m3 value c/2 (exact), in head-major rows laid out for v_mfma_f32_32x32x64_f8f6f4, and
+ * the scales head-major (the key scales times 4); the head-major attention kernel then runs QK
+ * on that MFMA, 64 channels per instruction at the cost of the int8 one's 32, with exact f32
+ * scores. Allocates nothing. */
+int h3_attention_i4qk_fp6(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
+                          h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
+                          h3_view workspace, h3_stream stream);
+size_t h3_fp6_workspace_bytes(const h3_attention_cfg *cfg);
+
 /* h3_attention_i8qk_static has no counterpart in the reference. It is for callers that cannot
  * allocate device memory and have none to lend (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): h3_attention_i8qk_ws with the workspace in a static

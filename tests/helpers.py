@@ -87,3 +87,54 @@ def north_star_ok(got: np.ndarray, want: np.ndarray):
     """max-abs 2e-2 and mean-abs 2e-3 on f16 outputs."""
     err = np.abs(got.astype(np.float64) - want)
     return float(err.max()), float(err.mean())
+
+
+# ---- the FP6 form of the int4 attention (h3_attention_i4qk_fp6): its workspace layout, restated
+
+def e2m3_value(code):
+    """The OCP FP6 E2M3 value of a 6-bit code: sign bit 5, exponent bits 4-3 (bias 1), mantissa
+    bits 2-0, subnormal at exponent 0; no infinities or NaNs."""
+    code = np.asarray(code, np.int64)
+    s = np.where(code & 32, -1.0, 1.0)
+    e = (code >> 3) & 3
+    m = (code & 7).astype(np.float64)
+    return s * np.where(e == 0, m / 8.0, (1.0 + m / 8.0) * np.exp2(e - 1.0))
+
+
+# e2m3 code of c/2 for the signed nibble c = 0..7, -8..-1 (index = the nibble's 4 bits)
+FP6_HALF_CODES = np.array([0, 4, 8, 12, 16, 18, 20, 22, 56, 54, 52, 50, 48, 44, 40, 36], np.uint8)
+
+
+def fp6_rows(words, heads, tokens, cap):
+    """Token-major int4 words [rows][heads*16] (low nibble first) -> the FP6 head-major rows
+    [heads*cap][128] bytes of the workspace for rows < tokens (other rows left 0): block b of a
+    row holds channels 32b..32b+31 as six-bit codes, code i in bits 6i.. of its first 24 bytes,
+    then 8 zero bytes."""
+    w = np.ascontiguousarray(words, np.int32).view(np.uint32)[:tokens].reshape(tokens, heads, 16)
+    nib = np.stack([(w >> np.uint32(4 * j)) & np.uint32(15) for j in range(8)], -1)
+    codes = FP6_HALF_CODES[nib.reshape(tokens, heads, 128)].astype(np.uint64)  # [t][h][ch]
+    out = np.zeros((heads, cap, 4, 32), np.uint8)
+    for b in range(4):
+        blk = codes[:, :, 32 * b:32 * b + 32]
+        acc = np.zeros((tokens, heads, 3), np.uint64)  # 192 bits as three u64
+        for i in range(32):
+            bit = 6 * i
+            acc[..., bit // 64] |= blk[..., i] << np.uint64(bit % 64)
+            if bit % 64 > 58:
+                acc[..., bit // 64 + 1] |= blk[..., i] >> np.uint64(64 - bit % 64)
+        out[:, :tokens, b, :24] = acc.astype("<u8").view(np.uint8).reshape(tokens, heads, 24).transpose(1, 0, 2)
+    return out.reshape(heads * cap, 128)
+
+
+def fp6_decode_rows(rows):
+    """The values of FP6 rows [n][128] bytes: [n][128] channel values."""
+    r = np.ascontiguousarray(rows, np.uint8).reshape(-1, 4, 32)[:, :, :24]
+    q = r.reshape(-1, 4, 3, 8).copy().view("<u8")[..., 0]  # [n][4][3] u64
+    vals = np.zeros((r.shape[0], 4, 32), np.float64)
+    for i in range(32):
+        bit = 6 * i
+        c = (q[..., bit // 64] >> np.uint64(bit % 64)) & np.uint64(63)
+        if bit % 64 > 58:
+            c |= (q[..., bit // 64 + 1] << np.uint64(64 - bit % 64)) & np.uint64(63)
+        vals[..., i] = e2m3_value(c.astype(np.int64))
+    return vals.reshape(-1, 128)

@@ -11,7 +11,9 @@
   fused rows (codes and scales of sampled rows equal the oracle's), attention_i4qk and its _ws
   form (bit-identical), the skip twin at tau = 1000 (bit-identical to attention_i4qk) and at
   tau = 2 (finite), and sampled rows of attention_i4qk against the f64 attention of the read-back
-  codes (tests/kernels.rs:1994-2019 style sampled-row checks).
+  codes (tests/kernels.rs:1994-2019 style sampled-row checks); the FP6 form
+  (h3_attention_i4qk_fp6, NaN-filled workspace) finite and on the same sampled rows within the
+  same tolerance.
 - The token-major kernels (i8qk, i4qk, i4qks; plain and _ws) split their work into launches of
   16 * CUs items; 1100 workload heads over 1000 tokens (128-query blocks) make three launches
   on 256 CUs, the last one partial. Heads wrap
@@ -134,7 +136,13 @@ def test_config5a_int4_at_full_size(dev):
     for tau, name in ((1000.0, "tau1000"), (2.0, "tau2")):
         sc = H.AttentionSkipCfg(width, width, width, tokens, cap, 1.0, tau)
         H.attention_i4qks_ws(sc, tokens, heads, qi, qs, ki, ks, vt, outs[name], ws)
+    print("5a: attention_i4qk_fp6", flush=True)
+    outs["fp6"] = torch.full((tokens, width), float("nan"), dtype=torch.float16, device=dev)
+    ws6 = torch.full((H.fp6_workspace_bytes(cfg) // 4,), float("nan"), dtype=torch.float32,
+                     device=dev)
+    H.attention_i4qk_fp6(*args, outs["fp6"], ws6)
     torch.cuda.synchronize()
+    del ws6
     plain = from_dev(outs["plain"])
     assert np.array_equal(from_dev(outs["ws"]), plain)
     assert np.array_equal(from_dev(outs["tau1000"]), plain)
@@ -157,6 +165,11 @@ def test_config5a_int4_at_full_size(dev):
     got = plain.view(np.float16).astype(np.float64).reshape(tokens, heads, 128)[rows]
     mx, mean = north_star_ok(got, want)
     assert mx < 2e-2 and mean < 2e-3, (mx, mean)
+    got6 = from_dev(outs["fp6"]).view(np.float16).astype(np.float64).reshape(tokens, heads, 128)
+    mx, mean = north_star_ok(got6[rows], want)
+    print(f"5a fp6 sampled rows: max {mx:.3e} mean {mean:.3e}", flush=True)
+    assert mx < 2e-2 and mean < 2e-3, (mx, mean)
+    assert np.isfinite(got6).all()
 
 
 def test_token_major_kernels_past_one_launch(dev):

@@ -167,3 +167,21 @@ def test_runtime_build_refuses_bad_options_without_allocating():
     src, inverse, lengths, prefix = H.vsa_plan([(0, 65), (65, 6)], 246, 5, 5, 7)
     with pytest.raises(H.H3Error, match="keep_percent"):
         H.Vsa(src, inverse, lengths, prefix, 2, H.VsaOptions(keep_percent=0.0))
+
+
+def test_f16_vsa_attention_checks_its_bindings():
+    """h3_vsa_attention_f16 (vsa_attention_16.loom): q [cap][q_stride], k and v
+    [cap][kv_stride] f16, out [token_count][out_stride], routes [heads][blocks][blocks],
+    lengths [blocks]; whole cubes only."""
+    heads, blocks = 2, 5
+    n, w = 64 * blocks, 256
+    a = H.AttentionCfg(w, w, w, n, n, 0.088)
+    L = H.lib()
+    need = [n * w * 2, n * w * 2, n * w * 2, n * w * 2, heads * blocks * blocks * 4, blocks * 4]
+    for i in range(6):
+        views = [fake(x - (4 if j == i else 0)) for j, x in enumerate(need)]
+        st = L.h3_vsa_attention_f16(ctypes.byref(a), n, heads, *views, None)
+        assert st == H.H3_ERR_BINDING and f"binding {i} " in H.last_error(), H.last_error()
+    a.tokens = n - 1
+    st = L.h3_vsa_attention_f16(ctypes.byref(a), n - 1, heads, *[fake(x) for x in need], None)
+    assert st == H.H3_ERR_CONFIG, H.last_error()
