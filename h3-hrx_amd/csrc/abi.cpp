@@ -655,6 +655,8 @@ int h3_attention_i4qk_fp6(const h3_attention_cfg* cfg, uint32_t token_count, uin
                           h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                           h3_view workspace, h3_stream stream) {
   if (!workspace.ptr) return null_workspace("attention_i4qk_fp6");
+  // the conversion moves 16 bytes per access of the codes and of the workspace rows
+  if (int st = check_aligned16("attention_i4qk_fp6", {qi, ki, workspace})) return st;
   return attention_common("attention_i4qk_fp6", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
                           reinterpret_cast<hipStream_t>(stream), kModeTokenI4Fp6, 0.0f, {}, {},
                           workspace);
@@ -876,6 +878,7 @@ int h3_vsa_attention_f16(const h3_attention_cfg* cfg, uint32_t token_count, uint
                     head_limit * blocks * blocks * 4,
                     blocks * 4};
   if ((st = check_bindings(stage, views, need, 6))) return st;
+  if ((st = check_aligned16(stage, {q, k, v}))) return st;  // 16-byte row loads
   if ((st = device_ready(stage))) return st;
   return launched(stage, launch_attention_vsa_f16(
                              *cfg, token_count, heads, static_cast<const uint16_t*>(q.ptr),

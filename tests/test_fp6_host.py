@@ -64,3 +64,21 @@ def test_fp6_workspace_is_checked():
     st = L.h3_attention_i4qk_fp6(ctypes.byref(a), tokens, heads, H.raw_view(0x1000, cap * w // 2 - 1),
                                  big, big, big, big, big, H.raw_view(0x1000, need), None)
     assert st == H.H3_ERR_BINDING and "binding 0" in H.last_error()
+
+
+def test_fp6_and_f16_vsa_refuse_misaligned_rows():
+    heads, tokens = 2, 256
+    cap = H.capacity(tokens)
+    w = heads * 128
+    a = H.AttentionCfg(w, w, w, tokens, cap, 1.0)
+    big, odd = H.raw_view(0x1000, 1 << 28), H.raw_view(0x1008, 1 << 28)
+    L = H.lib()
+    st = L.h3_attention_i4qk_fp6(ctypes.byref(a), tokens, heads, odd, big, big, big, big, big,
+                                 big, None)
+    assert st == H.H3_ERR_ARGUMENT and "not 16-byte aligned" in H.last_error()
+    st = L.h3_attention_i4qk_fp6(ctypes.byref(a), tokens, heads, big, big, big, big, big, big,
+                                 odd, None)
+    assert st == H.H3_ERR_ARGUMENT and "binding 2 is not 16-byte aligned" in H.last_error()
+    v = H.AttentionCfg(w, w, w, 256, 256, 0.088)
+    st = L.h3_vsa_attention_f16(ctypes.byref(v), 256, heads, big, big, odd, big, big, big, None)
+    assert st == H.H3_ERR_ARGUMENT and "binding 2 is not 16-byte aligned" in H.last_error()
