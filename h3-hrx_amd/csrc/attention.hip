@@ -930,6 +930,14 @@ __device__ __forceinline__ v8h v_op_vsa(const char* vst, int n, int half, int w)
                                        16 * ((2 * g + half) ^ ((n >> 2) & 3)));
 }
 
+// A QK MFMA that starts from the bias `magic` and writes its own registers, so the bias stays in
+// place from tile to tile (a builtin MFMA onto a copy of the bias costs 16 moves a tile).
+__device__ __forceinline__ v16i qk_onto_vsa(v4i k, v4i q, const v16i& magic) {
+  v16i d;
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "v"(q), "v"(magic));
+  return d;
+}
+
 // The first tile's QK and dequant.
 __device__ __forceinline__ void first_tile_vsa(const char* kst, const v4i (&qop)[4], float qsl,
                                                State& st, float (&u)[16], int n, int half) {
@@ -958,7 +966,8 @@ __device__ __forceinline__ void first_tile_vsa(const char* kst, const v4i (&qop)
 //                                         the dequant + max of tile j+1 and the raise of m
 template <bool kNext>
 __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const v4i (&qop)[4],
-                                         float qsl, State& st, float (&u)[16], int n, int half) {
+                                         float qsl, State& st, float (&u)[16], int n, int half,
+                                         const v16i& magic) {
   if (__any(st.alpha != 1.0f)) {  // the rescale owed by the last raise of m
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -966,12 +975,9 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
       for (int r = 0; r < 16; ++r) st.acc[db][r] *= st.alpha;
     st.alpha = 1.0f;
   }
-  const v16i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
-                      kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits, kMagicBits,
-                      kMagicBits, kMagicBits, kMagicBits, kMagicBits};
   const float negm = -st.m;
   const float* kss = reinterpret_cast<const float*>(kst + kVsaKRows);
-  v16i s = magic;
+  v16i s;
   v8h pb[2];
   v4i kop[4];
   v8h vop[8];
@@ -986,7 +992,12 @@ __device__ __forceinline__ void step_vsa(const char* kst, const char* vst, const
   for (int c = 0; c < 4; ++c) {
     if (kNext && c + kVsaPf < 4) kop[c + kVsaPf] = k_op_vsa(kst, n, half, c + kVsaPf);
     if (c >= 4 - kVsaPf) vop[c - (4 - kVsaPf)] = v_op_vsa(vst, n, half, c - (4 - kVsaPf));
-    if (kNext) s = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[c], s, 0, 0, 0);
+    if (kNext) {
+      if (c == 0)
+        s = qk_onto_vsa(kop[0], qop[0], magic);
+      else
+        s = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[c], qop[c], s, 0, 0, 0);
+    }
     exp_pair_vsa(u, 2 * c, qsl, negm, pb);
     H3_CHUNK_END();
   }
@@ -1128,11 +1139,12 @@ __device__ __forceinline__ void step_f16(const char* kst, const char* vst, const
 
 template <bool kF16, bool kNext, class QOp>
 __device__ __forceinline__ void vsa_step(const char* kst, const char* vst, const QOp& qop,
-                                         float qsl, State& st, float (&u)[16], int lane) {
+                                         float qsl, State& st, float (&u)[16], int lane,
+                                         const v16i& magic) {
   if constexpr (kF16)
     step_f16<kNext>(kst, vst, qop, qsl, st, u, lane);
   else
-    step_vsa<kNext>(kst, vst, qop, qsl, st, u, lane & 31, lane >> 5);
+    step_vsa<kNext>(kst, vst, qop, qsl, st, u, lane & 31, lane >> 5, magic);
 }
 
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -1196,6 +1208,12 @@ void k_attention_vsa(Args a) {
   st.l = 0.0f;
   st.alpha = 1.0f;
   float u[16] = {};
+  v16i magic = {};  // the int8 form's QK accumulator bias, kept in registers for the whole walk
+  if constexpr (!kF16) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) magic[r] = kMagicBits;
+    asm volatile("" : "+v"(magic));
+  }
 
   const int32_t* route = a.routes + ((size_t)head * a.blocks + cube) * a.blocks;
   auto k0_of = [](uint32_t e) { return (e & kEntryCube) * 64 + ((e >> 14) & 1u) * kVsaKeys; };
@@ -1280,7 +1298,7 @@ void k_attention_vsa(Args a) {
         stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
     stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e2), live_of(e2), vn2);                          \
     const uint32_t e4 = entry(j + 4);                                                        \
-    vsa_step<kF16, true>(kn, vc, qop, qsl, st, u, lane);                                     \
+    vsa_step<kF16, true>(kn, vc, qop, qsl, st, u, lane, magic);                              \
     store_scales_vsa<kF16>(kn2, sg, ks_held, live_of(e2));                                   \
     ks_held = ks_new;                                                                        \
     e2 = e3;                                                                                 \
@@ -1300,7 +1318,8 @@ void k_attention_vsa(Args a) {
 #undef H3_VSA_STEP
     {  // the last tile's PV (stage j % 3)
       const uint32_t r = j % 3;
-      vsa_step<kF16, false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, lane);
+      vsa_step<kF16, false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, lane,
+                            magic);
     }
     step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
   }
