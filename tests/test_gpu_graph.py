@@ -1,8 +1,9 @@
 """The entry points are stream-ordered and capturable (the reference records its dispatch calls
 into graphs and replays them with fixed addresses, docs/shared-hrx.md:102-104): a HIP graph
 captured through torch.cuda.graph around the step's kernels (the fused RoPE quantizers of Q and
-K, the V transpose and the head-major attention), a _ws attention (scale transpose + attention)
-and the VSA attention with a lent workspace, replayed three times with eager work and
+K, the V transpose and the head-major attention), a _ws attention (scale transpose + attention),
+the FP6 int4 attention (conversion + attention), the VSA attention with a lent workspace and
+the f16 VSA attention and runtime, replayed three times with eager work and
 synchronisations between the replays, gives the eager result bit for bit on every replay. The
 captured regions hold only this library's kernels (no memset or library reduction nodes)."""
 import math
@@ -97,6 +98,27 @@ def test_workspace_forms_replay_from_a_graph(dev):
     replay_matches(torch, dev,
                    lambda: H.attention_i8qk_ws(cfg, tokens, heads, qi, qs, ki, ks, vt, out, ws),
                    [out, ws])
+
+
+def test_fp6_int4_attention_replays_from_a_graph(dev):
+    """h3_attention_i4qk_fp6: the conversion into the workspace and the FP6 attention."""
+    import torch
+
+    from test_gpu_fp6 import operands
+    from test_gpu_i4 import pack_i4
+
+    tokens, heads = 900, 2
+    stride = heads * 128
+    cap = H.capacity(tokens)
+    q, k, qs, ks, vt = operands(np.random.default_rng(14), tokens, heads, cap)
+    cfg = H.AttentionCfg(stride, stride, stride, tokens, cap, 1.0)
+    args = [to_dev(pack_i4(q), dev), to_dev(qs, dev), to_dev(pack_i4(k), dev), to_dev(ks, dev),
+            to_dev(vt, dev)]
+    ws = torch.zeros(H.fp6_workspace_bytes(cfg), dtype=torch.uint8, device=dev)
+    out = torch.zeros((tokens, stride), dtype=torch.float16, device=dev)
+    print("graph: attention_i4qk_fp6", flush=True)
+    replay_matches(torch, dev, lambda: H.attention_i4qk_fp6(cfg, tokens, heads, *args, out, ws),
+                   [out])
 
 
 def test_vsa_attention_replays_from_a_graph(dev):
