@@ -752,7 +752,6 @@ constexpr int kVsaF16KStage = kVsaF16KRows + kVsaKeys * 4;        // + c[32]: 83
 constexpr int kVsaF16VStage = kVsaKeys * kVsaF16RowBytes;         // 8192
 constexpr int kVsaF16KLoads = kVsaF16KRows / 1024 / kVsaWaves;    // 4
 constexpr int kVsaF16VLoads = kVsaF16VStage / 1024 / kVsaWaves;   // 4
-constexpr int kVsaF16WaitPrevStep = (kVsaF16KLoads + kVsaF16VLoads) | (7 << 4) | (0 << 8);
 static_assert(kVsaF16VStage == kVsaVStage, "the V stages of both forms are 8 KiB");
 constexpr int kVsaKLoadsMax = kVsaF16KLoads > kVsaKLoads ? kVsaF16KLoads : kVsaKLoads;
 constexpr int kVsaVLoadsMax = kVsaF16VLoads > kVsaVLoads ? kVsaF16VLoads : kVsaVLoads;
@@ -1152,16 +1151,16 @@ __device__ __forceinline__ uint32_t rfl(uint32_t v) { return __builtin_amdgcn_re
 // kHmScales: a.ks is head-major, [kv_head_limit][tokens]; otherwise token-major as the
 // operands' producer writes it, [tokens][kv_head_limit]. kF16: the f16 form (a.qi, a.ki, a.vt
 // are the token-major f16 q, k, v; a.q_row and a.kv_bytes their row pitches in bytes; scores
-// times a.scale), with three workgroups per CU (51.6 KB of LDS each).
+// times a.scale), on two-stage rings so that four workgroups share a CU (35.1 KB of LDS each).
 template <bool kHmScales, bool kF16 = false>
 __global__ __launch_bounds__(kVsaThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_attention_vsa(Args a) {
   __shared__ __attribute__((aligned(16))) char k0s[vsa_kstage<kF16>()];
   __shared__ __attribute__((aligned(16))) char k1s[vsa_kstage<kF16>()];
-  __shared__ __attribute__((aligned(16))) char k2s[vsa_kstage<kF16>()];
+  __shared__ __attribute__((aligned(16))) char k2s[kF16 ? 16 : kVsaKStage];  // int8: 3 stages
   __shared__ __attribute__((aligned(16))) char v0s[kVsaVStage];
   __shared__ __attribute__((aligned(16))) char v1s[kVsaVStage];
-  __shared__ __attribute__((aligned(16))) char v2s[kVsaVStage];
+  __shared__ __attribute__((aligned(16))) char v2s[kF16 ? 16 : kVsaVStage];
   __shared__ uint32_t list[kVsaListMax];
   __shared__ uint32_t wave_counts[kVsaWaves];
 
@@ -1270,56 +1269,90 @@ void k_attention_vsa(Args a) {
     }
     if (count == 0) continue;
 
-    // ---- the pipeline of k_attention over list[0 .. count): tile t is the half-cube list[t]
     auto entry = [&](uint32_t t) { return t < count ? rfl(list[t]) : 0u; };
-    uint32_t e2 = entry(2), e3 = entry(3);
-    {
-      const uint32_t e0 = entry(0), e1 = entry(1);
-      const float ks0 = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
-      const float ks1 = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
-      stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), v0s);
-      stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), v1s);
-      store_scales_vsa<kF16>(k0s, sg, ks0, live_of(e0));
-      store_scales_vsa<kF16>(k1s, sg, ks1, live_of(e1));
-    }
-    float ks_held = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
-    step_barrier<kWaitAll>();
-    if constexpr (kF16)
+    if constexpr (kF16) {
+      // ---- the f16 form on two-stage rings (35 KB of LDS, four workgroups per CU): step j
+      // stages K(j+2) into K(j)'s stage and V(j+1) into V(j-1)'s, with K(j+2)'s key mask (known
+      // from the list, no load), while QK(j+1) and PV(j) run; its barrier waits for all of its
+      // loads, which the next step reads.
+      {
+        const uint32_t e0 = entry(0), e1 = entry(1);
+        stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
+        stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
+        stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), v0s);
+        store_scales_vsa<kF16>(k0s, sg, 1.0f, live_of(e0));
+        store_scales_vsa<kF16>(k1s, sg, 1.0f, live_of(e1));
+      }
+      step_barrier<kWaitAll>();
       first_tile_f16(k0s, qop, qsl, st, u, n, half);
-    else
+      step_barrier<kWaitAll>();
+#define H3_VSA_F16_STEP(ka, kb, va, vb)                                                        \
+  {                                                                                          \
+    const uint32_t ek = entry(j + 2), ev = entry(j + 1);                                     \
+    stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(ek), live_of(ek), ka);                \
+    stage_v_vsa<kF16>(a, sg, kv_head, k0_of(ev), live_of(ev), vb);                           \
+    store_scales_vsa<kF16>(ka, sg, 1.0f, live_of(ek));                                       \
+    vsa_step<kF16, true>(kb, va, qop, qsl, st, u, lane, magic);                              \
+    step_barrier<kWaitAll>();                                                                \
+    ++j;                                                                                     \
+  }
+      const uint32_t steady = count - 1;
+      uint32_t j = 0;
+      for (; j + 2 <= steady;) {
+        H3_VSA_F16_STEP(k0s, k1s, v0s, v1s)
+        H3_VSA_F16_STEP(k1s, k0s, v1s, v0s)
+      }
+      if (j < steady) H3_VSA_F16_STEP(k0s, k1s, v0s, v1s)
+#undef H3_VSA_F16_STEP
+      vsa_step<kF16, false>(nullptr, (j & 1) ? v1s : v0s, qop, qsl, st, u, lane, magic);
+    } else {
+      // ---- the pipeline of k_attention over list[0 .. count): tile t is the half-cube list[t]
+      uint32_t e2 = entry(2), e3 = entry(3);
+      {
+        const uint32_t e0 = entry(0), e1 = entry(1);
+        const float ks0 = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), k0s);
+        const float ks1 = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), k1s);
+        stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e0), live_of(e0), v0s);
+        stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e1), live_of(e1), v1s);
+        store_scales_vsa<kF16>(k0s, sg, ks0, live_of(e0));
+        store_scales_vsa<kF16>(k1s, sg, ks1, live_of(e1));
+      }
+      float ks_held = stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e2), live_of(e2), k2s);
+      step_barrier<kWaitAll>();
       first_tile_vsa(k0s, qop, qsl, st, u, n, half);
-    step_barrier<kWaitAll>();
+      step_barrier<kWaitAll>();
 
-    // One step j: K(j+3) -> kc, V(j+2) -> vn2; QK(j+1) from kn, PV(j) from vc; then the scales
-    // of K(j+2) into kn2.
+      // One step j: K(j+3) -> kc, V(j+2) -> vn2; QK(j+1) from kn, PV(j) from vc; then the scales
+      // of K(j+2) into kn2.
 #define H3_VSA_STEP(kc, kn, kn2, vc, vn2)                                                      \
   {                                                                                          \
-    const float ks_new =                                                                     \
-        stage_k_vsa<kHmScales, kF16>(a, sg, kv_head, k0_of(e3), live_of(e3), kc);            \
-    stage_v_vsa<kF16>(a, sg, kv_head, k0_of(e2), live_of(e2), vn2);                          \
+    const float ks_new = stage_k_vsa<kHmScales, false>(a, sg, kv_head, k0_of(e3), live_of(e3), \
+                                                       kc);                                  \
+    stage_v_vsa<false>(a, sg, kv_head, k0_of(e2), live_of(e2), vn2);                         \
     const uint32_t e4 = entry(j + 4);                                                        \
-    vsa_step<kF16, true>(kn, vc, qop, qsl, st, u, lane, magic);                              \
-    store_scales_vsa<kF16>(kn2, sg, ks_held, live_of(e2));                                   \
+    vsa_step<false, true>(kn, vc, qop, qsl, st, u, lane, magic);                             \
+    store_scales_vsa<false>(kn2, sg, ks_held, live_of(e2));                                  \
     ks_held = ks_new;                                                                        \
     e2 = e3;                                                                                 \
     e3 = e4;                                                                                 \
-    step_barrier<kF16 ? kVsaF16WaitPrevStep : kVsaWaitPrevStep>();                           \
+    step_barrier<kVsaWaitPrevStep>();                                                        \
     ++j;                                                                                     \
   }
-    const uint32_t steady = count - 1;
-    uint32_t j = 0;
-    for (; j + 3 <= steady;) {
-      H3_VSA_STEP(k0s, k1s, k2s, v0s, v2s)
-      H3_VSA_STEP(k1s, k2s, k0s, v1s, v0s)
-      H3_VSA_STEP(k2s, k0s, k1s, v2s, v1s)
-    }
-    if (j < steady) H3_VSA_STEP(k0s, k1s, k2s, v0s, v2s)
-    if (j < steady) H3_VSA_STEP(k1s, k2s, k0s, v1s, v0s)
+      const uint32_t steady = count - 1;
+      uint32_t j = 0;
+      for (; j + 3 <= steady;) {
+        H3_VSA_STEP(k0s, k1s, k2s, v0s, v2s)
+        H3_VSA_STEP(k1s, k2s, k0s, v1s, v0s)
+        H3_VSA_STEP(k2s, k0s, k1s, v2s, v1s)
+      }
+      if (j < steady) H3_VSA_STEP(k0s, k1s, k2s, v0s, v2s)
+      if (j < steady) H3_VSA_STEP(k1s, k2s, k0s, v1s, v0s)
 #undef H3_VSA_STEP
-    {  // the last tile's PV (stage j % 3)
-      const uint32_t r = j % 3;
-      vsa_step<kF16, false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, lane,
-                            magic);
+      {  // the last tile's PV (stage j % 3)
+        const uint32_t r = j % 3;
+        vsa_step<kF16, false>(nullptr, r == 0 ? v0s : r == 1 ? v1s : v2s, qop, qsl, st, u, lane,
+                              magic);
+      }
     }
     step_barrier<kWaitAll>();  // no staging load outlives the run; the stages are reused
   }
@@ -1684,9 +1717,9 @@ hipError_t launch_attention_vsa_f16(const h3_attention_cfg& cfg, uint32_t token_
   a.lengths = lengths;
   a.blocks = cfg.tokens / 64;
   a.scale = cfg.scale;
-  // Generations of resident workgroups as in launch_attention_vsa, three per CU here (LDS).
+  // Generations of resident workgroups as in launch_attention_vsa (four per CU).
   const uint32_t items = a.q_blocks * heads;
-  const uint32_t gen = std::max(1u, 3u * device_cus());
+  const uint32_t gen = std::max(1u, 4u * device_cus());
   for (uint32_t base = 0; base < items; base += gen) {
     a.base = base;
     a.total = std::min(gen, items - base);
