@@ -69,6 +69,21 @@ def test_compact_qkv_half_step_and_row_padding(dev):
     same_bits(run_gemm(dev, a, w, ws, as_, k), O.gemm_i8_qkv(a, w, ws, as_, k))
 
 
+@pytest.mark.parametrize("k", [256, 320, 384, 448, 576])
+def test_compact_qkv_step_counts(dev, k):
+    """K advances 128 bytes a step through two LDS stages: 256-576 bytes are even and odd step
+    counts (2-5), with and without a final 64-byte half step (320, 448, 576), rows padded past K
+    by garbage and a partial last tile in M and in V, bit-exact."""
+    rng = np.random.default_rng(k)
+    m, n, stride = 300, 768, k + 64
+    a = rng.integers(-128, 128, (m, stride), dtype=np.int8)
+    w = rng.integers(-128, 128, (n, stride), dtype=np.int8)
+    ws = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    as_ = rng.uniform(1e-3, 5e-2, m).astype(np.float32)
+    print(f"gemm step-count case k={k}", flush=True)
+    same_bits(run_gemm(dev, a, w, ws, as_, k), O.gemm_i8_qkv(a, w, ws, as_, k))
+
+
 @pytest.mark.parametrize("m", [31104, 129024])
 def test_dit_projection_shape_on_sampled_tokens(dev, m):
     """K = 4096, N = 3*4096 at the BASELINE token counts; every column of 48 sampled tokens
