@@ -32,7 +32,9 @@
 //        (every p >= 0, so the sum of a lane's 16 probabilities bounds each of them; f16
 //        overflow shows as inf). Such a tile takes the exact path: its max is computed, m is
 //        raised, the output accumulators and the sum are rescaled and its probabilities
-//        recomputed. The first key tile always takes it (m starts at -1e30).
+//        recomputed. The first key tile always takes it (m starts at -1e30); in cross-
+//        attention it computes its max before its probabilities instead, since O^T and the sum
+//        are still zero and there is nothing to rescale.
 //   PV   O^T (128 ch x 32 queries) += V^T . P^T on v_mfma_f32_32x32x16_f16, f32 accumulators;
 //        the row sum adds the same f16 probabilities in f32, two at a time (v_dot2 with 1).
 // S^T and P are double-buffered by key-tile parity, so every dependence between the matrix and
@@ -514,6 +516,36 @@ __device__ __forceinline__ void raise_exact(Tile& T, int par, const float* kss, 
   asm volatile("s_nop 7" ::: "memory");  // fresh P before the next MFMA reads it
 }
 
+// The probabilities of a block's first key tile: the exact path with nothing to rescale. The
+// running max is still -1e30 (negm 1e30) and O^T and the row sum are zero, so the rescale of
+// raise_exact multiplies zeros and 0*alpha + sum is the sum: the max is taken first and the
+// probabilities computed once, from the same dequantised scores, with the results of the
+// general path bit for bit and none of its overflowing first pass.
+__device__ __forceinline__ void first_tile(Tile& T, int par, const float* kss, int b,
+                                           uint32_t soff) {
+  float u[4][4];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dequant_quarter(T.s[par], i, scale4(kss, b, i, soff), scale4(kss + kKeys, b, i, soff), u[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, u[i][j]);
+  }
+  tmax = half_swap_max(tmax);
+  T.negm = -fmaxf(-1.0e30f, tmax * T.qsl);
+  float ts = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w[2];
+    exparg_quarter(u[i], T.qsl, T.negm, w);
+    exp2_quarter(w);
+    put_quarter(T.p[par], i, w);
+    ts = sum_words(w, ts);
+  }
+  T.l = ts;
+  asm volatile("s_nop 7" ::: "memory");  // fresh P before the next MFMA reads it
+}
+
 // The first LDS operands of a sub-step, read during the sub-step before it: the four K chunks of
 // its QK and the scales of its first two quarters.
 struct Pre {
@@ -565,7 +597,7 @@ __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, in
 // exponentials), with the scales of quarters 2 and 3 read two quarters ahead. Each quarter adds
 // its probabilities to the lane's tile sum right away (f32 dot products), so the overflow check
 // after the last chunk waits on two instructions only.
-template <int kPar, bool kQK, bool kPV, bool kSM, bool kFp6, typename Stage>
+template <int kPar, bool kQK, bool kPV, bool kSM, bool kFp6, bool kFirst = false, typename Stage>
 __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int sb, Tile& T,
                                          const Lanes& ln, int half, const v16i& magic, Pre& pre,
                                          Stage&& stage) {
@@ -622,7 +654,7 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
       const int v = c - 4;
       pv_mfma(v & 3, vop[v], T.p[kPar][v >> 2]);
     }
-    if (kSM) {
+    if (kSM && !kFirst) {
       // quarter c/3: dequantisation, exponent arguments, exponentials (and its share of the tile
       // sum, two dot products into f32)
       const int i = c / 3, phase = c % 3;
@@ -643,7 +675,9 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
   }
   if (kQK && !kPV)  // the next sub-step's vector ALU reads this S^T at once: cover the latency
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  if (kSM) {
+  if constexpr (kSM && kFirst) {
+    first_tile(T, kSm, kss, sb, ln.s);
+  } else if (kSM) {
     if (__builtin_expect(__any(!(ts <= kSumLimit)), 0))
       raise_exact(T, kSm, kss, sb, ln.s, half);
     else
@@ -817,7 +851,11 @@ void k_attention_hm(Geometry g) {
                                   [&](int c, Pre& next) {
     if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, k0s, 1, s0s, 0, ln);
   });
-  sub_step<1, true, false, true, kFp6>(nullptr, s0s, 0, T, ln, half, magic, pre, [&](int c, Pre& next) {
+  // The first tile's own path pays where blocks are short (cross-attention's few key tiles);
+  // self-attention keeps the general path, whose code measured marginally faster at long
+  // sequences. The results are the same bits either way.
+  sub_step<1, true, false, true, kFp6, kCross>(nullptr, s0s, 0, T, ln, half, magic, pre,
+                                                [&](int c, Pre& next) {
     if (c == 0) store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
     if (c == kBarrierChunk) step_barrier<kWaitPrevStep<kCross>>();
     next_step_reads<kFp6>(c, next, k1s, s0s, ln);
