@@ -4,6 +4,7 @@
 // dispatch::emit checks bindings before dispatch (src/dispatch.rs:264-276) and as each Loom
 // kernel's config.decl ranges bound its specialisation (kernels/*.loom). A failing check
 // returns its status, records a message for h3_last_error(), and launches nothing.
+#include <algorithm>
 #include <cstdarg>
 #include <initializer_list>
 #include <cstdio>
@@ -200,17 +201,30 @@ int check_attention_cfg(const char* stage, const h3_attention_cfg* cfg, uint32_t
                 cfg->tokens);
   if (heads < 1 || heads > 65535)
     return set_error(H3_ERR_ARGUMENT, "%s: heads %u outside [1, 65535]", stage, heads);
-  const size_t head_limit = cfg->out_stride / 128;
-  if (cfg->q_stride / 128 < head_limit)
-    return set_error(H3_ERR_CONFIG, "%s: q_stride %u holds fewer heads than out_stride %u", stage,
-                cfg->q_stride, cfg->out_stride);
   return H3_OK;
+}
+
+// The heads a launch touches. Workgroup row y of the [.., heads] workload takes key/value head
+// y % (kv_stride/128) and query head kv_head % (out_stride/128)
+// (attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:300-340, attention_i8qk_family.loom:77-91), so
+// the key/value heads 0..kv-1 and the query heads 0..q-1 are read, with kv = min(heads,
+// kv_stride/128) and q = min(kv, out_stride/128). A padded output pitch (out_stride above
+// heads*128, src/stack.rs:751-758) therefore reads no more query heads than the launch has; the
+// binding extents below follow these counts, as the reference's caller sizes its operands by
+// the workload's heads (src/stack.rs:1830-1837).
+struct TouchedHeads {
+  size_t q, kv;
+};
+TouchedHeads touched_heads(const h3_attention_cfg& cfg, uint32_t heads) {
+  const size_t kv = std::min<size_t>(heads, cfg.kv_stride / 128);
+  return {std::min<size_t>(kv, cfg.out_stride / 128), kv};
 }
 
 int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t token_count,
                      uint32_t heads, h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
                      h3_view out, hipStream_t stream, int mode, float skip_tau = 0.0f,
-                     h3_view routes = {}, h3_view lengths = {}, h3_view workspace = {}) {
+                     h3_view routes = {}, h3_view lengths = {}, h3_view workspace = {},
+                     bool static_workspace = false) {
   const bool head_major = mode == kModeHeadI8;
   const bool vsa = mode == kModeTokenI8Vsa;
   const bool fp6 = mode == kModeTokenI4Fp6;
@@ -218,34 +232,54 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
   int st = check_attention_cfg(stage, cfg, token_count, heads);
   if (st) return st;
   const size_t cap = cfg->token_capacity;
-  const size_t head_limit = cfg->out_stride / 128, kv_head_limit = cfg->kv_stride / 128;
-  // The extents the kernel addresses: head-major views [head_limit*cap][32] i32 and
-  // [head_limit][cap] f32 (attention_i8qkhm...loom:394-401); token-major views
-  // [cap][q_stride/4] i32 and [cap][head_limit] f32 (attention_i8qk_family.loom:117-121).
+  const TouchedHeads th = touched_heads(*cfg, heads);
+  // Token-major code rows hold q_stride/128 query heads; a launch whose query heads lie past a
+  // row would read the next token's codes (the reference assumes it away,
+  // attention_i8qk_family.loom:160-170).
+  if (!head_major && th.q > cfg->q_stride / 128)
+    return set_error(H3_ERR_CONFIG, "%s: q_stride %u holds %u query heads, the launch reads %zu",
+                     stage, cfg->q_stride, cfg->q_stride / 128, th.q);
+  // The extents the kernel addresses. Head-major: codes [head*cap + t][32] i32 and scales
+  // [head][cap] f32 of the touched heads (attention_i8qkhm...loom:394-401). Token-major: whole
+  // rows [cap][q_stride/4] i32 and [cap][q_stride/128] f32, and the same for K
+  // (attention_i8qk_family.loom:108-113). V^T: the 128 rows of every touched key/value head,
+  // [kv_stride][cap] f16. Output: rows < token_count at out_stride, the touched heads' columns.
   size_t need[6];
   if (head_major) {
-    need[0] = head_limit * cap * 128;
-    need[1] = head_limit * cap * 4;
-    need[2] = kv_head_limit * cap * 128;
-    need[3] = kv_head_limit * cap * 4;
+    need[0] = th.q * cap * 128;
+    need[1] = th.q * cap * 4;
+    need[2] = th.kv * cap * 128;
+    need[3] = th.kv * cap * 4;
   } else {
     need[0] = cap * cfg->q_stride / code_div;
-    need[1] = cap * head_limit * 4;
+    need[1] = cap * (cfg->q_stride / 128) * 4;
     need[2] = cap * cfg->kv_stride / code_div;
-    need[3] = cap * kv_head_limit * 4;
+    need[3] = cap * (cfg->kv_stride / 128) * 4;
   }
-  need[4] = (size_t)cfg->kv_stride * cap * 2;
-  need[5] = (size_t)token_count * cfg->out_stride * 2;
+  need[4] = th.kv * 128 * cap * 2;
+  need[5] = ((size_t)(token_count - 1) * cfg->out_stride + th.q * 128) * 2;
   h3_view views[6] = {qi, qs, ki, ks, vt, out};
   st = check_bindings(stage, views, need, 6);
   if (st) return st;
-  // A workspace (token-major operands) receives a head-major copy of the key scales, which the
-  // kernel then reads; without one it reads them token-major. Nothing is allocated either way.
+  // A workspace (token-major operands) receives a head-major copy of the key scales (or the FP6
+  // operands), which the kernel then reads; without one it reads them token-major. Nothing is
+  // allocated either way. A lent workspace is device memory like any binding and goes through
+  // the same checks; the library's own static array (h3_attention_i8qk_static) is known good.
   if (workspace.ptr) {
     const size_t ws_need = fp6 ? fp6_layout(*cfg).bytes : scales_workspace_bytes(*cfg);
-    if (workspace.bytes < ws_need)
-      return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
-                       stage, workspace.bytes, ws_need);
+    if (static_workspace) {
+      if (workspace.bytes < ws_need)
+        return set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
+                         stage, workspace.bytes, ws_need);
+    } else {
+      h3_view wv[1] = {workspace};
+      size_t wneed[1] = {ws_need};
+      if ((st = check_bindings(stage, wv, wneed, 1)))
+        return st == H3_ERR_BINDING
+                   ? set_error(H3_ERR_BINDING, "%s: workspace is %zu bytes, the kernel addresses %zu",
+                               stage, workspace.bytes, ws_need)
+                   : st;
+    }
   }
   if (vsa) {
     // kernels/vsa_attention_8.loom:145-150: blocks = tokens / 64, routes [heads][blocks][blocks]
@@ -255,7 +289,7 @@ int attention_common(const char* stage, const h3_attention_cfg* cfg, uint32_t to
                        stage, cfg->tokens);
     const size_t blocks = cfg->tokens / 64;
     h3_view rv[2] = {routes, lengths};
-    size_t rneed[2] = {head_limit * blocks * blocks * 4, blocks * 4};
+    size_t rneed[2] = {th.q * blocks * blocks * 4, blocks * 4};
     if ((st = check_bindings(stage, rv, rneed, 2))) return st;
     if ((st = device_ready(stage))) return st;
     return launched(stage, launch_attention_vsa(*cfg, token_count, heads,
@@ -345,6 +379,13 @@ int transpose_common(const char* stage, const h3_transpose_cfg* cfg, uint32_t la
 }
 
 }  // namespace
+
+int attention_i8qk_static_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                             h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                             h3_view out, h3_view workspace, hipStream_t stream) {
+  return attention_common("attention_i8qk_static", cfg, token_count, heads, qi, qs, ki, ks, vt,
+                          out, stream, kModeTokenI8, 0.0f, {}, {}, workspace, true);
+}
 
 int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
@@ -869,13 +910,16 @@ int h3_vsa_attention_f16(const h3_attention_cfg* cfg, uint32_t token_count, uint
     return set_error(H3_ERR_CONFIG, "%s: tokens %u is not 64 * blocks with blocks <= 16384",
                      stage, cfg->tokens);
   const size_t cap = cfg->token_capacity, blocks = cfg->tokens / 64;
-  const size_t head_limit = cfg->out_stride / 128;
+  const TouchedHeads th = touched_heads(*cfg, heads);
+  if (th.q > cfg->q_stride / 128)
+    return set_error(H3_ERR_CONFIG, "%s: q_stride %u holds %u query heads, the launch reads %zu",
+                     stage, cfg->q_stride, cfg->q_stride / 128, th.q);
   h3_view views[6] = {q, k, v, out, routes, lengths};
   size_t need[6] = {cap * cfg->q_stride * 2,
                     cap * cfg->kv_stride * 2,
                     cap * cfg->kv_stride * 2,
-                    (size_t)token_count * cfg->out_stride * 2,
-                    head_limit * blocks * blocks * 4,
+                    ((size_t)(token_count - 1) * cfg->out_stride + th.q * 128) * 2,
+                    th.q * blocks * blocks * 4,
                     blocks * 4};
   if ((st = check_bindings(stage, views, need, 6))) return st;
   if ((st = check_aligned16(stage, {q, k, v}))) return st;  // 16-byte row loads

@@ -117,6 +117,12 @@ struct Args {
   uint32_t heads;     // workload heads (grid y of the reference)
   uint32_t kv_head_limit;
   uint32_t head_limit;
+  // Token-major Q scales [capacity][q_scale_pitch]: the heads a q_stride-wide code row holds
+  // (q_stride/128), which is what the quantizer writes per token. The reference's token-major
+  // kernel reads them at out_stride/128 instead (attention_i8qk_family.loom:87, 112, 197); the
+  // two agree unless the output pitch is padded (src/stack.rs:751-758), where its reading would
+  // take another (token, head)'s scale.
+  uint32_t q_scale_pitch;
   uint32_t total;      // q_blocks * heads
   uint32_t per_xcd;    // ceil(total / 8)
   float neg_tau;       // tile skip (kTokenI4Skip): -tau * log2(e)
@@ -613,7 +619,7 @@ void k_attention(Args a) {
     for (int dc = 0; dc < 4; ++dc) qop[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
   }
   const float qsv = kHeadMajor ? a.qs[(size_t)head * a.capacity + q_read]
-                               : a.qs[(size_t)q_read * a.head_limit + head];
+                               : a.qs[(size_t)q_read * a.q_scale_pitch + head];
   // log2 units; int4 scores arrive 256x (the widened codes are 16x each)
   const float qsl = isI4(kMode) ? qsv * kLog2e * (1.0f / 256.0f) : qsv * kLog2e;
 
@@ -1195,7 +1201,7 @@ void k_attention_vsa(Args a) {
     const int32_t* src = a.qi + (size_t)q_read * (a.q_row / 4) + head * 32;
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) qop[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
-    qsl = a.qs[(size_t)q_read * a.head_limit + head] * kLog2e;
+    qsl = a.qs[(size_t)q_read * a.q_scale_pitch + head] * kLog2e;
   }
 
   State st;
@@ -1567,6 +1573,7 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
   a.heads = heads;
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
+  a.q_scale_pitch = cfg.q_stride / 128;
   const bool hm_scales = workspace && mode != kHeadI8;
   if (hm_scales) {  // token-major codes, head-major copy of the key scales
     float* ks_hm = static_cast<float*>(workspace);
@@ -1635,6 +1642,7 @@ hipError_t launch_attention_cross(const h3_cross_cfg& cfg, const int32_t* qi, co
   a.heads = cfg.q_heads;
   a.kv_head_limit = cfg.kv_heads;
   a.head_limit = cfg.q_heads;
+  a.q_scale_pitch = cfg.q_heads;
   a.total = a.q_blocks * cfg.q_heads;
   a.per_xcd = (a.total + 7) / 8;
   hipLaunchKernelGGL(k_attention_cross, dim3(a.per_xcd * 8), dim3(kThreads), 0, stream, a);
@@ -1667,6 +1675,7 @@ hipError_t launch_attention_vsa(const h3_attention_cfg& cfg, uint32_t token_coun
   a.heads = heads;
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
+  a.q_scale_pitch = cfg.q_stride / 128;
   a.routes = routes;
   a.lengths = lengths;
   a.blocks = cfg.tokens / 64;
@@ -1713,6 +1722,7 @@ hipError_t launch_attention_vsa_f16(const h3_attention_cfg& cfg, uint32_t token_
   a.heads = heads;
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
+  a.q_scale_pitch = cfg.q_stride / 128;
   a.routes = routes;
   a.lengths = lengths;
   a.blocks = cfg.tokens / 64;

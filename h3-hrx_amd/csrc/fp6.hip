@@ -79,7 +79,9 @@ size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 Fp6Layout fp6_layout(const h3_attention_cfg& cfg) {
   const size_t cap = cfg.token_capacity;
-  const size_t hq = cfg.out_stride / 128, hk = cfg.kv_stride / 128;
+  // Every head of a code row is converted: q_stride/128 query heads, kv_stride/128 key heads
+  // (the launch reads a subset of them, checked by the caller).
+  const size_t hq = cfg.q_stride / 128, hk = cfg.kv_stride / 128;
   Fp6Layout L;
   L.q = 0;
   L.k = L.q + round256(hq * cap * 128);
@@ -95,9 +97,10 @@ hipError_t launch_attention_i4_fp6(const h3_attention_cfg& cfg, uint32_t token_c
                                    uint16_t* out, void* workspace, hipStream_t stream) {
   const Fp6Layout L = fp6_layout(cfg);
   char* ws = static_cast<char*>(workspace);
-  const uint32_t hq = cfg.out_stride / 128, hk = cfg.kv_stride / 128;
+  const uint32_t hq = cfg.q_stride / 128, hk = cfg.kv_stride / 128;
   const uint32_t tokens = cfg.tokens, cap = cfg.token_capacity;
-  // Q rows: the head_limit query heads of the q_stride-wide rows (q_stride/2 bytes each)
+  // Q rows: every query head of the q_stride-wide rows (q_stride/2 bytes each), with the Q
+  // scales [tokens][q_stride/128] the quantizer writes
   const size_t nq = (size_t)tokens * hq * 4, nk = (size_t)tokens * hk * 4;
   hipLaunchKernelGGL(k_i4_fp6_rows, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, stream,
                      reinterpret_cast<const uint4*>(qi), cfg.q_stride / 32, hq, tokens, cap,

@@ -136,6 +136,12 @@ hipError_t launch_attention_vsa_f16(const h3_attention_cfg& cfg, uint32_t token_
 int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
                         h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                         h3_view routes, h3_view lengths, h3_view workspace, hipStream_t stream);
+// h3_attention_i8qk_ws on the library's own static scratch array (noalloc.hip): the same
+// checks, except that the workspace, a device symbol's address, skips the runtime's pointer
+// query.
+int attention_i8qk_static_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint32_t heads,
+                             h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt,
+                             h3_view out, h3_view workspace, hipStream_t stream);
 // VSA operations (vsa.hip)
 hipError_t launch_vsa_gather(uint32_t tokens, uint32_t padded, uint32_t width, const int32_t* src,
                              const uint16_t* x, uint16_t* y, hipStream_t stream);

@@ -67,6 +67,6 @@ extern "C" int h3_attention_i8qk_static(const h3_attention_cfg* cfg, uint32_t to
   void* ptr = nullptr;
   int st = device_scratch(stage, &ptr);
   if (st) return st;
-  return h3_attention_i8qk_ws(cfg, token_count, heads, qi, qs, ki, ks, vt, out,
-                              h3_view{ptr, kScratchBytes}, stream);
+  return attention_i8qk_static_ws(cfg, token_count, heads, qi, qs, ki, ks, vt, out,
+                                  h3_view{ptr, kScratchBytes}, reinterpret_cast<hipStream_t>(stream));
 }

@@ -22,6 +22,10 @@ float config_f32(double v) {
   return strtof(buf, nullptr);
 }
 
+// gemm_pitch(k, 16) (src/model.rs:74-85): a 16-bit row whose bytes are a multiple of 1024 is
+// padded by 128 elements, so the GEMM's row stride avoids the same-channel conflicts.
+uint32_t gemm_pitch16(uint32_t k) { return (2 * k) % 1024 == 0 ? k + 128 : k; }
+
 }  // namespace
 }  // namespace h3
 
@@ -128,10 +132,10 @@ int h3_stack_build(const h3_stack_dims* dims, h3_stack** out) {
   s->prep_k = s->prep_q;
   s->prep_k.extra_scale = 1.0f;  // "the K operand differs only in its head offset" (626-632)
   if (s->fused) s->prep_k.head_offset = inner;
-  // src/stack.rs:745-766
+  // src/stack.rs:745-766 (out_stride: the padded pitch on the direct-attention route)
   s->attention.q_stride = inner;
   s->attention.kv_stride = inner;
-  s->attention.out_stride = inner;
+  s->attention.out_stride = dims->direct_attn ? gemm_pitch16(inner) : inner;
   s->attention.tokens = t;
   s->attention.token_capacity = s->capacity;
   s->attention.scale = config_f32(1.0 / std::sqrt(128.0));
@@ -227,7 +231,7 @@ int h3_stack_attend_fused(h3_stack* s, uint32_t t, h3_view fused, h3_view qnorm,
   if ((st = require(stage, 0, fused, rows * qkv * 2)) || (st = require(stage, 1, qnorm, 128 * 4)) ||
       (st = require(stage, 1, knorm, 128 * 4)) || (st = require(stage, 2, cos_t, rows * 48 * 4)) ||
       (st = require(stage, 3, sin_t, rows * 48 * 4)) ||
-      (st = require("attention", 5, out, rows * inner * 2)))
+      (st = require("attention", 5, out, rows * s->attention.out_stride * 2)))
     return st;
   // Three branches (src/stack.rs:1751-1813): Q on the caller's stream, K and the V transpose on
   // the side streams, all joined before the attention.
@@ -273,7 +277,7 @@ int h3_stack_attend_compact(h3_stack* s, uint32_t t, h3_view compact, h3_view qn
   const char* stage = "fused attention operands";
   int st;
   if ((st = require(stage, 0, compact, vt_offset + vt_bytes)) ||
-      (st = require("attention", 5, out, rows * inner * 2)))
+      (st = require("attention", 5, out, rows * s->attention.out_stride * 2)))
     return st;
   // src/stack.rs:643-648: Q/K rows of 2*inner elements, f16 (the projection's output)
   h3_prepare_cfg pq = s->prep_q, pk = s->prep_k;
@@ -304,7 +308,7 @@ int h3_stack_attend(h3_stack* s, uint32_t t, h3_view q, h3_view k, h3_view v, h3
   if ((st = require("attention operands", 0, q, rows * inner * 2)) ||
       (st = require("attention operands", 0, k, rows * inner * 2)) ||
       (st = require("attention operands", 0, v, rows * inner * 2)) ||
-      (st = require("attention", 5, out, rows * inner * 2)))
+      (st = require("attention", 5, out, rows * s->attention.out_stride * 2)))
     return st;
   h3_prepare_cfg pq = s->prep_q, pk = s->prep_k;
   pq.row_stride = pk.row_stride = (uint32_t)inner;  // separate Q/K buffers (src/stack.rs:609-612)

@@ -186,6 +186,8 @@ pub struct H3StackDims {
     pub elem: u32,
     pub ksmooth: c_int,
     pub fused: c_int,
+    /// f16 GEMM activations: the attention output at gemm_pitch(inner, 16) (src/stack.rs:751-758).
+    pub direct_attn: c_int,
 }
 
 #[repr(C)]
@@ -273,13 +275,15 @@ extern "C" {
     pub fn h3_attention_i4qks_ws(cfg: *const H3AttentionSkipCfg, token_count: u32, heads: u32,
                                  qi: H3View, qs: H3View, ki: H3View, ks: H3View, vt: H3View,
                                  out: H3View, workspace: H3View, stream: H3Stream) -> c_int;
-    /// `h3_attention_i8qk_ws` with the library's static 8 MiB device array as the workspace:
-    /// allocates nothing, for callers that cannot; (kv_stride/128)·tokens ≤ 2,097,152, and
-    /// calls that overlap on one GPU race on the array.
+    /// `h3_attention_i4qk`'s bindings and results (to the north-star tolerance) on the FP6 MFMA:
+    /// the int4 codes are converted into a lent workspace of `h3_fp6_workspace_bytes(cfg)` bytes.
     pub fn h3_attention_i4qk_fp6(cfg: *const H3AttentionCfg, token_count: u32, heads: u32,
                                  qi: H3View, qs: H3View, ki: H3View, ks: H3View, vt: H3View,
                                  out: H3View, workspace: H3View, stream: H3Stream) -> c_int;
     pub fn h3_fp6_workspace_bytes(cfg: *const H3AttentionCfg) -> usize;
+    /// `h3_attention_i8qk_ws` with the library's static 8 MiB device array as the workspace:
+    /// allocates nothing, for callers that cannot; (kv_stride/128)·tokens ≤ 2,097,152, and
+    /// calls that overlap on one GPU race on the array.
     pub fn h3_attention_i8qk_static(cfg: *const H3AttentionCfg, token_count: u32, heads: u32,
                                     qi: H3View, qs: H3View, ki: H3View, ks: H3View, vt: H3View,
                                     out: H3View, stream: H3Stream) -> c_int;
@@ -399,7 +403,7 @@ mod tests {
         assert_eq!(size_of::<H3AttentionSkipCfg>(), 28);
         assert_eq!(size_of::<H3CrossCfg>(), 28);
         assert_eq!(size_of::<H3VsaCfg>(), 28);
-        assert_eq!(size_of::<H3StackDims>(), 24);
+        assert_eq!(size_of::<H3StackDims>(), 28);
     }
 
     #[test]

@@ -116,6 +116,7 @@ class StackDims(ctypes.Structure):
         ("elem", ctypes.c_uint32),
         ("ksmooth", ctypes.c_int),
         ("fused", ctypes.c_int),
+        ("direct_attn", ctypes.c_int),
     ]
 
 
@@ -485,8 +486,9 @@ class Stack:
     attend_fused (prepare_fused_operands + attention) or attend (the separate route)."""
 
     def __init__(self, heads: int, tokens: int, eps: float = 1e-5, elem: int = H3_ELEM_F16,
-                 ksmooth: bool = False, fused: bool = True):
-        self.dims = StackDims(heads, tokens, eps, elem, int(ksmooth), int(fused))
+                 ksmooth: bool = False, fused: bool = True, direct_attn: bool = False):
+        self.dims = StackDims(heads, tokens, eps, elem, int(ksmooth), int(fused),
+                              int(direct_attn))
         handle = ctypes.c_void_p()
         check(lib().h3_stack_build(ctypes.byref(self.dims), ctypes.byref(handle)))
         self.handle = handle

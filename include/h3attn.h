@@ -235,7 +235,16 @@ int h3_rope_dit_tables(const double *pos, size_t rows, const float *inv_freq, fl
  *   tokens          [1, 1048576): keys (and query rows) of the sequence
  *   token_capacity  multiple of 16 in [32, 1048576), >= tokens
  *   scale           declared and unused, as in the reference (the softmax scale rides in
- *                   Q's extra_scale, src/stack.rs:622-625). */
+ *                   Q's extra_scale, src/stack.rs:622-625).
+ * Heads: the launch's `heads` rows take key/value head y % (kv_stride/128) and query head
+ * kv_head % (out_stride/128) (attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:300-340), so it reads
+ * kv = min(heads, kv_stride/128) key/value heads and q = min(kv, out_stride/128) query heads.
+ * out_stride may exceed heads*128: the reference's direct-attention pitch (src/stack.rs:751-758,
+ * gemm_pitch in src/model.rs:74-85, e.g. q/kv 7168, out 7296 at 56 heads) leaves the columns
+ * past the touched heads unwritten. Bindings are checked against what the launch addresses:
+ * head-major Q codes/scales q*token_capacity rows, K kv*token_capacity rows; token-major whole
+ * rows of token_capacity; V^T kv*128 rows of token_capacity; out (token_count-1)*out_stride +
+ * q*128 elements. Token-major launches need q <= q_stride/128. */
 typedef struct {
   uint32_t q_stride;
   uint32_t kv_stride;
@@ -257,8 +266,11 @@ int h3_attention_i8qkhm(const h3_attention_cfg *cfg, uint32_t token_count, uint3
                         h3_stream stream);
 
 /* h3_attention_i8qk (kernels/attention_i8qk_family.loom: attention_i8qk_mha_lds_f16_wmma): the
- * same attention over token-major operands: qi [capacity][q_stride/4] i32, qs [capacity][heads],
- * ki [capacity][kv_stride/4], ks [capacity][heads]. */
+ * same attention over token-major operands: qi [capacity][q_stride/4] i32,
+ * qs [capacity][q_stride/128], ki [capacity][kv_stride/4], ks [capacity][kv_stride/128]. The Q
+ * scales are read at the pitch the quantizer writes them, q_stride/128 heads per token; the
+ * reference's kernel reads them at out_stride/128 (attention_i8qk_family.loom:87, 112, 197),
+ * which differs only under a padded output pitch, where it would read another row's scale. */
 int h3_attention_i8qk(const h3_attention_cfg *cfg, uint32_t token_count, uint32_t heads,
                       h3_view qi, h3_view qs, h3_view ki, h3_view ks, h3_view vt, h3_view out,
                       h3_stream stream);
@@ -562,6 +574,11 @@ typedef struct {
   uint32_t elem;  /* element format of the fused QKV projection */
   int ksmooth;    /* H3_KSMOOTH=1: K-mean smoothing on (separate, unfused route) */
   int fused;      /* H3_FUSED_OPERANDS != 0: fused RoPE+quantize operands */
+  int direct_attn; /* f16 GEMM activations: the attention writes the out projection's operand
+                    * directly, at the padded pitch gemm_pitch(inner, 16) = inner + 128 when
+                    * inner*2 is a multiple of 1024, else inner (src/stack.rs:408, 751-758,
+                    * 817-822; src/model.rs:74-85). The output binding of the attend calls is
+                    * then [t][pitch] f16, and the pad columns are never written. */
 } h3_stack_dims;
 
 typedef struct h3_stack h3_stack;

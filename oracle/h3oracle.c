@@ -215,6 +215,17 @@ void h3o_colmean_f32(const uint16_t *x, int fmt, int tokens, int width, int row_
 void h3o_rope_qknorm_f16(const uint16_t *x, int fmt, int tokens, int row_stride, int head_offset,
                          int heads, const float *weight, const float *cos_t, const float *sin_t,
                          float eps, uint16_t *out, int out_stride) {
+  h3o_rope_qknorm_f16_ulps(x, fmt, tokens, row_stride, head_offset, heads, weight, cos_t, sin_t,
+                           eps, out, out_stride, 0);
+}
+
+/* The same with r moved by r_ulps units in the last place (nextafterf, r_ulps in [-8, 8]):
+ * the sensitivity of the route's outputs to an rsqrt that is not correctly rounded, as the
+ * reference's scalar.rsqrtf (prepare_qk_rope_i8hm.loom:117) need not be. */
+void h3o_rope_qknorm_f16_ulps(const uint16_t *x, int fmt, int tokens, int row_stride,
+                              int head_offset, int heads, const float *weight, const float *cos_t,
+                              const float *sin_t, float eps, uint16_t *out, int out_stride,
+                              int r_ulps) {
   float v[128], xn[128], part[32], nxt[32];
   for (int t = 0; t < tokens; ++t) {
     const float *cs = cos_t + (size_t)t * 48;
@@ -235,6 +246,8 @@ void h3o_rope_qknorm_f16(const uint16_t *x, int fmt, int tokens, int row_stride,
       float me = ms + eps;
       float sq = sqrtf(me);
       float r = 1.0f / sq;
+      for (int u = 0; u < r_ulps && u < 8; ++u) r = nextafterf(r, INFINITY);
+      for (int u = 0; u > r_ulps && u > -8; --u) r = nextafterf(r, 0.0f);
       for (int c = 0; c < 128; ++c) {
         float nv = v[c] * r;
         xn[c] = nv * weight[c];

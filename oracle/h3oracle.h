@@ -136,6 +136,10 @@ void h3o_colmean_f32(const uint16_t *x, int fmt, int tokens, int width, int row_
 void h3o_rope_qknorm_f16(const uint16_t *x, int fmt, int tokens, int row_stride, int head_offset,
                          int heads, const float *weight, const float *cos_t, const float *sin_t,
                          float eps, uint16_t *out, int out_stride);
+void h3o_rope_qknorm_f16_ulps(const uint16_t *x, int fmt, int tokens, int row_stride,
+                              int head_offset, int heads, const float *weight, const float *cos_t,
+                              const float *sin_t, float eps, uint16_t *out, int out_stride,
+                              int r_ulps);
 
 /* The reference's f64 RMSNorm+RoPE oracle (tests/kernels.rs:1146-1180), f64 out. */
 void h3o_rope_qknorm_f64(const uint16_t *x, int fmt, int tokens, int row_stride, int head_offset,

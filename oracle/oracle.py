@@ -60,6 +60,9 @@ def lib():
         L.h3o_rope_qknorm_f16.argtypes = [u16, c_int, c_int, c_int, c_int, c_int, f32, f32, f32,
                                           c_float, u16, c_int]
         L.h3o_rope_qknorm_f16.restype = None
+        L.h3o_rope_qknorm_f16_ulps.argtypes = [u16, c_int, c_int, c_int, c_int, c_int, f32, f32,
+                                               f32, c_float, u16, c_int, c_int]
+        L.h3o_rope_qknorm_f16_ulps.restype = None
         L.h3o_rope_qknorm_f64.argtypes = [u16, c_int, c_int, c_int, c_int, c_int, f32, f32, f32,
                                           c_double, f64]
         L.h3o_rope_qknorm_f64.restype = None
@@ -203,12 +206,17 @@ def colmean(x_bits: np.ndarray, fmt: int, tokens: int, width: int, row_stride: i
 
 
 def rope_qknorm_f16(x_bits, fmt, tokens, row_stride, head_offset, heads, weight, cos_t, sin_t,
-                    eps) -> np.ndarray:
+                    eps, r_ulps: int = 0) -> np.ndarray:
+    """RMSNorm + RoPE to f16 in this build's fixed fp32 order; r_ulps moves the RMS reciprocal
+    by that many units in the last place (a sensitivity probe for an rsqrt that is not correctly
+    rounded)."""
     out = np.zeros((tokens, heads * 128), np.uint16)
-    lib().h3o_rope_qknorm_f16(np.ascontiguousarray(x_bits, np.uint16), fmt, tokens, row_stride,
-                              head_offset, heads, np.ascontiguousarray(weight, np.float32),
-                              np.ascontiguousarray(cos_t, np.float32),
-                              np.ascontiguousarray(sin_t, np.float32), eps, out, heads * 128)
+    lib().h3o_rope_qknorm_f16_ulps(np.ascontiguousarray(x_bits, np.uint16), fmt, tokens,
+                                   row_stride, head_offset, heads,
+                                   np.ascontiguousarray(weight, np.float32),
+                                   np.ascontiguousarray(cos_t, np.float32),
+                                   np.ascontiguousarray(sin_t, np.float32), eps, out, heads * 128,
+                                   int(r_ulps))
     return out
 
 

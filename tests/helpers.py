@@ -138,3 +138,50 @@ def fp6_decode_rows(rows):
             c |= (q[..., bit // 64 + 1] << np.uint64(64 - bit % 64)) & np.uint64(63)
         vals[..., i] = e2m3_value(c.astype(np.int64))
     return vals.reshape(-1, 128)
+
+
+# ---- inputs whose scores rise at every 32-key tile (the exact path at every tile)
+
+LOG2E = 1.4426950408889634
+
+
+def rising_scores(rng, tokens, rise=(5.0, 7.0), spread=0.5):
+    """Score targets in log2 units: key j gets base(j // 32) + e_j, e_j in [0, spread), where
+    the bases of consecutive 32-key tiles step up by rise[0]..rise[1] (a different step each
+    tile). With rise[0] - spread > 4, each of a tile's probabilities against the max of all
+    earlier keys exceeds 2^4, so any 16 of them sum past 2^8."""
+    tiles = (tokens + 31) // 32
+    steps = rng.uniform(rise[0], rise[1], tiles)
+    base = 1.0 + np.concatenate([[0.0], np.cumsum(steps)[:-1]])
+    return base[np.arange(tokens) // 32] + rng.uniform(0.0, spread, tokens)
+
+
+def rank1_operands(rng, q_heads, q_tokens, q_cap, kv_heads, kv_tokens, kv_cap, code_max=20,
+                   mult_max=(3, 6), gain=(1.0, 1.25)):
+    """Codes of rank one, Q rows a_q * u and K rows b_j * w (u, w random vectors in
+    [-code_max, code_max] with u.w > 0, integer multipliers a, b >= 1), so S_qj = a_q b_j (u.w)
+    exactly, and scales that set the score of query q and key j (log2 units) to
+    g_q * rising_scores[j]: ks_j = target_j / (b_j u.w), qs_q = g_q / (a_q log2 e). Head-major
+    codes [heads][cap][128] int8, scales [heads][cap] f32, V^T [kv_heads*128][kv_cap] f16 bits
+    N(0,1)*0.3; capacity rows zero."""
+    u = rng.integers(-code_max, code_max + 1, 128)
+    w = np.clip(u + rng.integers(-2, 3, 128), -code_max, code_max)
+    uw = int(u @ w)
+    assert uw > 0
+    qc = np.zeros((q_heads, q_cap, 128), np.int8)
+    kc = np.zeros((kv_heads, kv_cap, 128), np.int8)
+    a = rng.integers(1, mult_max[0] + 1, (q_heads, q_tokens))
+    b = rng.integers(1, mult_max[1] + 1, (kv_heads, kv_tokens))
+    assert code_max * max(mult_max) <= 127
+    qc[:, :q_tokens] = (a[..., None] * u).astype(np.int8)
+    kc[:, :kv_tokens] = (b[..., None] * w).astype(np.int8)
+    target = np.stack([rising_scores(rng, kv_tokens) for _ in range(kv_heads)])
+    g = rng.uniform(gain[0], gain[1], (q_heads, q_tokens))
+    qs = np.zeros((q_heads, q_cap), np.float32)
+    ks = np.zeros((kv_heads, kv_cap), np.float32)
+    qs[:, :q_tokens] = (g / (a * LOG2E)).astype(np.float32)
+    ks[:, :kv_tokens] = (target / (b * uw)).astype(np.float32)
+    vt = np.zeros((kv_heads * 128, kv_cap), np.float16)
+    vt[:, :kv_tokens] = (rng.standard_normal((kv_heads * 128, kv_tokens), np.float32) *
+                         0.3).astype(np.float16)
+    return qc, qs, kc, ks, vt.view(np.uint16)

@@ -275,3 +275,101 @@ def test_cross_attention_checks_groups_capacities_and_bindings():
         setattr(bad, field, value)
         st = L.h3_attention_i8qkhm_cross(ctypes.byref(bad), *[fake(1 << 30)] * 7, None)
         assert st == H.H3_ERR_CONFIG, (field, H.last_error())
+
+
+def gemm_pitch16(k):
+    """gemm_pitch(k, 16) (src/model.rs:74-85)."""
+    return k + 128 if (2 * k) % 1024 == 0 else k
+
+
+def direct_pitch_bindings(heads, tokens, cap):
+    """The byte lengths the reference's Stack::attend passes as `required` for its attention
+    (src/stack.rs:1815-1838): operands sized by the workload's heads, the output at the
+    direct-attention pitch (src/stack.rs:1683, 817-822)."""
+    inner = heads * 128
+    return [cap * heads * 128, cap * heads * 4, cap * heads * 128, cap * heads * 4,
+            inner * cap * 2, tokens * gemm_pitch16(inner) * 2]
+
+
+def no_device_reached():
+    """Fake bindings pass every host check and stop at the device query on a CPU host."""
+    return H.H3_ERR_NO_DEVICE
+
+
+@pytest.mark.parametrize("entry", ["h3_attention_i8qkhm", "h3_attention_i8qk"])
+def test_attention_accepts_the_reference_direct_attention_pitch(entry):
+    """tests/compiler.rs:43-45 qualifies q/kv 7168, out 7296 (56 heads, gemm_pitch(7168, 16));
+    the reference's caller binds operands of cap*56*... bytes and an output of t*7296*2
+    (src/stack.rs:1683, 1830-1837). Every binding one byte short is refused with the reference's
+    message; the exact sizes pass every check."""
+    heads, tokens = 56, 37977
+    inner = heads * 128
+    cap = H.capacity(tokens)
+    assert gemm_pitch16(inner) == 7296
+    cfg = H.AttentionCfg(inner, inner, 7296, tokens, cap, 1.0)
+    need = direct_pitch_bindings(heads, tokens, cap)
+    fn = getattr(H.lib(), entry)
+    st = fn(ctypes.byref(cfg), tokens, heads, *[fake(n) for n in need], None)
+    assert st == no_device_reached(), H.last_error()
+    # the output extent the kernel addresses ends at the last touched head's columns
+    need[5] = ((tokens - 1) * 7296 + inner) * 2
+    st = fn(ctypes.byref(cfg), tokens, heads, *[fake(n) for n in need], None)
+    assert st == no_device_reached(), H.last_error()
+    for i in range(6):
+        sizes = list(need)
+        sizes[i] -= 1
+        st = fn(ctypes.byref(cfg), tokens, heads, *[fake(n) for n in sizes], None)
+        assert st == H.H3_ERR_BINDING, (i, H.last_error())
+        assert H.last_error().endswith(f"binding {i} is {sizes[i]} bytes, the kernel addresses "
+                                       f"{need[i]}")
+
+
+def test_attention_extents_follow_the_touched_heads():
+    """A launch of `heads` rows reads key/value heads < min(heads, kv_stride/128) and query
+    heads < min(that, out_stride/128) (attention_i8qkhm_mha8_k64_lds_f16_wmma.loom:300-340):
+    fewer heads than the strides hold need smaller bindings; a token-major launch whose query
+    heads lie past a q_stride row is refused."""
+    lib = H.lib()
+    tokens, cap = 97, 128
+    cfg = H.AttentionCfg(8 * 128, 8 * 128, 8 * 128, tokens, cap, 1.0)
+    heads = 3
+    need = [heads * cap * 128, heads * cap * 4, heads * cap * 128, heads * cap * 4,
+            heads * 128 * cap * 2, ((tokens - 1) * 1024 + heads * 128) * 2]
+    assert lib.h3_attention_i8qkhm(ctypes.byref(cfg), tokens, heads, *[fake(n) for n in need],
+                                   None) == no_device_reached(), H.last_error()
+    for i in range(6):
+        sizes = list(need)
+        sizes[i] -= 1
+        st = lib.h3_attention_i8qkhm(ctypes.byref(cfg), tokens, heads,
+                                     *[fake(n) for n in sizes], None)
+        assert st == H.H3_ERR_BINDING and f"binding {i} " in H.last_error()
+    # GQA-style wrap: 8 workload rows over 2 key/value heads read 2 query heads
+    gqa = H.AttentionCfg(8 * 128, 2 * 128, 8 * 128, tokens, cap, 1.0)
+    need = [2 * cap * 128, 2 * cap * 4, 2 * cap * 128, 2 * cap * 4, 2 * 128 * cap * 2,
+            ((tokens - 1) * 1024 + 2 * 128) * 2]
+    assert lib.h3_attention_i8qkhm(ctypes.byref(gqa), tokens, 8, *[fake(n) for n in need],
+                                   None) == no_device_reached(), H.last_error()
+    # head-major does not address Q through q_stride; token-major rows must hold the heads
+    narrow = H.AttentionCfg(128, 4 * 128, 4 * 128, tokens, cap, 1.0)
+    assert lib.h3_attention_i8qkhm(ctypes.byref(narrow), tokens, 4, *[fake(1 << 40)] * 6,
+                                   None) == no_device_reached(), H.last_error()
+    st = lib.h3_attention_i8qk(ctypes.byref(narrow), tokens, 4, *[fake(1 << 40)] * 6, None)
+    assert st == H.H3_ERR_CONFIG and "holds 1 query heads, the launch reads 4" in H.last_error()
+
+
+def test_lent_workspace_is_checked_like_a_binding():
+    """The _ws forms check the workspace's size before any launch."""
+    lib = H.lib()
+    stride = 4 * 128
+    cfg = H.AttentionCfg(stride, stride, stride, 97, 128, 1.0)
+    ws = lib.h3_scales_workspace_bytes(ctypes.byref(cfg))
+    assert ws == 4 * 97 * 4
+    need = [128 * stride, 128 * 4 * 4, 128 * stride, 128 * 4 * 4, stride * 128 * 2,
+            97 * stride * 2]
+    st = lib.h3_attention_i8qk_ws(ctypes.byref(cfg), 97, 4, *[fake(n) for n in need],
+                                  fake(ws - 1), None)
+    assert st == H.H3_ERR_BINDING and H.last_error() == (
+        f"attention_i8qk: workspace is {ws - 1} bytes, the kernel addresses {ws}")
+    st = lib.h3_attention_i8qk_ws(ctypes.byref(cfg), 97, 4, *[fake(n) for n in need], fake(ws),
+                                  None)
+    assert st == no_device_reached(), H.last_error()

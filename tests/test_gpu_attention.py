@@ -112,8 +112,17 @@ def test_head_major_attention_handles_short_sequences_and_partial_tiles(dev):
 
 
 def test_head_major_attention_handles_long_reference_sequences(dev):
-    check_head_major(dev, [4096, 4097, 8193, 65537, 119585], 129)
+    """head_major_int8_attention_handles_long_reference_sequences (tests/kernels.rs:1994-1996):
+    the same lengths, 478,340 included, 129 query rows; 65,537 again with 127."""
+    check_head_major(dev, [4096, 4097, 8193, 65537, 119585, 478340], 129)
     check_head_major(dev, [65537], 127, seed_base=1)
+
+
+def test_head_major_attention_at_the_qualified_maximum_length(dev):
+    """tests/compiler.rs:34-45 qualifies the head-major kernel at 1,048,544 tokens (capacity
+    1,048,576, the largest the config allows): one head, 129 query rows over every key, guard
+    bytes and three bit-identical runs as check_head_major_attention."""
+    check_head_major(dev, [1048544], 129, heads=1)
 
 
 def test_token_count_below_tokens_writes_only_those_rows(dev):
