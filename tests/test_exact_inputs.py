@@ -6,7 +6,8 @@ alpha = 2^(m_old - m_new)) when a lane's 16 probabilities sum past 2^8. The GPU 
 that rise at every tile (helpers.rank1_operands), so that this path runs at every tile position.
 Here, on the CPU:
   - the codes and scales give the intended scores: S = a_q b_j (u.w) exactly, and
-    S * qs * ks * log2(e) = g_q * target_j to f32 accuracy;
+    S * qs * ks * log2(e) = g_q * target_j to f32 accuracy; the int8 codes span most of the
+    range, so the kernels' dequantisation error (under 0.75 units of S) stays far below the bar;
   - every tile after the first lifts every lane over the limit: each probability of tile t
     against the max of the keys before it exceeds 2^4, so any 16 of them pass 2^8;
   - a tile-by-tile online softmax in f64 with the rescale reproduces the f64 oracle, and the
@@ -54,6 +55,8 @@ def test_rising_scores_force_the_exact_path_and_planted_mistakes_show():
             run_max = np.maximum.accumulate([t.max() for t in tiles])
             lift = np.array([tiles[t].min() - run_max[t - 1] for t in range(1, len(tiles))])
             assert lift.min() > 4.0, (h, r, lift.min())
+            # the kernels' dequantisation (within 0.75 units of S) moves a score by at most this
+            assert 0.75 * np.abs(y).max() / np.abs(s).min() < 4e-3
             got = online_softmax(qc, qs, kc, ks, vt, tokens, h, r)
             assert np.allclose(got, want[i, h], rtol=1e-12, atol=1e-12)
             bar = 1e-3 + 2e-3 * np.abs(want[i, h])
@@ -76,3 +79,6 @@ def test_rank1_codes_give_the_intended_scores():
     y = s * qs[0, :qt, None].astype(np.float64) * ks[0, None, :kt].astype(np.float64) * LOG2E
     ratio = y / y[:, :1]  # g_q cancels: every row is the same target profile
     assert np.allclose(ratio, ratio[:1], rtol=1e-6)
+    # one unit of S in log2 units, at the largest score: well below the bar's reach
+    per_unit = np.abs(y).max() / np.abs(s).min()
+    assert np.abs(s).min() >= 3e5 and 0.75 * per_unit < 2e-3, (np.abs(s).min(), per_unit)

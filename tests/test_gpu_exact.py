@@ -31,6 +31,7 @@ pytestmark = pytest.mark.gpu
 
 def assert_close(got, want, what):
     err = np.abs(got - want)
+    print(f"  {what}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
     bad = err > 1e-3 + 2e-3 * np.abs(want)
     assert not bad.any(), (what, float(err.max()), np.argwhere(bad)[:4].tolist())
 
@@ -140,8 +141,10 @@ def test_fp6_exact_path_at_every_tile(dev, tokens, heads, kv_heads):
 
     cap = H.capacity(tokens)
     rng = np.random.default_rng(tokens + 6)
+    # int4 codes: |u| in [2, 3], multipliers 1-2 (codes -6..6); the FP6 form accumulates S/4
+    # exactly in f32 from zero, so its dequantisation has no bias error to bound
     qc, qs, kc, ks, vt = rank1_operands(rng, heads, tokens, cap, kv_heads, tokens, cap,
-                                        code_max=3, mult_max=(2, 2))
+                                        code_min=2, code_max=3, mult_max=(2, 2))
     # token-major int4 operands: [cap][heads*128] codes, [cap][heads] scales
     q_tm = np.ascontiguousarray(qc.transpose(1, 0, 2)).reshape(cap, heads * 128)
     k_tm = np.ascontiguousarray(kc.transpose(1, 0, 2)).reshape(cap, kv_heads * 128)
