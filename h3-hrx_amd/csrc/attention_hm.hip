@@ -171,8 +171,9 @@ __device__ __forceinline__ Stager make_stager(const Geometry& g, int wave, int l
   return s;
 }
 
-// Staging of one stage (K tile at key kk0 with its scales, V^T tile at key vk0): buffer
-// descriptors that end at the last valid key (K, scales) or at the end of the head's V^T block.
+// Staging loads of one step (K tile at key kk0, V^T tile at key vk0, the key scales of the tile at
+// key sk0): buffer descriptors that end at the last valid key (K, scales) or at the end of the
+// head's V^T block.
 struct StepLoads {
   __amdgpu_buffer_rsrc_t rk, rv, rs, rm;
   char* kst;
@@ -182,11 +183,12 @@ struct StepLoads {
 };
 template <bool kCross>
 __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_head, uint32_t kk0,
-                                               char* kst, uint32_t vk0, char* vst) {
+                                               char* kst, uint32_t vk0, char* vst, uint32_t sk0) {
   StepLoads L;
   const uint32_t live = g.tokens > kk0 ? min(g.tokens - kk0, (uint32_t)kKeys) : 0u;
-  L.rs = rsrc(g.ks + (size_t)kv_head * g.capacity + kk0, live * 4);
-  if (kCross) L.rm = rsrc(g.key_mask + kk0, live);
+  const uint32_t slive = g.tokens > sk0 ? min(g.tokens - sk0, (uint32_t)kKeys) : 0u;
+  L.rs = rsrc(g.ks + (size_t)kv_head * g.capacity + sk0, slive * 4);
+  if (kCross) L.rm = rsrc(g.key_mask + sk0, slive);
   L.keep = 0;
   L.rk = rsrc(reinterpret_cast<const char*>(g.ki) + ((size_t)kv_head * g.capacity + kk0) * 128,
               live * 128);
@@ -201,7 +203,8 @@ __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_he
   return L;
 }
 // Load `slot` of a step: 0 the key scale (into a register; with cross-attention also the key's
-// mask byte), then the K tile's LDS-DMA loads, then the V^T tile's.
+// mask byte), then the K tile's LDS-DMA loads, then the V^T tile's. The scale is of the stage
+// after the step's K tile, so that it has two steps to land before it is stored.
 template <bool kCross>
 __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int slot) {
   if (slot == 0) {
@@ -281,6 +284,7 @@ struct Tile {
   v4i q[4];     // Q^T operand: 4 chunks of 32 channels
   v6i qf[2];    // FP6 form: the Q^T operand, 2 chunks of 64 channels
   float qsl;    // qs * log2(e)
+  float cq;     // -1.5*2^23 * qsl: removes the QK accumulators' bias (0 in the FP6 form)
   float negm;   // minus the running max (log2 units)
   float l;      // this lane's share of the row sum
 };
@@ -410,13 +414,6 @@ __device__ __forceinline__ float half_swap_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// acc + the four probabilities in two packed words, accumulated in f32 (dot products with 1).
-__device__ __forceinline__ float sum_words(const uint32_t (&w)[2], float acc) {
-  const v2h one = {(_Float16)1.0f, (_Float16)1.0f};
-  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, w[0]), one, acc, false);
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, w[1]), one, acc, false);
-}
-
 // Scales of quarter i (slots 4i..4i+3) of key block b: ks at kss[32b + 8i + 4h .. +3] for lane
 // half h (byte offset `soff` = 16h), c 64 floats further.
 __device__ __forceinline__ float4 scale4(const float* kss, int b, int i, uint32_t soff) {
@@ -424,9 +421,9 @@ __device__ __forceinline__ float4 scale4(const float* kss, int b, int i, uint32_
                                           soff);
 }
 
-// Dequantized scores of quarter i of the tile's S^T: u = acc*ks + c, with the scales of row j in
-// slot j+1 of k4 and j+2 of c4 (stored rotated). Written as assembly so that, like the rest of a
-// chunk's vector work, it is issued after the chunk's MFMA.
+// Dequantized scores of quarter i of the tile's S^T on the masked path (a key's c is -inf when
+// it is dead): u = acc*ks + c, with the scales of row j in slot j+1 of k4 and j+2 of c4 (stored
+// rotated, so the three operands of each FMA lie in different VGPR banks).
 __device__ __forceinline__ void dequant_quarter(const v16i& s, int i, float4 k4, float4 c4,
                                                 float (&u)[4]) {
   asm volatile("v_fma_f32 %0, %4, %8, %12\n\t"
@@ -438,28 +435,78 @@ __device__ __forceinline__ void dequant_quarter(const v16i& s, int i, float4 k4,
                  "v"(k4.y), "v"(k4.z), "v"(k4.w), "v"(k4.x),
                  "v"(c4.z), "v"(c4.w), "v"(c4.x), "v"(c4.y));
 }
-
-// Exponent arguments y = u*qsl - m of a quarter, computed in f32 and rounded once to f16 into the
-// low and high halves of two words (v_fma_mixlo/mixhi_f16). Then p = 2^y in place with the f16
-// exponential on each half (SDWA, the other half preserved): the probabilities come out packed
-// as PV's B operand with no separate conversion. Each exponential's result is read two
-// instructions later at the earliest, and the trailing nop covers the first read after the block.
-__device__ __forceinline__ void exparg_quarter(const float (&u)[4], float qsl, float negm,
-                                               uint32_t (&w)[2]) {
-  asm volatile("v_fma_mixlo_f16 %0, %2, %6, %7\n\t"
-               "v_fma_mixlo_f16 %1, %4, %6, %7\n\t"
-               "v_fma_mixhi_f16 %0, %3, %6, %7\n\t"
-               "v_fma_mixhi_f16 %1, %5, %6, %7"
-               : "=&v"(w[0]), "=&v"(w[1])
-               : "v"(u[0]), "v"(u[1]), "v"(u[2]), "v"(u[3]), "v"(qsl), "v"(negm));
+// y = u*qsl + negm for the four dequantized scores.
+__device__ __forceinline__ void exparg_quarter(float (&y)[4], float qsl, float negm) {
+  asm volatile("v_fma_f32 %0, %0, %4, %5\n\t"
+               "v_fma_f32 %1, %1, %4, %5\n\t"
+               "v_fma_f32 %2, %2, %4, %5\n\t"
+               "v_fma_f32 %3, %3, %4, %5"
+               : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3])
+               : "v"(qsl), "v"(negm));
 }
-__device__ __forceinline__ void exp2_quarter(uint32_t (&w)[2]) {
-  asm volatile("v_exp_f16_sdwa %0, %0 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0\n\t"
-               "v_exp_f16_sdwa %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0\n\t"
-               "v_exp_f16_sdwa %0, %0 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_1\n\t"
-               "v_exp_f16_sdwa %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_1\n\t"
-               "s_nop 0"
-               : "+v"(w[0]), "+v"(w[1]));
+
+// Exponent arguments y (log2 units, less the running max) of quarter i, on a tile whose keys all
+// lie inside the sequence: t = acc*qsl + cq with the lane's own constants (cq removes the
+// accumulators' bias, so t is S*qs*log2(e) to within 0.75*qsl, less than one unit of S), then
+// y = t*ks + negm. Only the key scales come from LDS (row j's in slot j+1 of k4). Both FMAs are
+// full-rate vector instructions; the masked path below needs the c values as well.
+__device__ __forceinline__ void scores_quarter(const v16i& s, int i, float4 k4, float qsl,
+                                               float cq, float negm, float (&y)[4]) {
+  asm volatile("v_fma_f32 %0, %4, %8, %9\n\t"
+               "v_fma_f32 %1, %5, %8, %9\n\t"
+               "v_fma_f32 %2, %6, %8, %9\n\t"
+               "v_fma_f32 %3, %7, %8, %9\n\t"
+               "v_fma_f32 %0, %0, %10, %14\n\t"
+               "v_fma_f32 %1, %1, %11, %14\n\t"
+               "v_fma_f32 %2, %2, %12, %14\n\t"
+               "v_fma_f32 %3, %3, %13, %14"
+               : "=&v"(y[0]), "=&v"(y[1]), "=&v"(y[2]), "=&v"(y[3])
+               : "v"(s[4 * i]), "v"(s[4 * i + 1]), "v"(s[4 * i + 2]), "v"(s[4 * i + 3]),
+                 "v"(qsl), "v"(cq), "v"(k4.y), "v"(k4.z), "v"(k4.w), "v"(k4.x), "v"(negm));
+}
+// The same on a tile that holds dead keys (past the sequence, or masked in cross-attention):
+// u = acc*ks + c with c = -inf for a dead key, then y = u*qsl + negm (-inf: probability 0).
+__device__ __forceinline__ void scores_quarter_masked(const v16i& s, int i, float4 k4, float4 c4,
+                                                      float qsl, float negm, float (&y)[4]) {
+  dequant_quarter(s, i, k4, c4, y);
+  exparg_quarter(y, qsl, negm);
+}
+// The exponent arguments of quarter i: on a tile that may hold dead keys (kMasked) through their
+// staged c values, else from the key scales alone.
+template <bool kMasked>
+__device__ __forceinline__ void scores(const v16i& s, int i, float4 k4, float4 c4, float qsl,
+                                       float cq, float negm, float (&y)[4]) {
+  if constexpr (kMasked)
+    scores_quarter_masked(s, i, k4, c4, qsl, negm, y);
+  else
+    scores_quarter(s, i, k4, qsl, cq, negm, y);
+}
+
+// p = 2^y in f32, in place, in two parts: three of the quarter's exponentials with the sum of
+// the first two (`a`), then the fourth with the f16 packing (v_cvt_pk_f16_f32, round to nearest
+// even) of (p0, p1) and (p2, p3) as PV's B operand and the rest of the quarter's sum into the
+// tile sum `ts`. The row sum adds the unrounded f32 probabilities, as the reference does; f32
+// adds run beside the matrix pipe, where dot-product instructions would occupy it. A
+// transcendental's result is read only after one wait state: p0 and p1 two and one
+// instructions after their exponentials in the first part, p3 after the first conversion.
+__device__ __forceinline__ void exp3_quarter(float (&y)[4], float& a) {
+  asm volatile("v_exp_f32 %0, %0\n\t"
+               "v_exp_f32 %1, %1\n\t"
+               "v_exp_f32 %2, %2\n\t"
+               "v_add_f32 %3, %0, %1"
+               : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "=&v"(a));
+}
+__device__ __forceinline__ void exp_pack_quarter(float (&y)[4], uint32_t (&w)[2], float& a,
+                                                 float& ts) {
+  float b;
+  asm volatile("v_exp_f32 %3, %3\n\t"
+               "v_cvt_pk_f16_f32 %0, %6, %7\n\t"
+               "v_cvt_pk_f16_f32 %1, %8, %3\n\t"
+               "v_add_f32 %2, %8, %3\n\t"
+               "v_add_f32 %4, %4, %2\n\t"
+               "v_add_f32 %5, %5, %4"
+               : "=&v"(w[0]), "=&v"(w[1]), "=&v"(b), "+v"(y[3]), "+v"(a), "+v"(ts)
+               : "v"(y[0]), "v"(y[1]), "v"(y[2]));
 }
 // The words of quarter i go to group i/2 (16 keys), elements 4(i%2)..+3.
 __device__ __forceinline__ void put_quarter(v8h (&p)[2], int i, const uint32_t (&w)[2]) {
@@ -471,25 +518,42 @@ __device__ __forceinline__ void put_quarter(v8h (&p)[2], int i, const uint32_t (
   p[g][e + 3] = b[1];
 }
 
+// The probabilities of quarter i against negm: y, then p = 2^y packed as PV's operand into
+// T.p[par], and its share of the tile sum.
+template <bool kMasked>
+__device__ __forceinline__ float probs_quarter(Tile& T, int par, int i, float4 k4, float4 c4,
+                                               float ts) {
+  float y[4];
+  uint32_t w[2];
+  float a;
+  scores<kMasked>(T.s[par], i, k4, c4, T.qsl, T.cq, T.negm, y);
+  exp3_quarter(y, a);
+  exp_pack_quarter(y, w, a, ts);
+  put_quarter(T.p[par], i, w);
+  return ts;
+}
+
 // The exact path for probabilities of key tile `par` (computed against the running max) that may
 // exceed 2^8: take the tile's max, raise m, rescale the accumulators and the row sum, recompute
 // the probabilities. `kss` and `b` locate the key tile's scales. It works quarter by quarter,
-// re-reading the scales, so that few registers are live beside the loop's own.
+// re-reading the scales, so that few registers are live beside the loop's own. The max is of the
+// scores as the probabilities compute them, with negm = 0 (log2 units).
+template <bool kMasked>
 __device__ __forceinline__ void raise_exact(Tile& T, int par, const float* kss, int b,
                                             uint32_t soff, int half) {
   float tmax = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float4 k4 = scale4(kss, b, i, soff), c4 = scale4(kss + kKeys, b, i, soff);
-    const float kv[4] = {k4.x, k4.y, k4.z, k4.w}, cv[4] = {c4.x, c4.y, c4.z, c4.w};
+    const float4 k4 = scale4(kss, b, i, soff);
+    const float4 c4 = kMasked ? scale4(kss + kKeys, b, i, soff) : k4;
+    float y[4];
+    scores<kMasked>(T.s[par], i, k4, c4, T.qsl, T.cq, 0.0f, y);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      tmax = fmaxf(tmax, __builtin_fmaf(__int_as_float(T.s[par][4 * i + j]), kv[(j + 1) & 3],
-                                        cv[(j + 2) & 3]));
+    for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, y[j]);
   }
   tmax = half_swap_max(tmax);
   const float m_old = -T.negm;
-  const float m_new = fmaxf(m_old, tmax * T.qsl);
+  const float m_new = fmaxf(m_old, tmax);
   const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);
   // The tile's PV MFMAs of this sub-step were issued before; the waits on both sides of the
   // rescale cover them and the next MFMA that reads the accumulators. alpha is an input of the
@@ -504,22 +568,18 @@ __device__ __forceinline__ void raise_exact(Tile& T, int par, const float* kss, 
   float ts = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float u[4];
-    uint32_t w[2];
-    dequant_quarter(T.s[par], i, scale4(kss, b, i, soff), scale4(kss + kKeys, b, i, soff), u);
-    exparg_quarter(u, T.qsl, T.negm, w);
-    exp2_quarter(w);
-    put_quarter(T.p[par], i, w);
-    ts = sum_words(w, ts);
+    const float4 k4 = scale4(kss, b, i, soff);
+    const float4 c4 = kMasked ? scale4(kss + kKeys, b, i, soff) : k4;
+    ts = probs_quarter<kMasked>(T, par, i, k4, c4, ts);
   }
   T.l = T.l * alpha + ts;
   asm volatile("s_nop 7" ::: "memory");  // fresh P before the next MFMA reads it
 }
 
-// The probabilities of a block's first key tile: the exact path with nothing to rescale. The
-// running max is still -1e30 (negm 1e30) and O^T and the row sum are zero, so the rescale of
-// raise_exact multiplies zeros and 0*alpha + sum is the sum: the max is taken first and the
-// probabilities computed once, from the same dequantised scores, with the results of the
+// The probabilities of a block's first key tile in cross-attention: the exact path with nothing
+// to rescale. The running max is still -1e30 (negm 1e30) and O^T and the row sum are zero, so the
+// rescale of raise_exact multiplies zeros and 0*alpha + sum is the sum: the max is taken first
+// and the probabilities computed once, from the same dequantised scores, with the results of the
 // general path bit for bit and none of its overflowing first pass.
 __device__ __forceinline__ void first_tile(Tile& T, int par, const float* kss, int b,
                                            uint32_t soff) {
@@ -528,19 +588,22 @@ __device__ __forceinline__ void first_tile(Tile& T, int par, const float* kss, i
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     dequant_quarter(T.s[par], i, scale4(kss, b, i, soff), scale4(kss + kKeys, b, i, soff), u[i]);
+    float y[4] = {u[i][0], u[i][1], u[i][2], u[i][3]};
+    exparg_quarter(y, T.qsl, 0.0f);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, u[i][j]);
+    for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, y[j]);
   }
   tmax = half_swap_max(tmax);
-  T.negm = -fmaxf(-1.0e30f, tmax * T.qsl);
+  T.negm = -fmaxf(-1.0e30f, tmax);
   float ts = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t w[2];
-    exparg_quarter(u[i], T.qsl, T.negm, w);
-    exp2_quarter(w);
+    float a;
+    exparg_quarter(u[i], T.qsl, T.negm);
+    exp3_quarter(u[i], a);
+    exp_pack_quarter(u[i], w, a, ts);
     put_quarter(T.p[par], i, w);
-    ts = sum_words(w, ts);
   }
   T.l = ts;
   asm volatile("s_nop 7" ::: "memory");  // fresh P before the next MFMA reads it
@@ -551,7 +614,7 @@ __device__ __forceinline__ void first_tile(Tile& T, int par, const float* kss, i
 struct Pre {
   v4i k[4];
   v6i kf[2];  // FP6 form: the two K chunks
-  float4 k4[2], c4[2];
+  float4 k4[2];  // key scales of quarters 0 and 1 (a masked sub-step reads their c itself)
 };
 // Part `part` (0-5) of the reads of `pre` for a sub-step that reads block `kb` of K stage `kst`
 // and block `sb` of scale stage `sst`: parts 0-3 the K chunks, 4-5 the scales of quarters 0-1.
@@ -578,7 +641,6 @@ __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, in
   } else {
     const float* kss = reinterpret_cast<const float*>(sst);
     pre.k4[part - 4] = scale4(kss, sb, part - 4, ln.s);
-    pre.c4[part - 4] = scale4(kss + kKeys, sb, part - 4, ln.s);
   }
 }
 
@@ -586,18 +648,22 @@ __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, in
 //   kQK  QK of key tile t+2 (its K chunks in `pre`) into S^T[kPar]
 //   kPV  PV of key tile t (block kPar of V^T stage `vst`) from P[kPar]
 //   kSM  probabilities of key tile t+1 (block `sb` of scale stage `sst`) from S^T[1-kPar] into
-//        P[1-kPar], then the overflow check.
+//        P[1-kPar], then the overflow check. kMasked: the tile may hold dead keys (past the
+//        sequence, or masked in cross-attention), so its scores take the masked path, which
+//        reads each key's c (-inf for a dead key) beside its scale.
 // Every chunk issues its MFMA first and its vector work right behind it (all of it inline
 // assembly, whose order the compiler keeps); then its LDS reads and whatever `stage(c, next)`
 // issues (staging loads, the step barrier, the reads of the next sub-step's `Pre`). The K chunks
-// and the first two quarters' scales come in `pre`, read during the sub-step before; the 8 V^T
-// chunks are read kPf chunks ahead. QK comes first, so the S^T it writes is read by the vector
-// ALU only in the next sub-step, after this one's 8 PV MFMAs. The softmax runs quarter by
-// quarter (4 keys of each lane half), three chunks each (dequantisation, exponent arguments,
-// exponentials), with the scales of quarters 2 and 3 read two quarters ahead. Each quarter adds
-// its probabilities to the lane's tile sum right away (f32 dot products), so the overflow check
-// after the last chunk waits on two instructions only.
-template <int kPar, bool kQK, bool kPV, bool kSM, bool kFp6, bool kFirst = false, typename Stage>
+// and the first two quarters' key scales come in `pre`, read during the sub-step before; the 8
+// V^T chunks are read kPf chunks ahead. QK comes first, so the S^T it writes is read by the
+// vector ALU only in the next sub-step, after this one's 8 PV MFMAs. The softmax runs quarter by
+// quarter (4 keys of each lane half), three chunks each (the exponent arguments, three
+// exponentials, the last one with the f16 packing and the quarter's share of the tile sum), with
+// the scales of quarters 2 and 3 read two quarters ahead. Each quarter adds its probabilities to
+// the lane's tile sum right away (f32 adds), so the overflow check after the last chunk waits on
+// a few instructions only.
+template <int kPar, bool kQK, bool kPV, bool kSM, bool kFp6, bool kFirst = false,
+          bool kMasked = false, typename Stage>
 __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int sb, Tile& T,
                                          const Lanes& ln, int half, const v16i& magic, Pre& pre,
                                          Stage&& stage) {
@@ -607,7 +673,7 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
   v6i kopf[2];
   v8h vop[8];
   float4 k4[4], c4[4];
-  float u[4];
+  float y[4], ysum;
   uint32_t w[2];
   float ts = 0.0f;  // the lane's tile sum
   auto read_op = [&](int o) {
@@ -619,7 +685,7 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
   };
   auto read_scales = [&](int i) {
     k4[i] = scale4(kss, sb, i, ln.s);
-    c4[i] = scale4(kss + kKeys, sb, i, ln.s);
+    if (kMasked) c4[i] = scale4(kss + kKeys, sb, i, ln.s);
   };
   if constexpr (kFp6) {
     kopf[0] = pre.kf[0];
@@ -631,8 +697,10 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     k4[i] = pre.k4[i];
-    c4[i] = pre.c4[i];
+    c4[i] = kMasked && kSM && !kFirst ? scale4(kss + kKeys, sb, i, ln.s) : k4[i];
   }
+#pragma unroll
+  for (int i = 2; i < 4; ++i) c4[i] = k4[0];  // defined before read_scales fills them
 #pragma unroll
   for (int o = 4; o < 4 + kPf; ++o) read_op(o);
 #pragma unroll
@@ -655,17 +723,16 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
       pv_mfma(v & 3, vop[v], T.p[kPar][v >> 2]);
     }
     if (kSM && !kFirst) {
-      // quarter c/3: dequantisation, exponent arguments, exponentials (and its share of the tile
-      // sum, two dot products into f32)
+      // quarter c/3: exponent arguments; three exponentials; the fourth with the packing and
+      // the quarter's share of the tile sum (two dot products into f32)
       const int i = c / 3, phase = c % 3;
       if (phase == 0) {
-        dequant_quarter(T.s[kSm], i, k4[i], c4[i], u);
+        scores<kMasked>(T.s[kSm], i, k4[i], c4[i], T.qsl, T.cq, T.negm, y);
       } else if (phase == 1) {
-        exparg_quarter(u, T.qsl, T.negm, w);
+        exp3_quarter(y, ysum);
       } else {
-        exp2_quarter(w);
+        exp_pack_quarter(y, w, ysum, ts);
         put_quarter(T.p[kSm], i, w);
-        ts = sum_words(w, ts);
         if (i == 0 || i == 1) read_scales(i + 2);
       }
     }
@@ -679,7 +746,7 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
     first_tile(T, kSm, kss, sb, ln.s);
   } else if (kSM) {
     if (__builtin_expect(__any(!(ts <= kSumLimit)), 0))
-      raise_exact(T, kSm, kss, sb, ln.s, half);
+      raise_exact<kMasked>(T, kSm, kss, sb, ln.s, half);
     else
       T.l += ts;
   }
@@ -792,12 +859,15 @@ void k_attention_hm(Geometry g) {
       for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
     }
     T.qsl = g.qs[(size_t)w.head * q_cap + q_read] * kLog2e;
+    T.cq = kFp6 ? 0.0f : -(kMagic * T.qsl);
   };
 
   bool chained = false;  // this block's first stages were staged by the previous block
   bool have_q = false;   // this block's Q was loaded by the previous block
-  float ks_carry = 0.0f;
-  uint32_t keep_carry = 0;
+  // The next block's stage-2 and stage-3 key scales (and mask bytes), loaded by a block that
+  // chains into it.
+  float ks_carry[2] = {0.0f, 0.0f};
+  uint32_t keep_carry[2] = {0u, 0u};
   Tile T;
 
   for (;;) {
@@ -811,19 +881,24 @@ void k_attention_hm(Geometry g) {
   // stage index of a load: past the last stage it is the next block's (chained) or out of range
   auto stage_of = [&](uint32_t st) { return wrap && st >= n_stages ? st - n_stages : st; };
 
-  // ---- prologue: K and scales of stages 0..2, V^T of stages 0 and 1 in flight (unless chained)
-  StepLoads L0 = plan_step<kCross>(g, kv_head, 0, k0s, 0, v0s);
-  StepLoads L1 = plan_step<kCross>(g, kv_head, kKeys, k1s, kKeys, v1s);
-  StepLoads L2 = plan_step<kCross>(g, kv_head, 2 * kKeys, k2s, 0, nullptr);
+  // ---- prologue: K and scales of stages 0..2, V^T of stages 0 and 1 and the scales of stage 3
+  // in flight (unless chained)
+  StepLoads L0 = plan_step<kCross>(g, kv_head, 0, k0s, 0, v0s, 0);
+  StepLoads L1 = plan_step<kCross>(g, kv_head, kKeys, k1s, kKeys, v1s, kKeys);
+  StepLoads L2 = plan_step<kCross>(g, kv_head, 2 * kKeys, k2s, 0, nullptr, 2 * kKeys);
+  StepLoads L3 = plan_step<kCross>(g, kv_head, 0, nullptr, 0, nullptr, stage_of(3) * kKeys);
   if (!chained) {
     issue_k<kCross>(L0, sg);
     issue_v<kCross>(L0, sg);
     issue_k<kCross>(L1, sg);
     issue_v<kCross>(L1, sg);
     issue_k<kCross>(L2, sg);
+    issue_load<kCross>(L3, sg, 0);
   } else {
-    L2.ks = ks_carry;
-    L2.keep = keep_carry;
+    L2.ks = ks_carry[0];
+    L2.keep = keep_carry[0];
+    L3.ks = ks_carry[1];
+    L3.keep = keep_carry[1];
   }
 
   if (!have_q) load_q(T, wb);
@@ -840,8 +915,10 @@ void k_attention_hm(Geometry g) {
     step_barrier<kWaitLds>();
   }
 
-  // ---- step -1: QK of key tiles 0 and 1, the probabilities of tile 0; K(3) and V(2) in flight
-  StepLoads Lm = plan_step<kCross>(g, kv_head, stage_of(3) * kKeys, k3s, 2 * kKeys, v2s);
+  // ---- step -1: QK of key tiles 0 and 1, the probabilities of tile 0; K(3), V(2) and the scales
+  // of stage 4 in flight
+  StepLoads Lm = plan_step<kCross>(g, kv_head, stage_of(3) * kKeys, k3s, 2 * kKeys, v2s,
+                                   stage_of(4) * kKeys);
   issue_k<kCross>(Lm, sg);
   issue_v<kCross>(Lm, sg);
   Pre pre;
@@ -853,21 +930,24 @@ void k_attention_hm(Geometry g) {
   });
   // The first tile's own path pays where blocks are short (cross-attention's few key tiles);
   // self-attention keeps the general path, whose code measured marginally faster at long
-  // sequences. The results are the same bits either way.
-  sub_step<1, true, false, true, kFp6, kCross>(nullptr, s0s, 0, T, ln, half, magic, pre,
-                                                [&](int c, Pre& next) {
+  // sequences. The results are the same bits either way. Tile 0 is the last one of a sequence of
+  // at most 32 keys, so it takes the masked path.
+  sub_step<1, true, false, true, kFp6, kCross, true>(nullptr, s0s, 0, T, ln, half, magic, pre,
+                                                      [&](int c, Pre& next) {
     if (c == 0) store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
     if (c == kBarrierChunk) step_barrier<kWaitPrevStep<kCross>>();
     next_step_reads<kFp6>(c, next, k1s, s0s, ln);
   });
-  float ks_held = Lm.ks;
-  uint32_t keep_held = Lm.keep;
+  // Key scales (and mask bytes) in registers until their store: those loaded in step j (stage
+  // j+5) wait in hold[j % 2] for step j+2; the prologue's (stage 3) count as step -2's.
+  float ks_hold[2] = {L3.ks, Lm.ks};
+  uint32_t keep_hold[2] = {L3.keep, Lm.keep};
 
   // Steady step j (stage j+1 exists), J = j % 4: sub-steps 2j and 2j+1 read K(j+1), V(j) and the
   // scales of tiles 2j+1 (stage j, block 1) and 2j+2 (stage j+1, block 0); the step stages K(j+4)
-  // into K(j)'s array and V(j+3) into V(j-1)'s, loads the scale of stage j+4, and stores the
-  // scales of stage j+3 (loaded one step earlier) into S(j-1)'s. Every load has three steps to
-  // land. The step's barrier comes once its last read of K(j+1) and V(j) is issued (chunk
+  // into K(j)'s array and V(j+3) into V(j-1)'s, loads the scale of stage j+5, and stores the
+  // scales of stage j+3 (loaded two steps earlier) into S(j-1)'s. Every K and V^T load has three
+  // steps to land, every scale two. The step's barrier comes once its last read of K(j+1) and V(j) is issued (chunk
   // kBarrierChunk of its second sub-step), after a wait for this wave's loads of two steps
   // before; the reads for the next step's first sub-step follow it. Stages past the last are the
   // next block's first ones when the blocks chain.
@@ -875,25 +955,31 @@ void k_attention_hm(Geometry g) {
   auto steady = [&](auto J_) {
     constexpr int J = decltype(J_)::value;
     StepLoads L = plan_step<kCross>(g, kv_head, stage_of(j + 4) * kKeys, kr(J),
-                                    stage_of(j + 3) * kKeys, vr(J + 3));
+                                    stage_of(j + 3) * kKeys, vr(J + 3), stage_of(j + 5) * kKeys);
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
-    sub_step<0, true, true, true, kFp6>(vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
+    sub_step<0, true, true, true, kFp6, false, kCross>(vr(J), sr(J), 1, T, ln, half, magic, pre,
+                                                       [&](int c, Pre& next) {
       if (c == 0)
-        store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_held, keep_held, stage_of(j + 3) * kKeys,
-                                   g.tokens);
+        store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_hold[J & 1], keep_hold[J & 1],
+                                         stage_of(j + 3) * kKeys, g.tokens);
       if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep)
         issue_load<kCross>(L, sg, c / kLoadGap);
       if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
     });
-    sub_step<1, true, true, true, kFp6>(vr(J), sr(J + 1), 0, T, ln, half, magic, pre,
-                                  [&](int c, Pre& next) {
+    auto stage1 = [&](int c, Pre& next) {
       const int slot = (c + 12) / kLoadGap;
       if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
       if (c == kBarrierChunk) step_barrier<kWaitTwoSteps<kCross>>();
       next_step_reads<kFp6>(c, next, kr(J + 2), sr(J + 1), ln);
-    });
-    ks_held = L.ks;
-    keep_held = L.keep;
+    };
+    // Tile 2j+2 (keys 64(j+1) ..) holds keys past the sequence in the last steady step when the
+    // sequence ends inside its 32 keys: this sub-step always takes the masked path. (A branch
+    // between the two paths here puts register copies at its join that the inline-assembly
+    // MFMAs after it may read before they land, which the compiler does not guard against.)
+    sub_step<1, true, true, true, kFp6, false, true>(vr(J), sr(J + 1), 0, T, ln, half, magic, pre,
+                                                     stage1);
+    ks_hold[J & 1] = L.ks;
+    keep_hold[J & 1] = L.keep;
     ++j;
   };
   const uint32_t n_steady = n_stages - 1;  // steps j with stage j+1
@@ -909,8 +995,10 @@ void k_attention_hm(Geometry g) {
   if (rest > 2) steady(std::integral_constant<int, 2>{});
 
   // ---- last step (j = n_stages - 1): PV of tiles 2j and 2j+1, the probabilities of 2j+1 between
-  // (its scales came in `pre`; its K reads there are unused)
-  sub_step<0, false, true, true, kFp6>(vr(j), sr(j), 1, T, ln, half, magic, pre, [](int, Pre&) {});
+  // (its scales came in `pre`; its K reads there are unused). Tile 2j+1 may hold keys past the
+  // sequence: the masked path.
+  sub_step<0, false, true, true, kFp6, false, true>(vr(j), sr(j), 1, T, ln, half, magic, pre,
+                                                    [](int, Pre&) {});
   sub_step<1, false, true, false, kFp6>(vr(j), nullptr, 0, T, ln, half, magic, pre, [](int, Pre&) {});
   step_barrier<kWaitAll>();  // no staging load outlives the block (chained ones have landed)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // the last PV MFMAs have landed
@@ -968,8 +1056,12 @@ void k_attention_hm(Geometry g) {
   if (!has_next) break;
   have_q = true;
   chained = wrap;
-  ks_carry = ks_held;
-  keep_carry = keep_held;
+  // after the last steady step (j - 1): hold[j % 2] holds stage n_stages + 2, the other
+  // n_stages + 3, i.e. the next block's stages 2 and 3 when it chains
+  ks_carry[0] = (j & 1) ? ks_hold[1] : ks_hold[0];
+  ks_carry[1] = (j & 1) ? ks_hold[0] : ks_hold[1];
+  keep_carry[0] = (j & 1) ? keep_hold[1] : keep_hold[0];
+  keep_carry[1] = (j & 1) ? keep_hold[0] : keep_hold[1];
   local = next_local;
   }
 }

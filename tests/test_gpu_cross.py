@@ -73,8 +73,14 @@ def test_one_sequence_unmasked_is_the_dense_kernel(dev):
     for name, o in (("cross", got), ("dense", dense)):
         mx, mean = north_star_ok(o.view(np.float16).astype(np.float32), want)
         assert mx < 2e-2 and mean < 2e-3, (name, mx, mean)
-    # the same kernel code with every key live: identical bits
-    assert np.array_equal(got, dense)
+    # The two forms share the kernel but not the last rounding of every score: cross-attention
+    # removes the QK bias with each key's constant (c = -1.5*2^23*ks, -inf for a masked key),
+    # the dense form does so on tiles without dead keys with the query's (-1.5*2^23*qs*log2 e).
+    # Both put a score within 0.75 units of S of its exact value, so the outputs agree to within
+    # a few f16 steps, far inside the oracle's bar.
+    a = got.view(np.float16).astype(np.float64)
+    b = dense.view(np.float16).astype(np.float64)
+    assert np.abs(a - b).max() <= 1e-3 + 2e-3 * np.abs(want).max(), np.abs(a - b).max()
 
 
 def test_config4_text_shape_on_sampled_rows(dev):
