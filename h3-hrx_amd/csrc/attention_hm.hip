@@ -280,7 +280,6 @@ __device__ __forceinline__ void step_barrier() {
 // belong to.
 struct Tile {
   v16i s[2];    // S^T of the 32-key tiles of each parity
-  v8h p[2][2];  // probabilities of the 32-key tiles of each parity, packed f16 (16 keys each)
   v4i q[4];     // Q^T operand: 4 chunks of 32 channels
   v6i qf[2];    // FP6 form: the Q^T operand, 2 chunks of 64 channels
   float qsl;    // qs * log2(e)
@@ -339,23 +338,40 @@ __device__ __forceinline__ Lanes make_lanes(int n, int half) {
 // sub-step before PV reads it, and touches O^T only in the exact path and the epilogue, both
 // behind explicit waits.
 constexpr int kOReg = 192;  // first VGPR of O^T
+// P, PV's B operand: the probabilities of the 32-key tile of parity `par` as packed f16, 16 keys
+// per MFMA group g, in v[kPReg + 8 par + 4 g .. +3] (four words: quarters 2g and 2g+1, two words
+// each). Written by the softmax's conversions and read by the PV MFMAs in place, so no copies sit
+// between them; the compiler's share ends below kPReg.
+constexpr int kPReg = 176;
 #define H3_V16(b) "v" #b "0", "v" #b "1", "v" #b "2", "v" #b "3", "v" #b "4", "v" #b "5", \
                   "v" #b "6", "v" #b "7", "v" #b "8", "v" #b "9"
+#define H3_P_CLOBBERS "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", \
+    "v185", "v186", "v187", "v188", "v189", "v190", "v191"
 #define H3_O_CLOBBERS "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", H3_V16(20), \
     H3_V16(21), H3_V16(22), H3_V16(23), H3_V16(24), "v250", "v251", "v252", "v253", "v254", "v255"
 
-// O^T block at VGPR kBase += V^T . P^T
-template <int kBase>
-__device__ __forceinline__ void pv_block(v8h v, v8h p) {
-  asm volatile("v_mfma_f32_32x32x16_f16 v[%2:%3], %0, %1, v[%2:%3]"
-               :: "v"(v), "v"(p), "n"(kBase), "n"(kBase + 15) : H3_O_CLOBBERS);
+// O^T block at VGPR kBase += V^T . P^T, P group at VGPR kP
+template <int kBase, int kP>
+__device__ __forceinline__ void pv_block(v8h v) {
+  asm volatile("v_mfma_f32_32x32x16_f16 v[%1:%2], %0, v[%3:%4], v[%1:%2]"
+               :: "v"(v), "n"(kBase), "n"(kBase + 15), "n"(kP), "n"(kP + 3) : H3_O_CLOBBERS);
 }
-__device__ __forceinline__ void pv_mfma(int db, v8h v, v8h p) {
+template <int kP>
+__device__ __forceinline__ void pv_group(int db, v8h v) {
   switch (db) {  // db is a constant once the chunk loop is unrolled
-    case 0: pv_block<kOReg>(v, p); break;
-    case 1: pv_block<kOReg + 16>(v, p); break;
-    case 2: pv_block<kOReg + 32>(v, p); break;
-    default: pv_block<kOReg + 48>(v, p); break;
+    case 0: pv_block<kOReg, kP>(v); break;
+    case 1: pv_block<kOReg + 16, kP>(v); break;
+    case 2: pv_block<kOReg + 32, kP>(v); break;
+    default: pv_block<kOReg + 48, kP>(v); break;
+  }
+}
+// PV for channel block db with P group g of parity par (all constants once unrolled).
+__device__ __forceinline__ void pv_mfma(int db, v8h v, int par, int g) {
+  switch (2 * par + g) {
+    case 0: pv_group<kPReg>(db, v); break;
+    case 1: pv_group<kPReg + 4>(db, v); break;
+    case 2: pv_group<kPReg + 8>(db, v); break;
+    default: pv_group<kPReg + 12>(db, v); break;
   }
 }
 // Accumulator register kOReg + kR *= alpha, its read for the epilogue, and its clearing.
@@ -496,40 +512,45 @@ __device__ __forceinline__ void exp3_quarter(float (&y)[4], float& a) {
                "v_add_f32 %3, %0, %1"
                : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "=&v"(a));
 }
-__device__ __forceinline__ void exp_pack_quarter(float (&y)[4], uint32_t (&w)[2], float& a,
-                                                 float& ts) {
+template <int kW>
+__device__ __forceinline__ void exp_pack_to(float (&y)[4], float& a, float& ts) {
   float b;
-  asm volatile("v_exp_f32 %3, %3\n\t"
-               "v_cvt_pk_f16_f32 %0, %6, %7\n\t"
-               "v_cvt_pk_f16_f32 %1, %8, %3\n\t"
-               "v_add_f32 %2, %8, %3\n\t"
-               "v_add_f32 %4, %4, %2\n\t"
-               "v_add_f32 %5, %5, %4"
-               : "=&v"(w[0]), "=&v"(w[1]), "=&v"(b), "+v"(y[3]), "+v"(a), "+v"(ts)
-               : "v"(y[0]), "v"(y[1]), "v"(y[2]));
+  asm volatile("v_exp_f32 %1, %1\n\t"
+               "v_cvt_pk_f16_f32 v[%4], %6, %7\n\t"
+               "v_cvt_pk_f16_f32 v[%5], %8, %1\n\t"
+               "v_add_f32 %0, %8, %1\n\t"
+               "v_add_f32 %2, %2, %0\n\t"
+               "v_add_f32 %3, %3, %2"
+               : "=&v"(b), "+v"(y[3]), "+v"(a), "+v"(ts)
+               : "n"(kW), "n"(kW + 1), "v"(y[0]), "v"(y[1]), "v"(y[2])
+               : H3_P_CLOBBERS);
 }
-// The words of quarter i go to group i/2 (16 keys), elements 4(i%2)..+3.
-__device__ __forceinline__ void put_quarter(v8h (&p)[2], int i, const uint32_t (&w)[2]) {
-  const v2h a = __builtin_bit_cast(v2h, w[0]), b = __builtin_bit_cast(v2h, w[1]);
-  const int g = i >> 1, e = 4 * (i & 1);
-  p[g][e + 0] = a[0];
-  p[g][e + 1] = a[1];
-  p[g][e + 2] = b[0];
-  p[g][e + 3] = b[1];
+// The fourth exponential of quarter i, the f16 packing of (p0, p1) and (p2, p3) into the P words
+// of parity par (group i/2, words 2(i%2) and +1) and the rest of the quarter's sum into `ts`.
+__device__ __forceinline__ void exp_pack_quarter(float (&y)[4], float& a, float& ts, int par,
+                                                 int i) {
+  switch (8 * par + 2 * i) {  // constants once unrolled
+    case 0: exp_pack_to<kPReg + 0>(y, a, ts); break;
+    case 2: exp_pack_to<kPReg + 2>(y, a, ts); break;
+    case 4: exp_pack_to<kPReg + 4>(y, a, ts); break;
+    case 6: exp_pack_to<kPReg + 6>(y, a, ts); break;
+    case 8: exp_pack_to<kPReg + 8>(y, a, ts); break;
+    case 10: exp_pack_to<kPReg + 10>(y, a, ts); break;
+    case 12: exp_pack_to<kPReg + 12>(y, a, ts); break;
+    default: exp_pack_to<kPReg + 14>(y, a, ts); break;
+  }
 }
 
-// The probabilities of quarter i against negm: y, then p = 2^y packed as PV's operand into
-// T.p[par], and its share of the tile sum.
+// The probabilities of quarter i against negm: y, then p = 2^y packed as PV's operand into the P
+// words of parity par, and its share of the tile sum.
 template <bool kMasked>
 __device__ __forceinline__ float probs_quarter(Tile& T, int par, int i, float4 k4, float4 c4,
                                                float ts) {
   float y[4];
-  uint32_t w[2];
   float a;
   scores<kMasked>(T.s[par], i, k4, c4, T.qsl, T.cq, T.negm, y);
   exp3_quarter(y, a);
-  exp_pack_quarter(y, w, a, ts);
-  put_quarter(T.p[par], i, w);
+  exp_pack_quarter(y, a, ts, par, i);
   return ts;
 }
 
@@ -598,12 +619,10 @@ __device__ __forceinline__ void first_tile(Tile& T, int par, const float* kss, i
   float ts = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    uint32_t w[2];
     float a;
     exparg_quarter(u[i], T.qsl, T.negm);
     exp3_quarter(u[i], a);
-    exp_pack_quarter(u[i], w, a, ts);
-    put_quarter(T.p[par], i, w);
+    exp_pack_quarter(u[i], a, ts, par, i);
   }
   T.l = ts;
   asm volatile("s_nop 7" ::: "memory");  // fresh P before the next MFMA reads it
@@ -674,7 +693,6 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
   v8h vop[8];
   float4 k4[4], c4[4];
   float y[4], ysum;
-  uint32_t w[2];
   float ts = 0.0f;  // the lane's tile sum
   auto read_op = [&](int o) {
     if (o >= 4 && kPV) {
@@ -720,19 +738,18 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
       }
     } else if (kPV) {
       const int v = c - 4;
-      pv_mfma(v & 3, vop[v], T.p[kPar][v >> 2]);
+      pv_mfma(v & 3, vop[v], kPar, v >> 2);
     }
     if (kSM && !kFirst) {
       // quarter c/3: exponent arguments; three exponentials; the fourth with the packing and
-      // the quarter's share of the tile sum (two dot products into f32)
+      // the quarter's share of the tile sum
       const int i = c / 3, phase = c % 3;
       if (phase == 0) {
         scores<kMasked>(T.s[kSm], i, k4[i], c4[i], T.qsl, T.cq, T.negm, y);
       } else if (phase == 1) {
         exp3_quarter(y, ysum);
       } else {
-        exp_pack_quarter(y, w, ysum, ts);
-        put_quarter(T.p[kSm], i, w);
+        exp_pack_quarter(y, ysum, ts, kSm, i);
         if (i == 0 || i == 1) read_scales(i + 2);
       }
     }
@@ -777,7 +794,7 @@ __device__ __forceinline__ char* ring(int i, char* a0, char* a1, char* a2, char*
 
 template <bool kCross, bool kChain, bool kFp6 = false>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(2, 2), amdgpu_num_vgpr(kOReg)))
+__attribute__((amdgpu_waves_per_eu(2, 2), amdgpu_num_vgpr(kPReg)))
 void k_attention_hm(Geometry g) {
   // Four-stage rings, each stage its own array so that the compiler can tell an LDS-DMA into one
   // stage from the reads of another.
