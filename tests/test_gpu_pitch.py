@@ -150,3 +150,37 @@ def test_stack_direct_attention_route(dev, tokens):
                            O.unpack(kw).reshape(heads, cap, 128), ks, vt, tokens, cap, heads,
                            rows)
     check_padded_output(out.cpu().numpy(), tokens, pitch, inner, rows, want)
+
+
+@pytest.mark.parametrize("tokens", [1000, 5000])
+def test_fp6_attention_at_a_direct_pitch(dev, tokens):
+    """h3_attention_i4qk_fp6 (int4 operands converted to FP6, the head-major kernel's FP6 form)
+    under a padded output pitch: 4 heads (inner 512, pitch 640); 1,000 tokens run the chained
+    kernel, 5,000 the unchained one."""
+    import torch
+
+    from test_gpu_i4 import pack_i4
+
+    heads = 4
+    inner = heads * 128
+    pitch = gemm_pitch16(inner)
+    assert pitch == 640
+    cap = H.capacity(tokens)
+    rng = np.random.default_rng(tokens + 640)
+    qc, qs, kc, ks, vt = int_operands(rng, heads, tokens, cap)
+    # int4 codes in [-7, 7] in place of the int8 ones (capacity rows stay zero)
+    qc[:, :tokens] = rng.integers(-7, 8, (heads, tokens, 128), dtype=np.int8)
+    kc[:, :tokens] = rng.integers(-7, 8, (heads, tokens, 128), dtype=np.int8)
+    tm = lambda c: pack_i4(np.ascontiguousarray(c.transpose(1, 0, 2)).reshape(cap, inner))
+    cfg = H.AttentionCfg(inner, inner, pitch, tokens, cap, 1.0)
+    ws = torch.zeros((H.fp6_workspace_bytes(cfg),), dtype=torch.uint8, device=dev)
+    out = filled((tokens * pitch * 2 + GUARD,), 0xFF, np.uint8, dev)
+    print(f"fp6 attention at a direct pitch: S={tokens} H={heads} out_stride={pitch}", flush=True)
+    H.attention_i4qk_fp6(cfg, tokens, heads, to_dev(tm(qc), dev), to_dev(qs.T.copy(), dev),
+                         to_dev(tm(kc), dev), to_dev(ks.T.copy(), dev), to_dev(vt, dev),
+                         out[: tokens * pitch * 2], ws)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([[0, 31, 32, 255, 256, tokens - 1],
+                                     rng.integers(0, tokens, 4)])).astype(np.int32)
+    want = O.attention_f64(qc, qs, kc, ks, vt, tokens, cap, heads, rows)
+    check_padded_output(out.cpu().numpy(), tokens, pitch, inner, rows, want)
