@@ -277,6 +277,28 @@ __device__ __forceinline__ void step_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
+// Issue priority of the two waves of a SIMD. The matrix pipe serves the older wave (waves 0-3)
+// first when both have an MFMA ready, so with equal priorities waves 0-3 finished a step's first
+// sub-step in ~1,160 cycles and waves 4-7 in ~1,780, and waves 0-3 then idled ~870 cycles of a
+// ~3,020-cycle step at the barrier while waves 4-7 ran alone (s_memtime stamps at C3). Waves 4-7
+// take priority 1 for the first sub-step of every steady step and all waves return to 0 for the
+// second: the barrier wait falls to ~240 cycles and a step to ~2,840 (-2.4 to -3.1 % at C3).
+// Longer or shorter windows measured worse. The choice between the two values is made inside
+// the asm (a scalar branch the compiler does not see), so the steady loop's control flow, and
+// the register allocation around its inline-asm MFMAs, stay as they are.
+__device__ __forceinline__ void prio_late_waves_first(uint32_t wave) {
+  asm volatile(
+      "s_cmp_lt_u32 %0, 4\n\t"
+      "s_cbranch_scc1 1f\n\t"
+      "s_setprio 1\n\t"
+      "s_branch 2f\n"
+      "1:\n\t"
+      "s_setprio 0\n"
+      "2:" ::"s"(wave)
+      : "scc");
+}
+__device__ __forceinline__ void prio_equal() { asm volatile("s_setprio 0"); }
+
 // The wave's 32-query tile. S^T and P are double-buffered by the parity of the 32-key tile they
 // belong to.
 struct Tile {
@@ -977,6 +999,7 @@ void k_attention_hm(Geometry g) {
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
     sub_step<0, true, true, true, kFp6, false, kCross>(vr(J), sr(J), 1, T, ln, half, magic, pre,
                                                        [&](int c, Pre& next) {
+      if (c == 0) prio_late_waves_first(wave);
       if (c == 0)
         store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_hold[J & 1], keep_hold[J & 1],
                                          stage_of(j + 3) * kKeys, g.tokens);
@@ -985,6 +1008,7 @@ void k_attention_hm(Geometry g) {
       if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
     });
     auto stage1 = [&](int c, Pre& next) {
+      if (c == 0) prio_equal();
       const int slot = (c + 12) / kLoadGap;
       if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
       if (c == kBarrierChunk) step_barrier<kWaitTwoSteps<kCross>>();
