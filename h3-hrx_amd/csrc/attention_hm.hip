@@ -89,11 +89,18 @@ constexpr int kWaitAll = 0 | (7 << 4) | (0 << 8);
 constexpr int kWaitLds = 0xF | (7 << 4) | (0 << 8) | (3 << 14);
 constexpr int kWaitLdsWrites = kWaitLds;  // the same wait, named for its use in the epilogue
 static_assert(2 * kVmemPerStep<true> < 16, "the vmcnt field's low four bits hold the count");
-constexpr int kPf = 4;                            // V^T operands read this many chunks ahead
+// V^T operands are read kPf chunks ahead of their MFMA, and a step's barrier comes right after
+// the last operand read of its second sub-step, at chunk 12 - kPf. The unchained INT8 kernel
+// reads 5 ahead (0.5 % faster at C3 than 4, with the priority scheme below); the chained ones
+// keep 4, where 5 makes the compiler spill 4-12 dwords, and so does the FP6 form, which 5 made
+// 0.7 % slower.
+template <bool kChain, bool kFp6>
+constexpr int kPf = kChain || kFp6 ? 4 : 5;
+template <bool kChain, bool kFp6>
+constexpr int kBarrierChunk = 12 - kPf<kChain, kFp6>;
 constexpr int kKBias = 65536;                     // see Lanes
-constexpr int kBarrierChunk = 8;
 constexpr int kOStage = kTileQ * 64 * 2;          // 4 KiB: 32 output rows x 64 channels of f16
-static_assert(4 * kOStage == kVStage, "four waves' output stages fill one V^T stage");                  // chunk of a step's second sub-step with its barrier
+static_assert(4 * kOStage == kVStage, "four waves' output stages fill one V^T stage");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMagic = 12582912.0f;             // 1.5 * 2^23, the QK accumulators' bias
 constexpr int kMagicBits = 0x4B400000;            // its bit pattern
@@ -697,7 +704,7 @@ __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, in
 // assembly, whose order the compiler keeps); then its LDS reads and whatever `stage(c, next)`
 // issues (staging loads, the step barrier, the reads of the next sub-step's `Pre`). The K chunks
 // and the first two quarters' key scales come in `pre`, read during the sub-step before; the 8
-// V^T chunks are read kPf chunks ahead. QK comes first, so the S^T it writes is read by the
+// V^T chunks are read kPfT chunks ahead. QK comes first, so the S^T it writes is read by the
 // vector ALU only in the next sub-step, after this one's 8 PV MFMAs. The softmax runs quarter by
 // quarter (4 keys of each lane half), three chunks each (the exponent arguments, three
 // exponentials, the last one with the f16 packing and the quarter's share of the tile sum), with
@@ -705,7 +712,7 @@ __device__ __forceinline__ void prefetch(Pre& pre, int part, const char* kst, in
 // the lane's tile sum right away (f32 adds), so the overflow check after the last chunk waits on
 // a few instructions only.
 template <int kPar, bool kQK, bool kPV, bool kSM, bool kFp6, bool kFirst = false,
-          bool kMasked = false, typename Stage>
+          bool kMasked = false, int kPfT = 4, typename Stage>
 __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int sb, Tile& T,
                                          const Lanes& ln, int half, const v16i& magic, Pre& pre,
                                          Stage&& stage) {
@@ -743,7 +750,7 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
 #pragma unroll
   for (int i = 2; i < 4; ++i) c4[i] = k4[0];  // defined before read_scales fills them
 #pragma unroll
-  for (int o = 4; o < 4 + kPf; ++o) read_op(o);
+  for (int o = 4; o < 4 + kPfT; ++o) read_op(o);
 #pragma unroll
   for (int c = 0; c < 12; ++c) {
     if (c < 4) {
@@ -776,7 +783,7 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
         if (i == 0 || i == 1) read_scales(i + 2);
       }
     }
-    if (c >= 4 && c + kPf < 12) read_op(c + kPf);
+    if (c >= 4 && c + kPfT < 12) read_op(c + kPfT);
     stage(c, pre);
     H3_CHUNK_END();
   }
@@ -794,16 +801,16 @@ __device__ __forceinline__ void sub_step(const char* vst, const char* sst, int s
 
 // The reads of the next step's first `Pre` (K stage `kst` block 0, scale stage `sst` block 1) in
 // the chunks after the step barrier of a step's second sub-step.
-template <bool kFp6>
+template <bool kFp6, int kBar>
 __device__ __forceinline__ void next_step_reads(int c, Pre& next, const char* kst, const char* sst,
                                                 const Lanes& ln) {
-  if (c == kBarrierChunk + 1) {
+  if (c == kBar + 1) {
     prefetch<kFp6>(next, 0, kst, 0, sst, 1, ln);
     prefetch<kFp6>(next, 4, kst, 0, sst, 1, ln);
-  } else if (c == kBarrierChunk + 2) {
+  } else if (c == kBar + 2) {
     prefetch<kFp6>(next, 1, kst, 0, sst, 1, ln);
     prefetch<kFp6>(next, 5, kst, 0, sst, 1, ln);
-  } else if (c == kBarrierChunk + 3) {
+  } else if (c == kBar + 3) {
     prefetch<kFp6>(next, 2, kst, 0, sst, 1, ln);
     prefetch<kFp6>(next, 3, kst, 0, sst, 1, ln);
   }
@@ -827,6 +834,8 @@ void k_attention_hm(Geometry g) {
   auto kr = [&](int i) { return ring(i & 3, k0s, k1s, k2s, k3s); };
   auto vr = [&](int i) { return ring(i & 3, v0s, v1s, v2s, v3s); };
   auto sr = [&](int i) { return ring(i & 3, s0s, s1s, s2s, s3s); };
+  constexpr int kPfK = kPf<kChain, kFp6>;
+  constexpr int kBarK = kBarrierChunk<kChain, kFp6>;
 
   // Persistent workgroups, XCD-aware: the hardware hands workgroup b to XCD b % 8, and each XCD
   // owns a contiguous range of per_xcd (head, query block) blocks, which its wpx workgroups take
@@ -975,8 +984,8 @@ void k_attention_hm(Geometry g) {
   sub_step<1, true, false, true, kFp6, kCross, true>(nullptr, s0s, 0, T, ln, half, magic, pre,
                                                       [&](int c, Pre& next) {
     if (c == 0) store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
-    if (c == kBarrierChunk) step_barrier<kWaitPrevStep<kCross>>();
-    next_step_reads<kFp6>(c, next, k1s, s0s, ln);
+    if (c == kBarK) step_barrier<kWaitPrevStep<kCross>>();
+    next_step_reads<kFp6, kBarK>(c, next, k1s, s0s, ln);
   });
   // Key scales (and mask bytes) in registers until their store: those loaded in step j (stage
   // j+5) wait in hold[j % 2] for step j+2; the prologue's (stage 3) count as step -2's.
@@ -987,18 +996,18 @@ void k_attention_hm(Geometry g) {
   // scales of tiles 2j+1 (stage j, block 1) and 2j+2 (stage j+1, block 0); the step stages K(j+4)
   // into K(j)'s array and V(j+3) into V(j-1)'s, loads the scale of stage j+5, and stores the
   // scales of stage j+3 (loaded two steps earlier) into S(j-1)'s. Every K and V^T load has three
-  // steps to land, every scale two. The step's barrier comes once its last read of K(j+1) and V(j) is issued (chunk
-  // kBarrierChunk of its second sub-step), after a wait for this wave's loads of two steps
-  // before; the reads for the next step's first sub-step follow it. Stages past the last are the
-  // next block's first ones when the blocks chain.
+  // steps to land, every scale two. The step's barrier comes once its last read of K(j+1) and
+  // V(j) is issued (chunk kBarK of its second sub-step), after a wait for this wave's loads of
+  // two steps before; the reads for the next step's first sub-step follow it. Stages past the
+  // last are the next block's first ones when the blocks chain.
   uint32_t j = 0;
   auto steady = [&](auto J_) {
     constexpr int J = decltype(J_)::value;
     StepLoads L = plan_step<kCross>(g, kv_head, stage_of(j + 4) * kKeys, kr(J),
                                     stage_of(j + 3) * kKeys, vr(J + 3), stage_of(j + 5) * kKeys);
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
-    sub_step<0, true, true, true, kFp6, false, kCross>(vr(J), sr(J), 1, T, ln, half, magic, pre,
-                                                       [&](int c, Pre& next) {
+    sub_step<0, true, true, true, kFp6, false, kCross, kPfK>(
+        vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
       if (c == 0) prio_late_waves_first(wave);
       if (c == 0)
         store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_hold[J & 1], keep_hold[J & 1],
@@ -1011,15 +1020,15 @@ void k_attention_hm(Geometry g) {
       if (c == 0) prio_equal();
       const int slot = (c + 12) / kLoadGap;
       if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
-      if (c == kBarrierChunk) step_barrier<kWaitTwoSteps<kCross>>();
-      next_step_reads<kFp6>(c, next, kr(J + 2), sr(J + 1), ln);
+      if (c == kBarK) step_barrier<kWaitTwoSteps<kCross>>();
+      next_step_reads<kFp6, kBarK>(c, next, kr(J + 2), sr(J + 1), ln);
     };
     // Tile 2j+2 (keys 64(j+1) ..) holds keys past the sequence in the last steady step when the
     // sequence ends inside its 32 keys: this sub-step always takes the masked path. (A branch
     // between the two paths here puts register copies at its join that the inline-assembly
     // MFMAs after it may read before they land, which the compiler does not guard against.)
-    sub_step<1, true, true, true, kFp6, false, true>(vr(J), sr(J + 1), 0, T, ln, half, magic, pre,
-                                                     stage1);
+    sub_step<1, true, true, true, kFp6, false, true, kPfK>(vr(J), sr(J + 1), 0, T, ln, half,
+                                                           magic, pre, stage1);
     ks_hold[J & 1] = L.ks;
     keep_hold[J & 1] = L.keep;
     ++j;
@@ -1039,9 +1048,10 @@ void k_attention_hm(Geometry g) {
   // ---- last step (j = n_stages - 1): PV of tiles 2j and 2j+1, the probabilities of 2j+1 between
   // (its scales came in `pre`; its K reads there are unused). Tile 2j+1 may hold keys past the
   // sequence: the masked path.
-  sub_step<0, false, true, true, kFp6, false, true>(vr(j), sr(j), 1, T, ln, half, magic, pre,
-                                                    [](int, Pre&) {});
-  sub_step<1, false, true, false, kFp6>(vr(j), nullptr, 0, T, ln, half, magic, pre, [](int, Pre&) {});
+  sub_step<0, false, true, true, kFp6, false, true, kPfK>(vr(j), sr(j), 1, T, ln, half, magic,
+                                                          pre, [](int, Pre&) {});
+  sub_step<1, false, true, false, kFp6, false, false, kPfK>(vr(j), nullptr, 0, T, ln, half,
+                                                            magic, pre, [](int, Pre&) {});
   step_barrier<kWaitAll>();  // no staging load outlives the block (chained ones have landed)
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // the last PV MFMAs have landed
 
