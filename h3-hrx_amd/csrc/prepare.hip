@@ -276,14 +276,20 @@ __device__ __forceinline__ RopeLane8 rope_lane8(int l, const float* weight, cons
   return t;
 }
 
-__device__ __forceinline__ void rmsnorm_rope_f16(float (&v)[8], int l, const RopeLane8& tab,
-                                                 float eps) {
+// r = 1/sqrt(mean(v^2) + eps) of the row held by a 16-lane group, eight channels per lane:
+// rms_inverse's operations in its order (the lane partial is that layout's first butterfly sum).
+__device__ __forceinline__ float rms_inverse8(const float (&v)[8], float eps) {
   const float p0 = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
   const float p1 = ((v[4] * v[4] + v[5] * v[5]) + v[6] * v[6]) + v[7] * v[7];
   const float part = row16_sum(p0 + p1);
   const float ms = part * 0.0078125f;
   const float me = ms + eps;
-  const float r = 1.0f / __builtin_sqrtf(me);
+  return 1.0f / __builtin_sqrtf(me);
+}
+
+__device__ __forceinline__ void rmsnorm_rope_f16(float (&v)[8], int l, const RopeLane8& tab,
+                                                 float eps) {
+  const float r = rms_inverse8(v, eps);
   float xn[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) xn[j] = (v[j] * r) * tab.w[j];
@@ -511,37 +517,38 @@ __global__ __launch_bounds__(64) void k_colmean(const void* __restrict__ x,
 // token order in fp32, one dependent add per token (kernels/colmean_f32.loom in-file 30-40). The
 // add chain of each column is inherently sequential; everything feeding it is spread out.
 //
-// Pass 1 (k_rope_rms): r of every (token, head) row, one row per half-wave, head-major into a
-// float buffer [heads][capacity] (the scales binding, which the quantizer pass then overwrites).
-// Rows are taken head-major (row = h * tokens + t), so a workgroup's writes are contiguous; each
-// half-wave loads kRowsAhead rows before reducing any, and the grid strides over the rows.
-constexpr uint32_t kRmsRowsPerStep = kRowsPerBlock * kRowsAhead;  // 32 rows per workgroup step
+// Pass 1 (k_rope_rms): r of every (token, head) row into a float buffer [heads][capacity] (the
+// scales binding, which the quantizer pass then overwrites). One row per 16-lane group, eight
+// channels per lane (rms_inverse8, the same bits as the four-channel layout). A workgroup takes
+// kRmsTokens consecutive tokens; group g walks heads g, g + 16, ... and for each loads that
+// head's row of all kRmsTokens tokens before reducing any (16 rows, 64 KiB per workgroup in
+// flight), so the 16 groups read whole contiguous runs of the fused rows. Lane i of the group
+// then stores token i's r: one 64-byte store per head.
+constexpr int kRmsTokens = 16;
+template <int kElem>
 __global__ __launch_bounds__(256) void k_rope_rms(const void* __restrict__ x,
                                                   float* __restrict__ r_out, uint32_t tokens,
                                                   uint32_t heads, uint32_t row_stride,
                                                   uint32_t head_offset, uint32_t capacity,
-                                                  float eps, uint32_t elem) {
-  const int half = threadIdx.x >> 5, lane = threadIdx.x & 31;
-  const uint32_t rows = tokens * heads;
-  for (uint32_t base = blockIdx.x * kRmsRowsPerStep; base < rows;
-       base += gridDim.x * kRmsRowsPerStep) {
-    v4f v[kRowsAhead];
-    uint32_t row[kRowsAhead];
+                                                  float eps) {
+  const int g = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const uint32_t t0 = blockIdx.x * kRmsTokens;
+  for (uint32_t h = g; h < heads; h += kGroupsPerBlock) {
+    uint4 raw[kRmsTokens];
 #pragma unroll
-    for (int i = 0; i < kRowsAhead; ++i) {
-      row[i] = base + kRowsPerBlock * i + half;
-      const uint32_t rr = row[i] < rows ? row[i] : rows - 1;  // every lane stays in the butterfly
-      const uint32_t h = rr / tokens, t = rr - h * tokens;
-      v[i] = widen4(load4(x, (size_t)t * row_stride + head_offset + 128u * h + 4u * lane), elem);
+    for (int i = 0; i < kRmsTokens; ++i) {
+      const uint32_t t = min(t0 + i, tokens - 1);  // every lane stays in the butterfly
+      raw[i] = load8(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
     }
+    float mine = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRowsAhead; ++i) {
-      const float r = rms_inverse(v[i], eps);
-      if (row[i] < rows && lane == 0) {
-        const uint32_t h = row[i] / tokens, t = row[i] - h * tokens;
-        r_out[(size_t)h * capacity + t] = r;
-      }
+    for (int i = 0; i < kRmsTokens; ++i) {
+      float v[8];
+      widen8(raw[i], kElem, v);
+      const float r = rms_inverse8(v, eps);
+      mine = l == i ? r : mine;
     }
+    if (t0 + l < tokens) r_out[(size_t)h * capacity + t0 + l] = mine;
   }
 }
 
@@ -843,11 +850,15 @@ hipError_t launch_colmean(uint32_t width, uint32_t row_stride, uint32_t elem, ui
 hipError_t launch_rope_colmean(const h3_prepare_cfg& cfg, uint32_t tokens, const void* x,
                                const float* weight, const float* cos_t, const float* sin_t,
                                float* r_scratch, float* mean, hipStream_t stream) {
-  const uint32_t rows = tokens * cfg.heads;
-  const uint32_t rms_blocks = std::min(div_up(rows, kRmsRowsPerStep), 8192u);
-  hipLaunchKernelGGL(k_rope_rms, dim3(rms_blocks), dim3(256), 0, stream, x,
-                     r_scratch, tokens, cfg.heads, cfg.row_stride, cfg.head_offset,
-                     cfg.token_capacity, cfg.eps, cfg.elem);
+  const dim3 rms_grid(div_up(tokens, kRmsTokens));
+  if (cfg.elem == H3_ELEM_BF16)
+    hipLaunchKernelGGL(k_rope_rms<H3_ELEM_BF16>, rms_grid, dim3(256), 0, stream, x, r_scratch,
+                       tokens, cfg.heads, cfg.row_stride, cfg.head_offset, cfg.token_capacity,
+                       cfg.eps);
+  else
+    hipLaunchKernelGGL(k_rope_rms<H3_ELEM_F16>, rms_grid, dim3(256), 0, stream, x, r_scratch,
+                       tokens, cfg.heads, cfg.row_stride, cfg.head_offset, cfg.token_capacity,
+                       cfg.eps);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const uint32_t total = cfg.heads * kSlabs, per_xcd = div_up(total, 8);
