@@ -404,41 +404,219 @@ __global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ 
   }
 }
 
+// ---------------------------------------------------------------- 8-lane row groups
+// The RoPE quantizer holds one 128-channel row in an 8-lane group, sixteen channels per lane
+// (two 16-byte loads): a wave then works on eight rows at once, so the per-row work (the norm's
+// square root and division, the quantizer's two divisions, the reductions) is spread over twice
+// as many rows as in the 16-lane layout, and one more Hadamard stage runs inside the lane. The
+// lane of local index i holds channels 16i..16i+15, i.e. the four-channel lanes 4i..4i+3 of the
+// 32-lane layout; every sum below is formed from the same two operands in the same order as
+// there, so the bits are the same. A group's lanes are those that differ in lane bits 0, 1 and
+// 3 (local bits 0, 1, 2), so its three partner exchanges are single DPP moves (quad_perm,
+// quad_perm, row_ror:8), where lane bit 2 would need two.
+__device__ __forceinline__ int local8(int lane) { return (lane & 3) | ((lane >> 1) & 4); }
+__device__ __forceinline__ int group8(int lane) { return ((lane >> 2) & 1) | ((lane >> 3) & 6); }
+// The lane of local index i in the group of `lane`.
+__device__ __forceinline__ int lane8(int lane, int i) { return (lane & 0x34) | (i & 3) | ((i & 4) << 1); }
+constexpr int kLane8Xor[3] = {1, 2, 8};  // lane exchange of local bit 0, 1, 2
+__device__ __forceinline__ float row8_sum(float v) {  // local order 1, 2, 4
+#pragma unroll
+  for (int b = 0; b < 3; ++b) v = v + xor_partner(v, kLane8Xor[b]);
+  return v;
+}
+__device__ __forceinline__ float row8_max(float v) {
+#pragma unroll
+  for (int b = 2; b >= 0; --b) v = fmaxf(v, xor_partner(v, kLane8Xor[b]));
+  return v;
+}
+
+struct RopeLane16 {
+  float w[16], c[16], s[16];
+};
+
+// Norm weights of the lane's channels and, for lanes 0-5 (channels 0-95), the cos/sin columns
+// of their rotation pairs: channel c < 48 and c + 48 share column c. Lanes 0-2 keep -sin, so that
+// both halves of the rotation are one addition (a + (-b) is a - b exactly; -(px*sin) is
+// px*(-sin) exactly).
+__device__ __forceinline__ RopeLane16 rope_lane16(int l, const float* weight, const float* cos_row,
+                                                  const float* sin_row) {
+  const int pairlane = l < 3 ? l : (l < 6 ? l - 3 : 0);
+  RopeLane16 t;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 w = *reinterpret_cast<const float4*>(weight + 16 * l + 4 * q);
+    const float4 c = *reinterpret_cast<const float4*>(cos_row + 16 * pairlane + 4 * q);
+    const float4 sn = *reinterpret_cast<const float4*>(sin_row + 16 * pairlane + 4 * q);
+    t.w[4 * q] = w.x; t.w[4 * q + 1] = w.y; t.w[4 * q + 2] = w.z; t.w[4 * q + 3] = w.w;
+    t.c[4 * q] = c.x; t.c[4 * q + 1] = c.y; t.c[4 * q + 2] = c.z; t.c[4 * q + 3] = c.w;
+    t.s[4 * q] = sn.x; t.s[4 * q + 1] = sn.y; t.s[4 * q + 2] = sn.z; t.s[4 * q + 3] = sn.w;
+  }
+  if (l < 3) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t.s[j] = -t.s[j];
+  }
+  return t;
+}
+
+// rmsnorm_rope_f16 for a row held sixteen channels per lane: the four-channel partials p0..p3
+// of the 32-lane layout's lanes 4l..4l+3, its butterflies k = 1, 2 in the lane ((p0 + p1) +
+// (p2 + p3)), its k = 4, 8, 16 as the exchanges of local bits 0, 1, 2; the rotation partner is
+// local index l +- 3. `lane` is the wave lane, l its local index.
+__device__ __forceinline__ void rmsnorm_rope16(float (&v)[16], int lane, int l,
+                                               const RopeLane16& tab, float eps) {
+  float p[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    p[k] = ((v[4 * k] * v[4 * k] + v[4 * k + 1] * v[4 * k + 1]) + v[4 * k + 2] * v[4 * k + 2]) +
+           v[4 * k + 3] * v[4 * k + 3];
+  const float part = row8_sum((p[0] + p[1]) + (p[2] + p[3]));
+  const float ms = part * 0.0078125f;
+  const float me = ms + eps;
+  const float r = 1.0f / __builtin_sqrtf(me);
+  float xn[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) xn[j] = (v[j] * r) * tab.w[j];
+  const bool pair = l < 6;
+  const int partner = lane8(lane, l < 3 ? l + 3 : (pair ? l - 3 : l));
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float px = __shfl(xn[j], partner);
+    const float a = xn[j] * tab.c[j];
+    const float b = px * tab.s[j];  // tab.s is -sin on lanes 0-2: a + b is a - px*sin there
+    const float o = pair ? a + b : xn[j];
+    v[j] = f16_round(o);
+  }
+}
+
+// hadamard128 for sixteen elements per lane: element bits 0-1 (the radix-4 stage), 2 and 3 in
+// the lane, bits 4-6 across local bits 0, 1, 2; each stage keeps s + partner (bit clear) and
+// partner - s (bit set), the reference's operands in the reference's order. l: local index.
+__device__ __forceinline__ void hadamard128_16(float (&s)[16], int l) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float ab_p = s[4 * g] + s[4 * g + 1], ab_m = s[4 * g] - s[4 * g + 1];
+    const float cd_p = s[4 * g + 2] + s[4 * g + 3], cd_m = s[4 * g + 2] - s[4 * g + 3];
+    s[4 * g] = ab_p + cd_p;
+    s[4 * g + 1] = ab_m + cd_m;
+    s[4 * g + 2] = ab_p - cd_p;
+    s[4 * g + 3] = ab_m - cd_m;
+  }
+#pragma unroll
+  for (int b = 4; b <= 8; b <<= 1) {  // element bits 2 and 3
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (j & b) continue;
+      const float p = s[j] + s[j + b], m = s[j] - s[j + b];
+      s[j] = p;
+      s[j + b] = m;
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {  // element bits 4-6; fma(s, -1, p) is p - s exactly
+    const float sign = (l & (1 << b)) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s[j] = __builtin_fmaf(s[j], sign, xor_partner(s[j], kLane8Xor[b]));
+  }
+}
+
+// quantize_row for sixteen elements per lane; returns the lane's four words (elements
+// 16l..16l+15, low byte first). The code is clamp(rne(p), +-127) with p = r * inv, formed as
+// rne(clamp(p, +-127)) (the same integer for every p, NaN included: both give -127) by adding
+// 1.5 * 2^23: the sum is rounded to an integer, ties to even, and the low byte of its bits is
+// the code in two's complement.
+__device__ __forceinline__ uint4 quantize_row16(const float (&r)[16], float extra, float* scale) {
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(r[j]));
+  m = row8_max(m);
+  const float amax = fmaxf(m, 1.0000000000000001e-30f);
+  const float sc = amax / 127.0f;
+  const float inv = 127.0f / amax;
+  uint32_t b[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float q = fminf(fmaxf(r[j] * inv, -127.0f), 127.0f);
+    b[j] = __float_as_uint(q + 12582912.0f);
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = __builtin_amdgcn_perm(b[4 * k + 1], b[4 * k], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b[4 * k + 3], b[4 * k + 2], 0x04000c0cu);
+    w[k] = lo | hi;
+  }
+  *scale = sc * extra;
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
 // (kernels/prepare_qk_rope_i8hm.loom:94-239; mean == nullptr is the reference's unsmoothed
-// kernel, a mean is this build's fused K-smoothing second pass). One 16-lane group owns one token
+// kernel, a mean is this build's fused K-smoothing second pass). One 8-lane group owns one token
 // and walks its heads with kRowsAhead heads in flight: the token's RoPE tables are read once
-// (not once per head), its heads' inputs are one contiguous run of the fused row, and the 16
-// groups of a workgroup write 16 consecutive head-major rows (2 KiB) per head.
+// (not once per head), its heads' inputs are one contiguous run of the fused row, and the 32
+// groups of a workgroup write 32 consecutive head-major rows (4 KiB) per head. Group g of wave w
+// takes token 32 * block + 8w + g.
+constexpr int kRopeGroups = 32;  // 256 threads = 32 groups of 8 lanes
+template <int kElem, bool kMean>
 __global__ __launch_bounds__(256) void k_prepare_qk_rope(
     const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const float* __restrict__ mean, int32_t* __restrict__ codes,
     float* __restrict__ scales, uint32_t tokens, uint32_t row_stride, uint32_t head_offset,
-    uint32_t heads, uint32_t capacity, float extra, float eps, uint32_t elem) {
-  const uint32_t t = blockIdx.x * kGroupsPerBlock + (threadIdx.x >> 4);
-  const int l = threadIdx.x & 15;
+    uint32_t heads, uint32_t capacity, float extra, float eps) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t t = blockIdx.x * kRopeGroups + 8 * (threadIdx.x >> 6) + group8(lane);
+  const int l = local8(lane);
   if (t >= tokens) return;
-  const RopeLane8 tab = rope_lane8(l, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48);
-  const size_t row0 = (size_t)t * row_stride + head_offset + 8u * l;
-  uint4 ring[kRowsAhead];  // heads h .. h + kRowsAhead - 1 in flight
+  const RopeLane16 tab = rope_lane16(l, weight, cos_t + (size_t)t * 48, sin_t + (size_t)t * 48);
+  const size_t row0 = (size_t)t * row_stride + head_offset + 16u * l;
+  uint4 ring[kRowsAhead][2];  // heads h .. h + kRowsAhead - 1 in flight
 #pragma unroll
   for (int i = 0; i < kRowsAhead; ++i)
-    if ((uint32_t)i < heads) ring[i] = load8(x, row0 + 128u * i);
+    if ((uint32_t)i < heads) {
+      ring[i][0] = load8(x, row0 + 128u * i);
+      ring[i][1] = load8(x, row0 + 128u * i + 8);
+    }
   for (uint32_t h0 = 0; h0 < heads; h0 += kRowsAhead) {
 #pragma unroll
     for (int i = 0; i < kRowsAhead; ++i) {
       const uint32_t h = h0 + i;
       if (h >= heads) break;
-      float y[8];
-      widen8(ring[i], elem, y);
-      if (h + kRowsAhead < heads) ring[i] = load8(x, row0 + 128u * (h + kRowsAhead));
-      rmsnorm_rope_f16(y, l, tab, eps);
-      subtract_mean(y, mean, 128u * h + 8u * l);
-      hadamard128(y, l);
+      float y[16];
+      {
+        float lo8[8], hi8[8];
+        widen8(ring[i][0], kElem, lo8);
+        widen8(ring[i][1], kElem, hi8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          y[j] = lo8[j];
+          y[8 + j] = hi8[j];
+        }
+      }
+      if (h + kRowsAhead < heads) {
+        ring[i][0] = load8(x, row0 + 128u * (h + kRowsAhead));
+        ring[i][1] = load8(x, row0 + 128u * (h + kRowsAhead) + 8);
+      }
+      float4 mu[4];  // the column means, loaded before the norm so that they land under it
+      if (kMean) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          mu[q] = *reinterpret_cast<const float4*>(mean + 128u * h + 16u * l + 4 * q);
+      }
+      rmsnorm_rope16(y, lane, l, tab, eps);
+      if (kMean) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          y[4 * q] = y[4 * q] - mu[q].x;
+          y[4 * q + 1] = y[4 * q + 1] - mu[q].y;
+          y[4 * q + 2] = y[4 * q + 2] - mu[q].z;
+          y[4 * q + 3] = y[4 * q + 3] - mu[q].w;
+        }
+      }
+      hadamard128_16(y, l);
       float scale;
-      const uint2 w = quantize_row(y, extra, &scale);
+      const uint4 w = quantize_row16(y, extra, &scale);
       const size_t out_row = (size_t)h * capacity + t;
-      reinterpret_cast<uint2*>(codes + out_row * 32)[l] = w;
+      reinterpret_cast<uint4*>(codes + out_row * 32)[l] = w;
       if (l == 0) scales[out_row] = scale;
     }
   }
@@ -821,10 +999,17 @@ hipError_t launch_prepare_qk_rope_mean(const h3_prepare_cfg& cfg, uint32_t token
                                        const float* weight, const float* cos_t,
                                        const float* sin_t, const float* mean, int32_t* codes,
                                        float* scales, hipStream_t stream) {
-  hipLaunchKernelGGL(k_prepare_qk_rope, dim3(div_up(tokens, kGroupsPerBlock)), dim3(256), 0, stream,
-                     x, weight, cos_t, sin_t, mean, codes, scales, tokens, cfg.row_stride,
-                     cfg.head_offset, cfg.heads, cfg.token_capacity, cfg.extra_scale, cfg.eps,
-                     cfg.elem);
+  const dim3 grid(div_up(tokens, kRopeGroups));
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, x, weight, cos_t, sin_t, mean, codes,
+                       scales, tokens, cfg.row_stride, cfg.head_offset, cfg.heads,
+                       cfg.token_capacity, cfg.extra_scale, cfg.eps);
+  };
+  const bool bf16 = cfg.elem == H3_ELEM_BF16;
+  if (mean)
+    bf16 ? launch(k_prepare_qk_rope<H3_ELEM_BF16, true>) : launch(k_prepare_qk_rope<H3_ELEM_F16, true>);
+  else
+    bf16 ? launch(k_prepare_qk_rope<H3_ELEM_BF16, false>) : launch(k_prepare_qk_rope<H3_ELEM_F16, false>);
   return hipGetLastError();
 }
 
