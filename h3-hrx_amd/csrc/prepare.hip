@@ -328,47 +328,6 @@ __device__ __forceinline__ void subtract_mean(float (&y)[8], const float* mean, 
   y[7] = y[7] - b.w;
 }
 
-// (token, head) rows, one per 16-lane group; group g of block b takes rows
-// b*16*kRowsAhead + 16i + g, i < kRowsAhead, all loads issued before the first row is processed.
-template <bool kHeadMajor>
-__global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
-                                                    const float* __restrict__ mean,
-                                                    int32_t* __restrict__ codes,
-                                                    float* __restrict__ scales, uint32_t tokens,
-                                                    uint32_t row_stride, uint32_t head_offset,
-                                                    uint32_t heads, uint32_t capacity,
-                                                    float extra, uint32_t elem) {
-  const uint32_t first = blockIdx.x * kGroupsPerBlock * kRowsAhead + (threadIdx.x >> 4);
-  const int l = threadIdx.x & 15;
-  const uint32_t total = tokens * heads;
-  uint4 in[kRowsAhead];
-#pragma unroll
-  for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kGroupsPerBlock * i;
-    if (row >= total) break;
-    // head-major rows walk tokens fastest (contiguous code stores), token-major rows walk heads
-    const uint32_t t = kHeadMajor ? row % tokens : row / heads;
-    const uint32_t h = kHeadMajor ? row / tokens : row % heads;
-    in[i] = load8(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
-  }
-#pragma unroll
-  for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kGroupsPerBlock * i;
-    if (row >= total) break;
-    const uint32_t t = kHeadMajor ? row % tokens : row / heads;
-    const uint32_t h = kHeadMajor ? row / tokens : row % heads;
-    float y[8];
-    widen8(in[i], elem, y);
-    subtract_mean(y, mean, head_offset + 128u * h + 8u * l);
-    hadamard128(y, l);
-    float scale;
-    const uint2 w = quantize_row(y, extra, &scale);
-    const size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
-    reinterpret_cast<uint2*>(codes + out_row * 32)[l] = w;
-    if (l == 0) scales[out_row] = scale;
-  }
-}
-
 // int4 operands, token-major (kernels/prepare_qk_i4.loom): the same rotation; a lane's eight
 // codes are one word of the row (codes [tokens][heads*16] i32).
 __global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ x,
@@ -419,6 +378,7 @@ __device__ __forceinline__ int group8(int lane) { return ((lane >> 2) & 1) | ((l
 // The lane of local index i in the group of `lane`.
 __device__ __forceinline__ int lane8(int lane, int i) { return (lane & 0x34) | (i & 3) | ((i & 4) << 1); }
 constexpr int kLane8Xor[3] = {1, 2, 8};  // lane exchange of local bit 0, 1, 2
+constexpr int kRopeGroups = 32;  // 256 threads = 32 groups of 8 lanes
 __device__ __forceinline__ float row8_sum(float v) {  // local order 1, 2, 4
 #pragma unroll
   for (int b = 0; b < 3; ++b) v = v + xor_partner(v, kLane8Xor[b]);
@@ -549,6 +509,71 @@ __device__ __forceinline__ uint4 quantize_row16(const float (&r)[16], float extr
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// (token, head) rows (kernels/prepare_qk_i8.loom, prepare_qk_i8hm.loom), one per 8-lane group;
+// group g of block b takes rows b*32*kRowsAhead + 32i + g, i < kRowsAhead, all loads issued
+// before the first row is processed. Head-major rows walk tokens fastest (contiguous code
+// stores), token-major rows walk heads.
+template <bool kHeadMajor, int kElem, bool kMean>
+__global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
+                                                    const float* __restrict__ mean,
+                                                    int32_t* __restrict__ codes,
+                                                    float* __restrict__ scales, uint32_t tokens,
+                                                    uint32_t row_stride, uint32_t head_offset,
+                                                    uint32_t heads, uint32_t capacity,
+                                                    float extra) {
+  const int lane = threadIdx.x & 63;
+  const int l = local8(lane);
+  const uint32_t first =
+      blockIdx.x * kRopeGroups * kRowsAhead + 8 * (threadIdx.x >> 6) + group8(lane);
+  const uint32_t total = tokens * heads;
+  uint4 in[kRowsAhead][2];
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t row = first + kRopeGroups * i;
+    if (row >= total) break;
+    const uint32_t t = kHeadMajor ? row % tokens : row / heads;
+    const uint32_t h = kHeadMajor ? row / tokens : row % heads;
+    const size_t at = (size_t)t * row_stride + head_offset + 128u * h + 16u * l;
+    in[i][0] = load8(x, at);
+    in[i][1] = load8(x, at + 8);
+  }
+#pragma unroll
+  for (int i = 0; i < kRowsAhead; ++i) {
+    const uint32_t row = first + kRopeGroups * i;
+    if (row >= total) break;
+    const uint32_t t = kHeadMajor ? row % tokens : row / heads;
+    const uint32_t h = kHeadMajor ? row / tokens : row % heads;
+    float y[16];
+    {
+      float lo8[8], hi8[8];
+      widen8(in[i][0], kElem, lo8);
+      widen8(in[i][1], kElem, hi8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        y[j] = lo8[j];
+        y[8 + j] = hi8[j];
+      }
+    }
+    if (kMean) {
+      const float* mc = mean + head_offset + 128u * h + 16u * l;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 m4 = *reinterpret_cast<const float4*>(mc + 4 * q);
+        y[4 * q] = y[4 * q] - m4.x;
+        y[4 * q + 1] = y[4 * q + 1] - m4.y;
+        y[4 * q + 2] = y[4 * q + 2] - m4.z;
+        y[4 * q + 3] = y[4 * q + 3] - m4.w;
+      }
+    }
+    hadamard128_16(y, l);
+    float scale;
+    const uint4 w = quantize_row16(y, extra, &scale);
+    const size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
+    reinterpret_cast<uint4*>(codes + out_row * 32)[l] = w;
+    if (l == 0) scales[out_row] = scale;
+  }
+}
+
 // RMSNorm + RoPE + f16 rounding + (optional mean subtraction) + quantizer, head-major output
 // (kernels/prepare_qk_rope_i8hm.loom:94-239; mean == nullptr is the reference's unsmoothed
 // kernel, a mean is this build's fused K-smoothing second pass). One 8-lane group owns one token
@@ -556,7 +581,6 @@ __device__ __forceinline__ uint4 quantize_row16(const float (&r)[16], float extr
 // (not once per head), its heads' inputs are one contiguous run of the fused row, and the 32
 // groups of a workgroup write 32 consecutive head-major rows (4 KiB) per head. Group g of wave w
 // takes token 32 * block + 8w + g.
-constexpr int kRopeGroups = 32;  // 256 threads = 32 groups of 8 lanes
 template <int kElem, bool kMean>
 __global__ __launch_bounds__(256) void k_prepare_qk_rope(
     const void* __restrict__ x, const float* __restrict__ weight, const float* __restrict__ cos_t,
@@ -966,15 +990,24 @@ hipError_t launch_prepare_qk(const h3_prepare_cfg& cfg, uint32_t tokens, int hea
                              const void* x, const float* mean, int32_t* codes, float* scales,
                              hipStream_t stream) {
   const uint32_t rows = tokens * cfg.heads;
-  dim3 grid(div_up(rows, kGroupsPerBlock * kRowsAhead));
-  if (head_major)
-    hipLaunchKernelGGL(k_prepare_qk<true>, grid, dim3(256), 0, stream, x, mean, codes, scales,
-                       tokens, cfg.row_stride, cfg.head_offset, cfg.heads, cfg.token_capacity,
-                       cfg.extra_scale, cfg.elem);
-  else
-    hipLaunchKernelGGL(k_prepare_qk<false>, grid, dim3(256), 0, stream, x, mean, codes, scales,
-                       tokens, cfg.row_stride, cfg.head_offset, cfg.heads, 0u, cfg.extra_scale,
-                       cfg.elem);
+  const dim3 grid(div_up(rows, kRopeGroups * kRowsAhead));
+  const uint32_t cap = head_major ? cfg.token_capacity : 0u;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, x, mean, codes, scales, tokens,
+                       cfg.row_stride, cfg.head_offset, cfg.heads, cap, cfg.extra_scale);
+  };
+  // every (layout, element, mean) combination as its own kernel
+  const int pick = (head_major ? 4 : 0) | (cfg.elem == H3_ELEM_BF16 ? 2 : 0) | (mean ? 1 : 0);
+  switch (pick) {
+    case 0: launch(k_prepare_qk<false, H3_ELEM_F16, false>); break;
+    case 1: launch(k_prepare_qk<false, H3_ELEM_F16, true>); break;
+    case 2: launch(k_prepare_qk<false, H3_ELEM_BF16, false>); break;
+    case 3: launch(k_prepare_qk<false, H3_ELEM_BF16, true>); break;
+    case 4: launch(k_prepare_qk<true, H3_ELEM_F16, false>); break;
+    case 5: launch(k_prepare_qk<true, H3_ELEM_F16, true>); break;
+    case 6: launch(k_prepare_qk<true, H3_ELEM_BF16, false>); break;
+    default: launch(k_prepare_qk<true, H3_ELEM_BF16, true>); break;
+  }
   return hipGetLastError();
 }
 
