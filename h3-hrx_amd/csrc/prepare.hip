@@ -1,11 +1,13 @@
 // Operand preparation for INT8 attention on gfx950: Hadamard-rotated per-(token, head) INT8
 // quantisation, the fused RMSNorm + RoPE variant, the f16 RoPE kernel, K column means and the
-// V transposes. All of these are HBM-bound byte work. In the quantizers each (token, head) row of
-// 128 channels is held by a 16-lane group (a DPP row; eight channels per lane, one 16-byte load
-// per lane), a 256-thread workgroup holds sixteen rows at a time and every global access is a
-// whole 256-byte row; several rows per group are loaded before any is processed, to keep enough
-// bytes in flight. The f16 RoPE kernel and the column means use 32-lane halves (four channels
-// per lane) with the same arithmetic.
+// V transposes: byte work at HBM rates, the quantizers bounded by their vector issue (each row
+// takes a norm, a 128-point Hadamard butterfly and a quantisation). In the quantizers each
+// (token, head) row of 128 channels is held by an 8-lane group (sixteen channels per lane, two
+// 16-byte loads per lane), a 256-thread workgroup holds 32 rows at a time and every global
+// access covers whole 256-byte rows; several rows per group are loaded before any is processed,
+// to keep enough bytes in flight. The row-norm pass of the fused K smoothing uses 16-lane groups
+// (eight channels per lane), the f16 RoPE kernel and the column means 32-lane halves (four
+// channels per lane), all with the same arithmetic.
 //
 // The arithmetic is built with -ffp-contract=off: every float operation below is one IEEE
 // operation in the order written, which is what makes the quantizer bit-exact with the
@@ -19,7 +21,7 @@ namespace h3 {
 namespace {
 
 constexpr int kRowsPerBlock = 8;  // 256 threads = 8 half-waves = 8 (token, head) rows
-// Rows per 16-lane group in the quantizers: their loads are issued together before any row is
+// Rows per 8-lane group in the quantizers: their loads are issued together before any row is
 // processed, so each group keeps kRowsAhead 256-byte rows in flight (one row is far too few
 // bytes in flight to cover HBM latency at these kernels' occupancy).
 constexpr int kRowsAhead = 4;
@@ -59,18 +61,25 @@ __device__ __forceinline__ float half_sum(float v) {
 }
 
 // ---------------------------------------------------------------- 16-lane row groups
-// The quantizers hold one 128-channel row in a 16-lane group (a DPP row), eight channels per
-// lane, read with one 16-byte load per lane. Partner exchanges k = 1, 2, 4, 8 are the DPP moves
-// of xor_partner, which stay inside a DPP row.
+// The row-norm pass of the fused K smoothing holds one 128-channel row in a 16-lane group (a DPP
+// row), eight channels per lane, read with one 16-byte load per lane. Partner exchanges k = 1, 2,
+// 4, 8 are the DPP moves of xor_partner, which stay inside a DPP row.
 __device__ __forceinline__ float row16_sum(float v) {  // order k = 1, 2, 4, 8
 #pragma unroll
   for (int k = 1; k < 16; k <<= 1) v = v + xor_partner(v, k);
   return v;
 }
-__device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int k = 8; k >= 1; k >>= 1) v = fmaxf(v, xor_partner(v, k));
-  return v;
+
+// r = 1/sqrt(mean(v^2) + eps) of the row held by a 16-lane group, eight channels per lane: the
+// 32-lane layout's operations in its order (the lane partial is that layout's first butterfly
+// sum, k = 1, 2, 4, 8 here are its k = 2, 4, 8, 16).
+__device__ __forceinline__ float rms_inverse8(const float (&v)[8], float eps) {
+  const float p0 = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
+  const float p1 = ((v[4] * v[4] + v[5] * v[5]) + v[6] * v[6]) + v[7] * v[7];
+  const float part = row16_sum(p0 + p1);
+  const float ms = part * 0.0078125f;
+  const float me = ms + eps;
+  return 1.0f / __builtin_sqrtf(me);
 }
 
 // Eight 16-bit activations (f16 or bf16 bit patterns) widened to f32 exactly.
@@ -81,83 +90,6 @@ __device__ __forceinline__ void widen8(uint4 b, int elem, float (&v)[8]) {
     v[j] = lo[j];
     v[4 + j] = hi[j];
   }
-}
-
-// The unnormalised Sylvester Hadamard H_128, lane l of a 16-lane group holding elements
-// 8l..8l+7, in the reference's fp32 order (kernels/prepare_qk_i8.loom:84-156). The reference
-// holds four elements per lane: an in-lane stage over element bits 0-1, then lane butterflies
-// over lane bits 1, 2, 4, 8, 16 (element bits 2-6), where the element with the bit clear keeps
-// s + partner and the one with the bit set keeps partner - s. Here element bit 2 lies inside
-// the lane and the same two sums are formed there; element bits 3-6 are lane bits 1, 2, 4, 8.
-// Every result is one correctly rounded addition or subtraction of the same two operands as in
-// the reference, so the bits are the reference's.
-__device__ __forceinline__ void hadamard128(float (&s)[8], int l) {
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const float ab_p = s[4 * g] + s[4 * g + 1], ab_m = s[4 * g] - s[4 * g + 1];
-    const float cd_p = s[4 * g + 2] + s[4 * g + 3], cd_m = s[4 * g + 2] - s[4 * g + 3];
-    s[4 * g] = ab_p + cd_p;
-    s[4 * g + 1] = ab_m + cd_m;
-    s[4 * g + 2] = ab_p - cd_p;
-    s[4 * g + 3] = ab_m - cd_m;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {  // element bit 2: s + partner (bit clear), partner - s (set)
-    const float p = s[j] + s[j + 4], m = s[j] - s[j + 4];
-    s[j] = p;
-    s[j + 4] = m;
-  }
-#pragma unroll
-  for (int k = 1; k < 16; k <<= 1) {  // element bits 3-6; fma(s, -1, p) is p - s exactly
-    const float sign = (l & k) ? -1.0f : 1.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s[j] = __builtin_fmaf(s[j], sign, xor_partner(s[j], k));
-  }
-}
-
-// Quantise one rotated row (kernels/prepare_qk_i8.loom:157-188): amax over the group,
-// sc = amax/127, inv = 127/amax (correctly rounded divisions), codes = clamp(rne(r*inv), +-127)
-// packed low byte first. Returns this lane's two words (elements 8l..8l+3, 8l+4..8l+7); *scale
-// gets amax/127 * extra.
-__device__ __forceinline__ uint2 quantize_row(const float (&r)[8], float extra, float* scale) {
-  float m = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(r[j]));
-  m = row16_max(m);
-  const float amax = fmaxf(m, 1.0000000000000001e-30f);
-  const float sc = amax / 127.0f;
-  const float inv = 127.0f / amax;
-  uint32_t w[2] = {0u, 0u};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float q = __builtin_rintf(r[j] * inv);
-    q = fminf(fmaxf(q, -127.0f), 127.0f);
-    w[j / 4] |= ((uint32_t)(int)q & 0xffu) << (8 * (j % 4));
-  }
-  *scale = sc * extra;
-  return make_uint2(w[0], w[1]);
-}
-
-// The int4 form (kernels/prepare_qk_i4.loom:174-214): amax/7 scales, codes clamp(rne(r*7/amax),
-// +-7) as nibbles; returns this lane's eight codes as one word (low nibble first).
-__device__ __forceinline__ uint32_t quantize_row_i4(const float (&r)[8], float extra,
-                                                    float* scale) {
-  float m = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(r[j]));
-  m = row16_max(m);
-  const float amax = fmaxf(m, 1.0000000000000001e-30f);
-  const float sc = amax / 7.0f;
-  const float inv = 7.0f / amax;
-  uint32_t bits = 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float q = __builtin_rintf(r[j] * inv);
-    q = fminf(fmaxf(q, -7.0f), 7.0f);
-    bits |= ((uint32_t)(int)q & 0xfu) << (4 * j);
-  }
-  *scale = sc * extra;
-  return bits;
 }
 
 __device__ __forceinline__ uint2 load4(const void* base, size_t elem_index) {
@@ -252,115 +184,12 @@ __device__ __forceinline__ v4f rmsnorm_rope_f16(v4f v, int lane, const float* we
   return rmsnorm_rope_f16(v, lane, rope_lane(lane, weight, cos_row, sin_row), eps);
 }
 
-// The same RMSNorm + RoPE for a row held eight channels per lane by a 16-lane group (the
-// quantizers' layout), bit for bit: the lane partial is the sum of the two four-channel partials
-// of the layout above (that layout's first butterfly step, k = 1, adds exactly those two), then
-// butterflies k = 1, 2, 4, 8 here are its k = 2, 4, 8, 16; the rotation partner is lane l +- 6.
-struct RopeLane8 {
-  float w[8], c[8], s[8];
-};
-
-__device__ __forceinline__ RopeLane8 rope_lane8(int l, const float* weight, const float* cos_row,
-                                                const float* sin_row) {
-  const int pairlane = l < 6 ? l : (l < 12 ? l - 6 : 0);
-  RopeLane8 t;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float4 w = *reinterpret_cast<const float4*>(weight + 8 * l + 4 * h);
-    const float4 c = *reinterpret_cast<const float4*>(cos_row + 8 * pairlane + 4 * h);
-    const float4 sn = *reinterpret_cast<const float4*>(sin_row + 8 * pairlane + 4 * h);
-    t.w[4 * h] = w.x; t.w[4 * h + 1] = w.y; t.w[4 * h + 2] = w.z; t.w[4 * h + 3] = w.w;
-    t.c[4 * h] = c.x; t.c[4 * h + 1] = c.y; t.c[4 * h + 2] = c.z; t.c[4 * h + 3] = c.w;
-    t.s[4 * h] = sn.x; t.s[4 * h + 1] = sn.y; t.s[4 * h + 2] = sn.z; t.s[4 * h + 3] = sn.w;
-  }
-  return t;
-}
-
-// r = 1/sqrt(mean(v^2) + eps) of the row held by a 16-lane group, eight channels per lane:
-// rms_inverse's operations in its order (the lane partial is that layout's first butterfly sum).
-__device__ __forceinline__ float rms_inverse8(const float (&v)[8], float eps) {
-  const float p0 = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
-  const float p1 = ((v[4] * v[4] + v[5] * v[5]) + v[6] * v[6]) + v[7] * v[7];
-  const float part = row16_sum(p0 + p1);
-  const float ms = part * 0.0078125f;
-  const float me = ms + eps;
-  return 1.0f / __builtin_sqrtf(me);
-}
-
-__device__ __forceinline__ void rmsnorm_rope_f16(float (&v)[8], int l, const RopeLane8& tab,
-                                                 float eps) {
-  const float r = rms_inverse8(v, eps);
-  float xn[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) xn[j] = (v[j] * r) * tab.w[j];
-  const bool lo = l < 6, pair = l < 12;
-  const int partner = lo ? l + 6 : (pair ? l - 6 : l);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float px = __shfl(xn[j], partner, 16);
-    const float a = xn[j] * tab.c[j];
-    const float b = px * tab.s[j];
-    float o = lo ? (a - b) : (a + b);
-    o = pair ? o : xn[j];
-    v[j] = f16_round(o);
-  }
-}
-
 // ---------------------------------------------------------------- quantizer kernels
 
-constexpr int kGroupsPerBlock = 16;  // 256 threads = 16 row groups of 16 lanes
+constexpr int kGroupsPerBlock = 16;  // the row-norm pass: 256 threads = 16 groups of 16 lanes
 
 __device__ __forceinline__ uint4 load8(const void* base, size_t elem_index) {
   return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + elem_index);
-}
-
-__device__ __forceinline__ void subtract_mean(float (&y)[8], const float* mean, uint32_t col) {
-  if (!mean) return;
-  const float4 a = *reinterpret_cast<const float4*>(mean + col);
-  const float4 b = *reinterpret_cast<const float4*>(mean + col + 4);
-  y[0] = y[0] - a.x;
-  y[1] = y[1] - a.y;
-  y[2] = y[2] - a.z;
-  y[3] = y[3] - a.w;
-  y[4] = y[4] - b.x;
-  y[5] = y[5] - b.y;
-  y[6] = y[6] - b.z;
-  y[7] = y[7] - b.w;
-}
-
-// int4 operands, token-major (kernels/prepare_qk_i4.loom): the same rotation; a lane's eight
-// codes are one word of the row (codes [tokens][heads*16] i32).
-__global__ __launch_bounds__(256) void k_prepare_qk_i4(const void* __restrict__ x,
-                                                       const float* __restrict__ mean,
-                                                       int32_t* __restrict__ codes,
-                                                       float* __restrict__ scales,
-                                                       uint32_t tokens, uint32_t row_stride,
-                                                       uint32_t head_offset, uint32_t heads,
-                                                       float extra, uint32_t elem) {
-  const uint32_t first = blockIdx.x * kGroupsPerBlock * kRowsAhead + (threadIdx.x >> 4);
-  const int l = threadIdx.x & 15;
-  const uint32_t total = tokens * heads;
-  uint4 in[kRowsAhead];
-#pragma unroll
-  for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kGroupsPerBlock * i;
-    if (row >= total) break;
-    const uint32_t t = row / heads, h = row % heads;
-    in[i] = load8(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
-  }
-#pragma unroll
-  for (int i = 0; i < kRowsAhead; ++i) {
-    const uint32_t row = first + kGroupsPerBlock * i;
-    if (row >= total) break;
-    const uint32_t h = row % heads;
-    float y[8];
-    widen8(in[i], elem, y);
-    subtract_mean(y, mean, head_offset + 128u * h + 8u * l);
-    hadamard128(y, l);
-    float scale;
-    codes[(size_t)row * 16 + l] = (int32_t)quantize_row_i4(y, extra, &scale);
-    if (l == 0) scales[row] = scale;
-  }
 }
 
 // ---------------------------------------------------------------- 8-lane row groups
@@ -509,11 +338,34 @@ __device__ __forceinline__ uint4 quantize_row16(const float (&r)[16], float extr
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// (token, head) rows (kernels/prepare_qk_i8.loom, prepare_qk_i8hm.loom), one per 8-lane group;
-// group g of block b takes rows b*32*kRowsAhead + 32i + g, i < kRowsAhead, all loads issued
-// before the first row is processed. Head-major rows walk tokens fastest (contiguous code
+// The int4 form (kernels/prepare_qk_i4.loom:174-214) for sixteen elements per lane: amax/7
+// scales, codes clamp(rne(r*7/amax), +-7) formed as quantize_row16 forms its bytes; returns the
+// lane's two words of nibbles (elements 16l..16l+7 and 16l+8..16l+15, low nibble first).
+__device__ __forceinline__ uint2 quantize_row16_i4(const float (&r)[16], float extra,
+                                                   float* scale) {
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(r[j]));
+  m = row8_max(m);
+  const float amax = fmaxf(m, 1.0000000000000001e-30f);
+  const float sc = amax / 7.0f;
+  const float inv = 7.0f / amax;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float q = fminf(fmaxf(r[j] * inv, -7.0f), 7.0f);
+    w[j / 8] |= (__float_as_uint(q + 12582912.0f) & 0xfu) << (4 * (j % 8));
+  }
+  *scale = sc * extra;
+  return make_uint2(w[0], w[1]);
+}
+
+// (token, head) rows (kernels/prepare_qk_i8.loom, prepare_qk_i8hm.loom; with kI4 the token-major
+// int4 operands of kernels/prepare_qk_i4.loom, codes [tokens][heads*16] i32), one per 8-lane
+// group; group g of block b takes rows b*32*kRowsAhead + 32i + g, i < kRowsAhead, all loads
+// issued before the first row is processed. Head-major rows walk tokens fastest (contiguous code
 // stores), token-major rows walk heads.
-template <bool kHeadMajor, int kElem, bool kMean>
+template <bool kHeadMajor, int kElem, bool kMean, bool kI4 = false>
 __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
                                                     const float* __restrict__ mean,
                                                     int32_t* __restrict__ codes,
@@ -567,9 +419,12 @@ __global__ __launch_bounds__(256) void k_prepare_qk(const void* __restrict__ x,
     }
     hadamard128_16(y, l);
     float scale;
-    const uint4 w = quantize_row16(y, extra, &scale);
     const size_t out_row = kHeadMajor ? (size_t)h * capacity + t : (size_t)t * heads + h;
-    reinterpret_cast<uint4*>(codes + out_row * 32)[l] = w;
+    if constexpr (kI4) {
+      reinterpret_cast<uint2*>(codes + out_row * 16)[l] = quantize_row16_i4(y, extra, &scale);
+    } else {
+      reinterpret_cast<uint4*>(codes + out_row * 32)[l] = quantize_row16(y, extra, &scale);
+    }
     if (l == 0) scales[out_row] = scale;
   }
 }
@@ -1015,9 +870,18 @@ hipError_t launch_prepare_qk_i4(const h3_prepare_cfg& cfg, uint32_t tokens, cons
                                 const float* mean, int32_t* codes, float* scales,
                                 hipStream_t stream) {
   const uint32_t rows = tokens * cfg.heads;
-  hipLaunchKernelGGL(k_prepare_qk_i4, dim3(div_up(rows, kGroupsPerBlock * kRowsAhead)), dim3(256),
-                     0, stream, x, mean, codes, scales, tokens, cfg.row_stride, cfg.head_offset,
-                     cfg.heads, cfg.extra_scale, cfg.elem);
+  const dim3 grid(div_up(rows, kRopeGroups * kRowsAhead));
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, x, mean, codes, scales, tokens,
+                       cfg.row_stride, cfg.head_offset, cfg.heads, 0u, cfg.extra_scale);
+  };
+  const int pick = (cfg.elem == H3_ELEM_BF16 ? 2 : 0) | (mean ? 1 : 0);
+  switch (pick) {
+    case 0: launch(k_prepare_qk<false, H3_ELEM_F16, false, true>); break;
+    case 1: launch(k_prepare_qk<false, H3_ELEM_F16, true, true>); break;
+    case 2: launch(k_prepare_qk<false, H3_ELEM_BF16, false, true>); break;
+    default: launch(k_prepare_qk<false, H3_ELEM_BF16, true, true>); break;
+  }
   return hipGetLastError();
 }
 
