@@ -1581,6 +1581,11 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
                        dim3(256), 0, stream, ks, ks_hm, a.tokens, a.kv_head_limit);
     a.ks = ks_hm;
   }
+  // INT8 token-major operands run on the head-major kernel, which reads the token-major rows and
+  // scales through its row strides (eight waves share every staged K/V^T tile there).
+  if (mode == kTokenI8)
+    return launch_attention_hm_tm(cfg, token_count, heads, qi, qs, ki, a.ks, hm_scales, vt, out,
+                                  stream);
   // Head-major: one launch. Token-major: one launch per eight generations of resident
   // workgroups (two per CU), so the workgroups of a launch start together and stay closer in
   // the key stream, whose K rows and scales they share in L2 with fewer heads' neighbours
@@ -1605,11 +1610,6 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
         hipLaunchKernelGGL((k_attention<kTokenI4Skip, true>), grid, dim3(kThreads), 0, stream, a);
       else
         hipLaunchKernelGGL(k_attention<kTokenI4Skip>, grid, dim3(kThreads), 0, stream, a);
-    } else {
-      if (hm_scales)
-        hipLaunchKernelGGL((k_attention<kTokenI8, true>), grid, dim3(kThreads), 0, stream, a);
-      else
-        hipLaunchKernelGGL(k_attention<kTokenI8>, grid, dim3(kThreads), 0, stream, a);
     }
   }
   return hipGetLastError();

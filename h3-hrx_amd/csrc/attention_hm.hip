@@ -146,6 +146,14 @@ struct Geometry {
   uint32_t q_capacity;
   uint32_t kv_group;
   uint32_t waves_per_head;
+  // token-major operands (kTm; attention_i8qk_family's layouts): codes [token][stride] int8, key
+  // scales at ks[key * ks_key + kv_head * ks_head] ([token][kv_heads] f32, or the lent head-major
+  // copy [kv_head][tokens]), query scales at qs[query * qs_row + head]
+  uint32_t k_row;    // bytes from one key's row of K to the next (kv_stride)
+  uint32_t q_row;    // bytes from one query's row of Q to the next (q_stride)
+  uint32_t ks_key;
+  uint32_t ks_head;
+  uint32_t qs_row;   // q_stride / 128
 };
 
 // Per-lane constants of the staging loads (the wave's share of each tile).
@@ -158,7 +166,9 @@ struct Stager {
 };
 
 // LDS byte o of a K or V^T stage holds row o/128, logical 16-byte chunk ((o/16)%8) ^ ((row/2)%8);
-// K row m holds key swap23(m).
+// K row m holds key swap23(m). With token-major operands (kTm) a key's 128 bytes are one piece of
+// its token's row, k_row bytes after the previous key's.
+template <bool kTm = false>
 __device__ __forceinline__ Stager make_stager(const Geometry& g, int wave, int lane) {
   Stager s;
   s.wave = wave;
@@ -166,7 +176,7 @@ __device__ __forceinline__ Stager make_stager(const Geometry& g, int wave, int l
   for (int t = 0; t < kKLoads; ++t) {
     const uint32_t o = (wave * kKLoads + t) * 1024 + 16 * lane;
     const uint32_t row = o >> 7, chunk = ((o >> 4) & 7) ^ ((row >> 1) & 7);
-    s.koff[t] = swap23(row) * kRowBytes + 16 * chunk;
+    s.koff[t] = swap23(row) * (kTm ? g.k_row : kRowBytes) + 16 * chunk;
   }
 #pragma unroll
   for (int t = 0; t < kVLoads; ++t) {
@@ -187,19 +197,28 @@ struct StepLoads {
   char* kst;
   char* vst;
   float ks;
-  uint32_t keep;  // cross-attention: the key's mask byte (0 past the sequence)
+  uint32_t keep;    // cross-attention: the key's mask byte (0 past the sequence)
+  uint32_t sbytes;  // token-major operands: bytes from one key's scale to the next
 };
-template <bool kCross>
+template <bool kCross, bool kTm = false>
 __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_head, uint32_t kk0,
                                                char* kst, uint32_t vk0, char* vst, uint32_t sk0) {
   StepLoads L;
   const uint32_t live = g.tokens > kk0 ? min(g.tokens - kk0, (uint32_t)kKeys) : 0u;
   const uint32_t slive = g.tokens > sk0 ? min(g.tokens - sk0, (uint32_t)kKeys) : 0u;
-  L.rs = rsrc(g.ks + (size_t)kv_head * g.capacity + sk0, slive * 4);
+  if (kTm) {  // the descriptors end at the last valid key's scale and row
+    L.rs = rsrc(g.ks + (size_t)sk0 * g.ks_key + (size_t)kv_head * g.ks_head,
+                slive ? ((slive - 1) * g.ks_key + 1) * 4 : 0u);
+    L.rk = rsrc(reinterpret_cast<const char*>(g.ki) + (size_t)kk0 * g.k_row + kv_head * 128,
+                live ? (live - 1) * g.k_row + 128 : 0u);
+  } else {
+    L.rs = rsrc(g.ks + (size_t)kv_head * g.capacity + sk0, slive * 4);
+    L.rk = rsrc(reinterpret_cast<const char*>(g.ki) + ((size_t)kv_head * g.capacity + kk0) * 128,
+                live * 128);
+  }
   if (kCross) L.rm = rsrc(g.key_mask + sk0, slive);
   L.keep = 0;
-  L.rk = rsrc(reinterpret_cast<const char*>(g.ki) + ((size_t)kv_head * g.capacity + kk0) * 128,
-              live * 128);
+  L.sbytes = kTm ? g.ks_key * 4 : 4u;
   // V^T: columns past `tokens` inside the head's block are zero or belong to the next channel
   // row, and meet probability 0
   const uint32_t blk = 128 * g.capacity;
@@ -213,10 +232,11 @@ __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_he
 // Load `slot` of a step: 0 the key scale (into a register; with cross-attention also the key's
 // mask byte), then the K tile's LDS-DMA loads, then the V^T tile's. The scale is of the stage
 // after the step's K tile, so that it has two steps to land before it is stored.
-template <bool kCross>
+template <bool kCross, bool kTm = false>
 __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int slot) {
   if (slot == 0) {
-    L.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(L.rs, sg.skey * 4, 0, 0));
+    L.ks = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(L.rs, sg.skey * (kTm ? L.sbytes : 4u), 0, 0));
     if (kCross) L.keep = __builtin_amdgcn_raw_buffer_load_b8(L.rm, sg.skey, 0, 0);
   } else if (slot <= kKLoads) {
     const int t = slot - 1;
@@ -228,15 +248,15 @@ __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int s
         L.rv, (lds_void*)(L.vst + (sg.wave * kVLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
   }
 }
-template <bool kCross>
+template <bool kCross, bool kTm = false>
 __device__ __forceinline__ void issue_k(StepLoads& L, const Stager& sg) {
 #pragma unroll
-  for (int s = 0; s <= kKLoads; ++s) issue_load<kCross>(L, sg, s);
+  for (int s = 0; s <= kKLoads; ++s) issue_load<kCross, kTm>(L, sg, s);
 }
-template <bool kCross>
+template <bool kCross, bool kTm = false>
 __device__ __forceinline__ void issue_v(StepLoads& L, const Stager& sg) {
 #pragma unroll
-  for (int s = kKLoads + 1; s < kLoadsPerStep; ++s) issue_load<kCross>(L, sg, s);
+  for (int s = kKLoads + 1; s < kLoadsPerStep; ++s) issue_load<kCross, kTm>(L, sg, s);
 }
 
 // Scales of K tile k0 at their MFMA rows: ks, and c = -1.5*2^23*ks for a key inside the
@@ -822,10 +842,11 @@ __device__ __forceinline__ char* ring(int i, char* a0, char* a1, char* a2, char*
   return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : a3;
 }
 
-template <bool kCross, bool kChain, bool kFp6 = false>
+template <bool kCross, bool kChain, bool kFp6 = false, bool kTm = false>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2), amdgpu_num_vgpr(kPReg)))
 void k_attention_hm(Geometry g) {
+  static_assert(!kTm || (!kCross && !kFp6), "token-major operands: INT8 self-attention only");
   // Four-stage rings, each stage its own array so that the compiler can tell an LDS-DMA into one
   // stage from the reads of another.
   __shared__ __attribute__((aligned(16))) char k0s[kKStage], k1s[kKStage], k2s[kKStage], k3s[kKStage];
@@ -849,7 +870,7 @@ void k_attention_hm(Geometry g) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
-  const Stager sg = make_stager(g, wave, lane);
+  const Stager sg = make_stager<kTm>(g, wave, lane);
   const Lanes ln = make_lanes<kFp6>(n, half);
   // The QK bias 1.5*2^23, made opaque so that it stays in registers for the whole loop.
   v16i magic = {};  // the int8 form's accumulator bias (the FP6 form starts QK from zero)
@@ -893,7 +914,10 @@ void k_attention_hm(Geometry g) {
   auto load_q = [&](Tile& T, const WaveBlock& w) {
     const uint32_t qq = w.q0 + n;
     const uint32_t q_read = qq < q_limit ? qq : q_limit - 1;
-    const int32_t* src = g.qi + ((size_t)w.head * q_cap + q_read) * 32;
+    const int32_t* src =
+        kTm ? reinterpret_cast<const int32_t*>(reinterpret_cast<const char*>(g.qi) +
+                                               (size_t)q_read * g.q_row + w.head * 128)
+            : g.qi + ((size_t)w.head * q_cap + q_read) * 32;
     if constexpr (kFp6) {  // blocks 2x + half of the row: 24 bytes of codes each
       const char* b = reinterpret_cast<const char*>(src) + 32 * half;
 #pragma unroll
@@ -907,7 +931,8 @@ void k_attention_hm(Geometry g) {
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
     }
-    T.qsl = g.qs[(size_t)w.head * q_cap + q_read] * kLog2e;
+    T.qsl = (kTm ? g.qs[(size_t)q_read * g.qs_row + w.head] : g.qs[(size_t)w.head * q_cap + q_read]) *
+            kLog2e;
     T.cq = kFp6 ? 0.0f : -(kMagic * T.qsl);
   };
 
@@ -932,17 +957,17 @@ void k_attention_hm(Geometry g) {
 
   // ---- prologue: K and scales of stages 0..2, V^T of stages 0 and 1 and the scales of stage 3
   // in flight (unless chained)
-  StepLoads L0 = plan_step<kCross>(g, kv_head, 0, k0s, 0, v0s, 0);
-  StepLoads L1 = plan_step<kCross>(g, kv_head, kKeys, k1s, kKeys, v1s, kKeys);
-  StepLoads L2 = plan_step<kCross>(g, kv_head, 2 * kKeys, k2s, 0, nullptr, 2 * kKeys);
-  StepLoads L3 = plan_step<kCross>(g, kv_head, 0, nullptr, 0, nullptr, stage_of(3) * kKeys);
+  StepLoads L0 = plan_step<kCross, kTm>(g, kv_head, 0, k0s, 0, v0s, 0);
+  StepLoads L1 = plan_step<kCross, kTm>(g, kv_head, kKeys, k1s, kKeys, v1s, kKeys);
+  StepLoads L2 = plan_step<kCross, kTm>(g, kv_head, 2 * kKeys, k2s, 0, nullptr, 2 * kKeys);
+  StepLoads L3 = plan_step<kCross, kTm>(g, kv_head, 0, nullptr, 0, nullptr, stage_of(3) * kKeys);
   if (!chained) {
-    issue_k<kCross>(L0, sg);
-    issue_v<kCross>(L0, sg);
-    issue_k<kCross>(L1, sg);
-    issue_v<kCross>(L1, sg);
-    issue_k<kCross>(L2, sg);
-    issue_load<kCross>(L3, sg, 0);
+    issue_k<kCross, kTm>(L0, sg);
+    issue_v<kCross, kTm>(L0, sg);
+    issue_k<kCross, kTm>(L1, sg);
+    issue_v<kCross, kTm>(L1, sg);
+    issue_k<kCross, kTm>(L2, sg);
+    issue_load<kCross, kTm>(L3, sg, 0);
   } else {
     L2.ks = ks_carry[0];
     L2.keep = keep_carry[0];
@@ -966,10 +991,10 @@ void k_attention_hm(Geometry g) {
 
   // ---- step -1: QK of key tiles 0 and 1, the probabilities of tile 0; K(3), V(2) and the scales
   // of stage 4 in flight
-  StepLoads Lm = plan_step<kCross>(g, kv_head, stage_of(3) * kKeys, k3s, 2 * kKeys, v2s,
+  StepLoads Lm = plan_step<kCross, kTm>(g, kv_head, stage_of(3) * kKeys, k3s, 2 * kKeys, v2s,
                                    stage_of(4) * kKeys);
-  issue_k<kCross>(Lm, sg);
-  issue_v<kCross>(Lm, sg);
+  issue_k<kCross, kTm>(Lm, sg);
+  issue_v<kCross, kTm>(Lm, sg);
   Pre pre;
 #pragma unroll
   for (int part = 0; part < 4; ++part) prefetch<kFp6>(pre, part, k0s, 0, s0s, 0, ln);
@@ -1003,7 +1028,7 @@ void k_attention_hm(Geometry g) {
   uint32_t j = 0;
   auto steady = [&](auto J_) {
     constexpr int J = decltype(J_)::value;
-    StepLoads L = plan_step<kCross>(g, kv_head, stage_of(j + 4) * kKeys, kr(J),
+    StepLoads L = plan_step<kCross, kTm>(g, kv_head, stage_of(j + 4) * kKeys, kr(J),
                                     stage_of(j + 3) * kKeys, vr(J + 3), stage_of(j + 5) * kKeys);
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
     sub_step<0, true, true, true, kFp6, false, kCross, kPfK>(
@@ -1013,13 +1038,13 @@ void k_attention_hm(Geometry g) {
         store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_hold[J & 1], keep_hold[J & 1],
                                          stage_of(j + 3) * kKeys, g.tokens);
       if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep)
-        issue_load<kCross>(L, sg, c / kLoadGap);
+        issue_load<kCross, kTm>(L, sg, c / kLoadGap);
       if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
     });
     auto stage1 = [&](int c, Pre& next) {
       if (c == 0) prio_equal();
       const int slot = (c + 12) / kLoadGap;
-      if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross>(L, sg, slot);
+      if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross, kTm>(L, sg, slot);
       if (c == kBarK) step_barrier<kWaitTwoSteps<kCross>>();
       next_step_reads<kFp6, kBarK>(c, next, kr(J + 2), sr(J + 1), ln);
     };
@@ -1163,6 +1188,40 @@ hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count
     hipLaunchKernelGGL((k_attention_hm<false, true>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
   else
     hipLaunchKernelGGL((k_attention_hm<false, false>), dim3(g.wpx * 8), dim3(kThreads), 0, stream, g);
+  return hipGetLastError();
+}
+
+// attention_i8qk_family's token-major operands on this kernel: Q and K codes [token][stride],
+// query scales [token][q_stride / 128], key scales [token][kv_stride / 128] or, when
+// `ks_head_major`, the lent head-major copy [kv_head][tokens]; V^T and the output as above.
+hipError_t launch_attention_hm_tm(const h3_attention_cfg& cfg, uint32_t token_count,
+                                  uint32_t heads, const int32_t* qi, const float* qs,
+                                  const int32_t* ki, const float* ks, bool ks_head_major,
+                                  const uint16_t* vt, uint16_t* out, hipStream_t stream) {
+  Geometry g{};
+  g.qi = qi;
+  g.qs = qs;
+  g.ki = ki;
+  g.ks = ks;
+  g.vt = vt;
+  g.out = out;
+  g.tokens = cfg.tokens;
+  g.rows = std::min(token_count, cfg.tokens);
+  g.capacity = cfg.token_capacity;
+  g.out_stride = cfg.out_stride;
+  g.q_blocks = (token_count + kBlockQ - 1) / kBlockQ;
+  g.kv_head_limit = cfg.kv_stride / 128;
+  g.head_limit = cfg.out_stride / 128;
+  g.k_row = cfg.kv_stride;
+  g.q_row = cfg.q_stride;
+  g.qs_row = cfg.q_stride / 128;
+  g.ks_key = ks_head_major ? 1u : g.kv_head_limit;
+  g.ks_head = ks_head_major ? cfg.tokens : 1u;
+  g.total = g.q_blocks * heads;
+  g.per_xcd = (g.total + 7) / 8;
+  g.wpx = g.per_xcd;  // one workgroup per block at every length (the chained form would spill)
+  hipLaunchKernelGGL((k_attention_hm<false, false, false, true>), dim3(g.wpx * 8), dim3(kThreads),
+                     0, stream, g);
   return hipGetLastError();
 }
 

@@ -104,6 +104,13 @@ hipError_t launch_attention_hm(const h3_attention_cfg& cfg, uint32_t token_count
                                const int32_t* qi, const float* qs, const int32_t* ki,
                                const float* ks, const uint16_t* vt, uint16_t* out,
                                hipStream_t stream);
+// The same kernel on attention_i8qk_family's token-major operands: codes [token][stride], query
+// scales [token][q_stride/128], key scales [token][kv_stride/128] or (ks_head_major) the lent
+// head-major copy [kv_head][tokens].
+hipError_t launch_attention_hm_tm(const h3_attention_cfg& cfg, uint32_t token_count,
+                                  uint32_t heads, const int32_t* qi, const float* qs,
+                                  const int32_t* ki, const float* ks, bool ks_head_major,
+                                  const uint16_t* vt, uint16_t* out, hipStream_t stream);
 // The same kernel as cross-attention with a key mask and grouped heads; q_heads / kv_heads must
 // divide 8 (each workgroup holds all query heads of one key/value head).
 hipError_t launch_attention_hm_cross(const h3_cross_cfg& cfg, const int32_t* qi, const float* qs,
