@@ -108,8 +108,8 @@ def int4_path(torch, H, dev, tokens, heads, fused, vt, out):
                                                                vt, out, ws6), 2)
     fp6_finite = bool(torch.isfinite(out).all())
     del ws6
-    # the same token-major kernel on int8 codes (attention_i8qk, _ws form): what int4 costs over
-    # int8 in one kernel design
+    # the token-major INT8 entry on int8 codes of the same rows (attention_i8qk, _ws form; it runs
+    # on the head-major kernel with row strides, the int4 forms on the token-major kernel)
     del qi, ki
     qi8 = torch.zeros((cap, width // 4), dtype=torch.int32, device=dev)
     ki8 = torch.zeros_like(qi8)
