@@ -90,10 +90,19 @@ __device__ __forceinline__ void load_group(const void* x, size_t first, int elem
   }
 }
 
-__device__ __forceinline__ uint32_t code(float y, float inv_s) {
-  float q = rintf(y * inv_s);
-  q = fminf(fmaxf(q, -127.0f), 127.0f);
-  return (uint32_t)(int)q & 0xffu;
+// Four codes clamp(rne(y * inv_s), +-127) as one word, low byte first. Formed as
+// rne(clamp(y * inv_s, +-127)) (the same integer for every finite product; the caller only
+// quantises rows whose values are all finite) by adding 1.5 * 2^23: the sum is rounded to an
+// integer, ties to even, and the low byte of its bits is the code in two's complement.
+__device__ __forceinline__ uint32_t code_bits(float y, float inv_s) {
+  return __float_as_uint(fminf(fmaxf(y * inv_s, -127.0f), 127.0f) + 12582912.0f);
+}
+__device__ __forceinline__ uint32_t code4(const float* y, float inv_s) {
+  const uint32_t lo = __builtin_amdgcn_perm(code_bits(y[1], inv_s), code_bits(y[0], inv_s),
+                                            0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(code_bits(y[3], inv_s), code_bits(y[2], inv_s),
+                                            0x04000c0cu);
+  return lo | hi;
 }
 
 // Transform of the lane's 64 channels (the four radix-4 stages), the row's absmax (over the wave,
@@ -131,9 +140,7 @@ __device__ __forceinline__ void transform_store(float (&v)[kGroup], float* wave_
   uint32_t words[kGroup / 4];
   if (valid) {
 #pragma unroll
-    for (int i = 0; i < kGroup / 4; ++i)
-      words[i] = code(v[4 * i], inv_s) | code(v[4 * i + 1], inv_s) << 8 |
-                 code(v[4 * i + 2], inv_s) << 16 | code(v[4 * i + 3], inv_s) << 24;
+    for (int i = 0; i < kGroup / 4; ++i) words[i] = code4(v + 4 * i, inv_s);
   } else {
 #pragma unroll
     for (int i = 0; i < kGroup / 4; ++i) words[i] = 0;
