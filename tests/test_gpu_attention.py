@@ -181,9 +181,8 @@ def test_row_sum_error_is_bounded_on_long_flat_rows_with_large_values(dev, flat,
     accumulation and the f16 output rounding. Long rows (BASELINE config 3's 129,024 keys) with
     |V| up to ~1,500 and either exactly flat scores (every p = 1, out = mean of V) or nearly
     flat ones (every p a distinct value near 1, each rounded) check that bound at scale.
-    The token-major kernel adds a tile's 16 probabilities per lane in a packed f16 tree before the
-    f32 row sum, which adds at most ~2^-9 relative to l (four levels of f16 additions of values
-    <= 2^12), so its bound is 2^-10 + 2^-9 of max|V|."""
+    Both layouts run the head-major kernel (the token-major one through its row strides), so
+    both take the same bound."""
     import torch
 
     heads, tokens = 2, 129024
@@ -221,8 +220,57 @@ def test_row_sum_error_is_bounded_on_long_flat_rows_with_large_values(dev, flat,
         mean_v = vt[:, :tokens].view(np.float16).astype(np.float64).mean(1).reshape(heads, 128)
         assert np.allclose(want, mean_v[None], rtol=0, atol=1e-9 * vmax)
     err = np.abs(got[rows] - want)
-    rel = 2.0 ** -10 + (2.0 ** -12 if head_major else 2.0 ** -9)
+    rel = 2.0 ** -10 + 2.0 ** -12
     bound = rel * vmax + 2.0 ** -11 * np.abs(want)
     assert np.all(err <= bound), (flat, float(err.max()), vmax)
     assert float(err.mean()) <= 5e-5 * vmax, (flat, float(err.mean()), vmax)
     assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("tokens,q_heads,kv_heads,pad", [(1025, 3, 3, 0), (4096, 4, 2, 128),
+                                                         (4097, 2, 2, 0), (9000, 2, 1, 128)])
+def test_token_major_layout_gives_the_head_major_bits(dev, tokens, q_heads, kv_heads, pad):
+    """h3_attention_i8qk runs the head-major kernel with row strides (K and Q rows kv_stride and
+    q_stride bytes apart, key scales [token][kv heads], query scales [token][q_stride/128]): on
+    the same operands laid out both ways, its output equals h3_attention_i8qkhm's bit for bit.
+    Short and long sequences (the head-major entry chains blocks up to 4,096 keys, the
+    token-major one never does), GQA head wrap (kv_stride < q_stride) and a padded output pitch
+    whose pad columns stay untouched; sampled rows against the f64 oracle at 1e-3 + 2e-3 rel."""
+    import torch
+
+    cap = O.capacity(tokens)
+    rng = np.random.default_rng(tokens + 17 * q_heads)
+    qc, qs, _, _, _ = head_major_operands(rng, q_heads, tokens, cap, late_match=False)
+    _, _, kc, ks, vt = head_major_operands(rng, kv_heads, tokens, cap, late_match=False)
+    kc[:, tokens - 1] = qc[:kv_heads, 31]  # a strong match in the last key tile
+    q_stride, kv_stride, out_stride = q_heads * 128, kv_heads * 128, q_heads * 128 + pad
+    cfg = H.AttentionCfg(q_stride, kv_stride, out_stride, tokens, cap, 1.0)
+    hm = [to_dev(pack_codes(qc).reshape(q_heads * cap, 32), dev), to_dev(qs, dev),
+          to_dev(pack_codes(kc).reshape(kv_heads * cap, 32), dev), to_dev(ks, dev)]
+    tm = [to_dev(pack_codes(qc.transpose(1, 0, 2)).reshape(cap, q_heads * 32), dev),
+          to_dev(qs.T.copy(), dev),
+          to_dev(pack_codes(kc.transpose(1, 0, 2)).reshape(cap, kv_heads * 32), dev),
+          to_dev(ks.T.copy(), dev)]
+    vt_d = to_dev(vt, dev)
+    nbytes = tokens * out_stride * 2
+    outs = []
+    print(f"token-major vs head-major: S={tokens} heads={q_heads}/{kv_heads} pad={pad}", flush=True)
+    for fn, ops in ((H.attention_i8qkhm, hm), (H.attention_i8qk, tm)):
+        out = filled((nbytes,), 0xA5, np.uint8, dev)
+        fn(cfg, tokens, q_heads, *ops, vt_d, out)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1]), "token-major and head-major outputs differ"
+    # the reference's head wrap: workload row h reads key/value head h mod kv and query and
+    # output head h mod min(kv, out_stride/128), so only the first kv output heads are written
+    touched = min(kv_heads, out_stride // 128)
+    rows_out = outs[1].view(np.uint16).reshape(tokens, out_stride)
+    assert (rows_out[:, touched * 128:] == 0xA5A5).all(), "untouched heads or pad columns written"
+    got = rows_out[:, :touched * 128].reshape(tokens, touched, 128)
+    rows = np.unique(np.concatenate([[0, 31, 255, 256, tokens - 1],
+                                     rng.integers(0, tokens, 5)])).astype(np.int32)
+    want = O.attention_f64(qc[:touched], qs[:touched], kc[:touched], ks[:touched],
+                           vt.reshape(kv_heads, 128, cap)[:touched].reshape(touched * 128, cap),
+                           tokens, cap, touched, rows)
+    err = np.abs(got[rows].view(np.float16).astype(np.float64) - want)
+    assert np.all(err <= 1e-3 + 2e-3 * np.abs(want)), float(err.max())
