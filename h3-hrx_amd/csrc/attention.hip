@@ -1,4 +1,7 @@
-// INT8-QK flash attention for gfx950 (CDNA4).
+// INT8-QK flash attention for gfx950 (CDNA4): the kernel of the INT4 token-major family (codes
+// widened to int8 in registers), its skip twin, the VSA attention and the cross-attention groups
+// that do not divide eight. The INT8 entries, head-major and token-major, run on the eight-wave
+// kernel of attention_hm.hip.
 //
 // One workgroup = 4 wave64s x 32 queries of one head; keys stream through 64-key LDS tiles;
 // two workgroups share a CU (two waves per SIMD). Per wave and key tile:
@@ -1574,7 +1577,7 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
   a.kv_head_limit = cfg.kv_stride / 128;
   a.head_limit = cfg.out_stride / 128;
   a.q_scale_pitch = cfg.q_stride / 128;
-  const bool hm_scales = workspace && mode != kHeadI8;
+  const bool hm_scales = workspace != nullptr;
   if (hm_scales) {  // token-major codes, head-major copy of the key scales
     float* ks_hm = static_cast<float*>(workspace);
     hipLaunchKernelGGL(k_scales_head_major, dim3((a.tokens + 63) / 64, (a.kv_head_limit + 63) / 64),
@@ -1586,21 +1589,18 @@ hipError_t launch_attention(const h3_attention_cfg& cfg, int mode, float skip_ta
   if (mode == kTokenI8)
     return launch_attention_hm_tm(cfg, token_count, heads, qi, qs, ki, a.ks, hm_scales, vt, out,
                                   stream);
-  // Head-major: one launch. Token-major: one launch per eight generations of resident
-  // workgroups (two per CU), so the workgroups of a launch start together and stay closer in
-  // the key stream, whose K rows and scales they share in L2 with fewer heads' neighbours
-  // (measured at C3: -5.5 % int4, -6.8 % int8 token-major, -2.7 % int4 with head-major scales;
-  // +0.4-1.5 % for head-major, which stays one launch).
+  // One launch per eight generations of resident workgroups (two per CU), so the workgroups of
+  // a launch start together and stay closer in the key stream, whose K rows and scales they
+  // share in L2 with fewer heads' neighbours (measured at C3: -5.5 % int4, -2.7 % int4 with
+  // head-major scales).
   const uint32_t items = a.q_blocks * heads;
-  const uint32_t gen = mode == kHeadI8 ? items : std::max(1u, 16u * device_cus());
+  const uint32_t gen = std::max(1u, 16u * device_cus());
   for (uint32_t base = 0; base < items; base += gen) {
     a.base = base;
     a.total = std::min(gen, items - base);
     a.per_xcd = (a.total + 7) / 8;
     const dim3 grid(a.per_xcd * 8);
-    if (mode == kHeadI8) {
-      hipLaunchKernelGGL(k_attention<kHeadI8>, grid, dim3(kThreads), 0, stream, a);
-    } else if (mode == kTokenI4) {
+    if (mode == kTokenI4) {
       if (hm_scales)
         hipLaunchKernelGGL((k_attention<kTokenI4, true>), grid, dim3(kThreads), 0, stream, a);
       else
