@@ -333,3 +333,80 @@ def test_transpose_bf16_rounds_to_f16(dev):
     H.transpose_f16(H.TransposeCfg(width, cap, H.H3_ELEM_BF16), cap, tokens, to_dev(bits, dev), out)
     torch.cuda.synchronize()
     assert np.array_equal(from_dev(out).reshape(width, cap), want)
+
+
+@pytest.mark.parametrize("elem", [H.H3_ELEM_F16, H.H3_ELEM_BF16])
+def test_quantizers_on_non_finite_and_extreme_rows(dev, elem):
+    """Rows holding NaN, +inf, -inf, the format's largest finite values, subnormals or zeros
+    through every quantizer kernel (prepare_qk_i8, _i8hm, _i4, prepare_qk_rope_i8hm, with and
+    without a mean), bit for bit against the oracle's fp32 restatement. The kernels form the
+    code clamp(rne(p), +-127) as rne(clamp(p, +-127)) with a rounding add; for a NaN product
+    both give -127 (the clamp's max returns the number), which these rows exercise."""
+    import torch
+
+    tokens, heads = 67, 3
+    width = heads * 128
+    stride = 3 * width
+    fmt = O.F16 if elem == H.H3_ELEM_F16 else O.BF16
+    big = 65504.0 if elem == H.H3_ELEM_F16 else 3.0e38
+    rng = np.random.default_rng(21 + elem)
+    f = rng.standard_normal((tokens, stride)).astype(np.float32)
+    f[1, 5] = np.nan
+    f[2, 130] = np.inf
+    f[3, 300] = -np.inf
+    f[4, :] = big
+    f[5, 0:128] = -big
+    f[6, :] = 0.0
+    f[7, 128:256] = 1e-7  # subnormal in f16, tiny in bf16
+    f[8, 7] = np.nan
+    f[8, 9] = np.inf
+    f[9, 256:384] = np.nan
+    f[10, 128:256:2] = big
+    x = O.f16_bits(f) if fmt == O.F16 else O.bf16_bits(f)
+    x_d = to_dev(x, dev)
+    mean = O.values(stride, 0.3)
+    m_d = to_dev(mean, dev)
+    cap = 96
+    print(f"non-finite quantizer rows, elem={elem}", flush=True)
+    for offset, m, m_host in ((0, None, None), (width, m_d, mean)):
+        cfg = H.PrepareCfg(stride, offset, heads, EXTRA, cap, 1e-5, elem)
+        want_hw, want_hs = O.prepare_qk(x, fmt, m_host, tokens, stride, offset, heads, EXTRA, True,
+                                        cap)
+        want_tw, want_ts = O.prepare_qk(x, fmt, m_host, tokens, stride, offset, heads, EXTRA)
+        want_iw, want_is = O.prepare_qk_i4(x, fmt, m_host, tokens, stride, offset, heads, EXTRA)
+        codes = filled((cap * width,), 0x55, np.uint8, dev)
+        scales = filled((cap * heads * 4,), 0x55, np.uint8, dev)
+        H.prepare_qk_i8hm(cfg, tokens, x_d, m, codes, scales)
+        tcodes = torch.zeros(tokens * heads * 32, dtype=torch.int32, device=dev)
+        tscales = torch.zeros(tokens * heads, dtype=torch.float32, device=dev)
+        H.prepare_qk_i8(cfg, tokens, x_d, m, tcodes, tscales)
+        icodes = torch.zeros(tokens * heads * 16, dtype=torch.int32, device=dev)
+        iscales = torch.zeros(tokens * heads, dtype=torch.float32, device=dev)
+        H.prepare_qk_i4(cfg, tokens, x_d, m, icodes, iscales)
+        torch.cuda.synchronize()
+        hw = codes.cpu().numpy().view(np.int32).reshape(heads, cap, 32)[:, :tokens]
+        hs = scales.cpu().numpy().view(np.uint32).reshape(heads, cap)[:, :tokens]
+        assert np.array_equal(hw, want_hw.reshape(heads, cap, 32)[:, :tokens]), offset
+        assert np.array_equal(hs, want_hs.view(np.uint32)[:, :tokens]), offset
+        assert np.array_equal(tcodes.cpu().numpy(), want_tw.reshape(-1)), offset
+        assert np.array_equal(tscales.cpu().numpy().view(np.uint32), want_ts.view(np.uint32).reshape(-1))
+        assert np.array_equal(icodes.cpu().numpy(), want_iw.reshape(-1)), offset
+        assert np.array_equal(iscales.cpu().numpy().view(np.uint32), want_is.view(np.uint32).reshape(-1))
+    # the RoPE quantizer: RMSNorm + RoPE of the same rows (their non-finite values spread over
+    # the row through the norm), then the quantizer
+    w = (1.0 + O.values(128, 0.1)).astype(np.float32)
+    angles = O.values(tokens * 48, 3.0)
+    cos_t, sin_t = np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
+    for offset in (0, width):
+        cfg = H.PrepareCfg(stride, offset, heads, EXTRA, cap, 1e-5, elem)
+        roped = O.rope_qknorm_f16(x, fmt, tokens, stride, offset, heads, w, cos_t, sin_t, 1e-5)
+        want_w, want_s = O.prepare_qk(roped, O.F16, None, tokens, width, 0, heads, EXTRA, True, cap)
+        codes = filled((cap * width,), 0x55, np.uint8, dev)
+        scales = filled((cap * heads * 4,), 0x55, np.uint8, dev)
+        H.prepare_qk_rope_i8hm(cfg, tokens, x_d, to_dev(w, dev), to_dev(cos_t, dev),
+                               to_dev(sin_t, dev), codes, scales)
+        torch.cuda.synchronize()
+        got_w = codes.cpu().numpy().view(np.int32).reshape(heads, cap, 32)[:, :tokens]
+        got_s = scales.cpu().numpy().view(np.uint32).reshape(heads, cap)[:, :tokens]
+        assert np.array_equal(got_w, want_w.reshape(heads, cap, 32)[:, :tokens]), offset
+        assert np.array_equal(got_s, want_s.view(np.uint32)[:, :tokens]), offset
