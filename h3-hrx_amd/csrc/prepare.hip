@@ -191,6 +191,13 @@ constexpr int kGroupsPerBlock = 16;  // the row-norm pass: 256 threads = 16 grou
 __device__ __forceinline__ uint4 load8(const void* base, size_t elem_index) {
   return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + elem_index);
 }
+// The same load marked non-temporal: for inputs a kernel reads exactly once, so that they do not
+// push out of the caches what the neighbouring kernels will read again.
+__device__ __forceinline__ uint4 load8_nt(const void* base, size_t elem_index) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                                       reinterpret_cast<const uint16_t*>(base) + elem_index)));
+}
 
 // ---------------------------------------------------------------- 8-lane row groups
 // The RoPE quantizer holds one 128-channel row in an 8-lane group, sixteen channels per lane
@@ -595,7 +602,7 @@ __global__ __launch_bounds__(256) void k_rope_rms(const void* __restrict__ x,
 #pragma unroll
     for (int i = 0; i < kRmsTokens; ++i) {
       const uint32_t t = min(t0 + i, tokens - 1);  // every lane stays in the butterfly
-      raw[i] = load8(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
+      raw[i] = load8_nt(x, (size_t)t * row_stride + head_offset + 128u * h + 8u * l);
     }
     float mine = 0.0f;
 #pragma unroll
