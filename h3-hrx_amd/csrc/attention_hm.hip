@@ -69,6 +69,7 @@ constexpr int kRowBytes = 128;
 constexpr int kKStage = kKeys * kRowBytes;        // 8192: int8 codes of 64 keys
 constexpr int kVStage = 128 * kRowBytes;          // 16384: 128 channels x 64 keys of f16
 constexpr int kSStage = 2 * kKeys * 4;            // 512: ks[64], c[64] at MFMA-row index
+constexpr int kTabStages = 64;  // key tiles of a chained sequence (kPersistMaxStages)
 constexpr int kKLoads = kKStage / 1024 / kWaves;  // 1 KiB LDS-DMA loads per wave per tile: 1
 constexpr int kVLoads = kVStage / 1024 / kWaves;  // 2
 constexpr int kSRows = kKeys / kWaves;            // scale rows stored per wave: 8
@@ -80,10 +81,13 @@ constexpr int kLoadGap = 6;                       // chunks between a step's sta
 // cross-attention also the key's mask byte (a second load in the scale's slot).
 template <bool kCross>
 constexpr int kVmemPerStep = kLoadsPerStep + (kCross ? 1 : 0);
-template <bool kCross>
-constexpr int kWaitPrevStep = kVmemPerStep<kCross> | (7 << 4) | (0 << 8);
-template <bool kCross>
-constexpr int kWaitTwoSteps = (2 * kVmemPerStep<kCross>) | (7 << 4) | (0 << 8);
+// With the scales resident in LDS (kTab: chained cross-attention) a step loads no scale or mask.
+template <bool kCross, bool kTab = false>
+constexpr int kVmemStep = kTab ? kLoadsPerStep - 1 : kVmemPerStep<kCross>;
+template <bool kCross, bool kTab = false>
+constexpr int kWaitPrevStep = kVmemStep<kCross, kTab> | (7 << 4) | (0 << 8);
+template <bool kCross, bool kTab = false>
+constexpr int kWaitTwoSteps = (2 * kVmemStep<kCross, kTab>) | (7 << 4) | (0 << 8);
 constexpr int kWaitAll = 0 | (7 << 4) | (0 << 8);
 // LDS work only: vmcnt at its maximum (63: low bits 3:0 and high bits 15:14), lgkmcnt 0.
 constexpr int kWaitLds = 0xF | (7 << 4) | (0 << 8) | (3 << 14);
@@ -232,9 +236,10 @@ __device__ __forceinline__ StepLoads plan_step(const Geometry& g, uint32_t kv_he
 // Load `slot` of a step: 0 the key scale (into a register; with cross-attention also the key's
 // mask byte), then the K tile's LDS-DMA loads, then the V^T tile's. The scale is of the stage
 // after the step's K tile, so that it has two steps to land before it is stored.
-template <bool kCross, bool kTm = false>
+template <bool kCross, bool kTm = false, bool kTab = false>
 __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int slot) {
   if (slot == 0) {
+    if (kTab) return;  // the scales and mask bytes are resident in LDS
     L.ks = __builtin_bit_cast(
         float, __builtin_amdgcn_raw_buffer_load_b32(L.rs, sg.skey * (kTm ? L.sbytes : 4u), 0, 0));
     if (kCross) L.keep = __builtin_amdgcn_raw_buffer_load_b8(L.rm, sg.skey, 0, 0);
@@ -248,10 +253,10 @@ __device__ __forceinline__ void issue_load(StepLoads& L, const Stager& sg, int s
         L.rv, (lds_void*)(L.vst + (sg.wave * kVLoads + t) * 1024), 16, sg.voff[t], 0, 0, 0);
   }
 }
-template <bool kCross, bool kTm = false>
+template <bool kCross, bool kTm = false, bool kTab = false>
 __device__ __forceinline__ void issue_k(StepLoads& L, const Stager& sg) {
 #pragma unroll
-  for (int s = 0; s <= kKLoads; ++s) issue_load<kCross, kTm>(L, sg, s);
+  for (int s = 0; s <= kKLoads; ++s) issue_load<kCross, kTm, kTab>(L, sg, s);
 }
 template <bool kCross, bool kTm = false>
 __device__ __forceinline__ void issue_v(StepLoads& L, const Stager& sg) {
@@ -855,6 +860,15 @@ void k_attention_hm(Geometry g) {
   auto kr = [&](int i) { return ring(i & 3, k0s, k1s, k2s, k3s); };
   auto vr = [&](int i) { return ring(i & 3, v0s, v1s, v2s, v3s); };
   auto sr = [&](int i) { return ring(i & 3, s0s, s1s, s2s, s3s); };
+  // Chained cross-attention keeps the scale pairs (ks, c) of all its key tiles in LDS for as long
+  // as its workgroup stays on one key/value head: the text keys are few (at most
+  // kPersistMaxStages tiles here) and every block of the head walks the same ones, so the steps
+  // load no scale or mask byte and store nothing, and no wait of theirs lands behind the previous
+  // block's output stores. Stage `st`'s pairs sit at stab + st * kSStage in the ring layout.
+  constexpr bool kTab = kCross && kChain;
+  __shared__ __attribute__((aligned(16))) char stab[kTab ? kTabStages * kSStage : 16];
+  // the scale stage of stage `st`, ring slot i
+  auto ss = [&](int i, uint32_t st) -> char* { return kTab ? stab + st * kSStage : sr(i); };
   constexpr int kPfK = kPf<kChain, kFp6>;
   constexpr int kBarK = kBarrierChunk<kChain, kFp6>;
 
@@ -942,6 +956,7 @@ void k_attention_hm(Geometry g) {
   // chains into it.
   float ks_carry[2] = {0.0f, 0.0f};
   uint32_t keep_carry[2] = {0u, 0u};
+  uint32_t tab_head = ~0u;  // the key/value head whose scale pairs fill stab
   Tile T;
 
   for (;;) {
@@ -961,13 +976,27 @@ void k_attention_hm(Geometry g) {
   StepLoads L1 = plan_step<kCross, kTm>(g, kv_head, kKeys, k1s, kKeys, v1s, kKeys);
   StepLoads L2 = plan_step<kCross, kTm>(g, kv_head, 2 * kKeys, k2s, 0, nullptr, 2 * kKeys);
   StepLoads L3 = plan_step<kCross, kTm>(g, kv_head, 0, nullptr, 0, nullptr, stage_of(3) * kKeys);
+  if (kTab && kv_head != tab_head) {
+    // Every wave is past the previous block's last barrier, after which nothing reads stab; the
+    // prologue's barrier below publishes the new pairs.
+    for (uint32_t k = threadIdx.x; k < n_stages * kKeys; k += kThreads) {
+      const uint32_t m = swap23(k % kKeys);  // the MFMA row of key k % kKeys
+      const bool in = k < g.tokens;
+      const float ks = in ? g.ks[(size_t)kv_head * g.capacity + k] : 0.0f;
+      const bool live = in && g.key_mask[k] != 0;
+      float* sc = reinterpret_cast<float*>(stab + (k / kKeys) * kSStage);
+      sc[rot(m, 1)] = ks;
+      sc[kKeys + rot(m, 2)] = live ? -(kMagic * ks) : -INFINITY;
+    }
+    tab_head = kv_head;
+  }
   if (!chained) {
-    issue_k<kCross, kTm>(L0, sg);
+    issue_k<kCross, kTm, kTab>(L0, sg);
     issue_v<kCross, kTm>(L0, sg);
-    issue_k<kCross, kTm>(L1, sg);
+    issue_k<kCross, kTm, kTab>(L1, sg);
     issue_v<kCross, kTm>(L1, sg);
-    issue_k<kCross, kTm>(L2, sg);
-    issue_load<kCross, kTm>(L3, sg, 0);
+    issue_k<kCross, kTm, kTab>(L2, sg);
+    issue_load<kCross, kTm, kTab>(L3, sg, 0);
   } else {
     L2.ks = ks_carry[0];
     L2.keep = keep_carry[0];
@@ -980,8 +1009,10 @@ void k_attention_hm(Geometry g) {
   T.l = 0.0f;
   zero_all(std::make_integer_sequence<int, 64>{});
   if (!chained) {
-    store_stage_scales<kCross, kFp6>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
-    store_stage_scales<kCross, kFp6>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
+    if (!kTab) {
+      store_stage_scales<kCross, kFp6>(s0s, sg, L0.ks, L0.keep, 0, g.tokens);
+      store_stage_scales<kCross, kFp6>(s1s, sg, L1.ks, L1.keep, kKeys, g.tokens);
+    }
     step_barrier<kWaitAll>();
   } else {
     // The first stages landed before the previous block's last barrier; the previous block's
@@ -993,24 +1024,25 @@ void k_attention_hm(Geometry g) {
   // of stage 4 in flight
   StepLoads Lm = plan_step<kCross, kTm>(g, kv_head, stage_of(3) * kKeys, k3s, 2 * kKeys, v2s,
                                    stage_of(4) * kKeys);
-  issue_k<kCross, kTm>(Lm, sg);
+  issue_k<kCross, kTm, kTab>(Lm, sg);
   issue_v<kCross, kTm>(Lm, sg);
   Pre pre;
 #pragma unroll
-  for (int part = 0; part < 4; ++part) prefetch<kFp6>(pre, part, k0s, 0, s0s, 0, ln);
+  for (int part = 0; part < 4; ++part) prefetch<kFp6>(pre, part, k0s, 0, ss(0, 0), 0, ln);
   sub_step<0, true, false, false, kFp6>(nullptr, nullptr, 0, T, ln, half, magic, pre,
                                   [&](int c, Pre& next) {
-    if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, k0s, 1, s0s, 0, ln);
+    if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, k0s, 1, ss(0, 0), 0, ln);
   });
   // The first tile's own path pays where blocks are short (cross-attention's few key tiles);
   // self-attention keeps the general path, whose code measured marginally faster at long
   // sequences. The results are the same bits either way. Tile 0 is the last one of a sequence of
   // at most 32 keys, so it takes the masked path.
-  sub_step<1, true, false, true, kFp6, kCross, true>(nullptr, s0s, 0, T, ln, half, magic, pre,
+  sub_step<1, true, false, true, kFp6, kCross, true>(nullptr, ss(0, 0), 0, T, ln, half, magic, pre,
                                                       [&](int c, Pre& next) {
-    if (c == 0) store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
-    if (c == kBarK) step_barrier<kWaitPrevStep<kCross>>();
-    next_step_reads<kFp6, kBarK>(c, next, k1s, s0s, ln);
+    if (!kTab && c == 0)
+      store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
+    if (c == kBarK) step_barrier<kWaitPrevStep<kCross, kTab>>();
+    next_step_reads<kFp6, kBarK>(c, next, k1s, ss(0, 0), ln);
   });
   // Key scales (and mask bytes) in registers until their store: those loaded in step j (stage
   // j+5) wait in hold[j % 2] for step j+2; the prologue's (stage 3) count as step -2's.
@@ -1032,27 +1064,28 @@ void k_attention_hm(Geometry g) {
                                     stage_of(j + 3) * kKeys, vr(J + 3), stage_of(j + 5) * kKeys);
     // one staging load every kLoadGap chunks: the scale first, then K and V^T
     sub_step<0, true, true, true, kFp6, false, kCross, kPfK>(
-        vr(J), sr(J), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
+        vr(J), ss(J, j), 1, T, ln, half, magic, pre, [&](int c, Pre& next) {
       if (c == 0) prio_late_waves_first(wave);
-      if (c == 0)
+      if (!kTab && c == 0)
         store_stage_scales<kCross, kFp6>(sr(J + 3), sg, ks_hold[J & 1], keep_hold[J & 1],
                                          stage_of(j + 3) * kKeys, g.tokens);
       if (c % kLoadGap == 0 && c / kLoadGap < kLoadsPerStep)
-        issue_load<kCross, kTm>(L, sg, c / kLoadGap);
-      if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, kr(J + 1), 1, sr(J + 1), 0, ln);
+        issue_load<kCross, kTm, kTab>(L, sg, c / kLoadGap);
+      if (c >= 4 && c < 10) prefetch<kFp6>(next, c - 4, kr(J + 1), 1, ss(J + 1, j + 1), 0, ln);
     });
     auto stage1 = [&](int c, Pre& next) {
       if (c == 0) prio_equal();
       const int slot = (c + 12) / kLoadGap;
-      if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep) issue_load<kCross, kTm>(L, sg, slot);
-      if (c == kBarK) step_barrier<kWaitTwoSteps<kCross>>();
-      next_step_reads<kFp6, kBarK>(c, next, kr(J + 2), sr(J + 1), ln);
+      if ((c + 12) % kLoadGap == 0 && slot < kLoadsPerStep)
+        issue_load<kCross, kTm, kTab>(L, sg, slot);
+      if (c == kBarK) step_barrier<kWaitTwoSteps<kCross, kTab>>();
+      next_step_reads<kFp6, kBarK>(c, next, kr(J + 2), ss(J + 1, j + 1), ln);
     };
     // Tile 2j+2 (keys 64(j+1) ..) holds keys past the sequence in the last steady step when the
     // sequence ends inside its 32 keys: this sub-step always takes the masked path. (A branch
     // between the two paths here puts register copies at its join that the inline-assembly
     // MFMAs after it may read before they land, which the compiler does not guard against.)
-    sub_step<1, true, true, true, kFp6, false, true, kPfK>(vr(J), sr(J + 1), 0, T, ln, half,
+    sub_step<1, true, true, true, kFp6, false, true, kPfK>(vr(J), ss(J + 1, j + 1), 0, T, ln, half,
                                                            magic, pre, stage1);
     ks_hold[J & 1] = L.ks;
     keep_hold[J & 1] = L.keep;
@@ -1073,7 +1106,7 @@ void k_attention_hm(Geometry g) {
   // ---- last step (j = n_stages - 1): PV of tiles 2j and 2j+1, the probabilities of 2j+1 between
   // (its scales came in `pre`; its K reads there are unused). Tile 2j+1 may hold keys past the
   // sequence: the masked path.
-  sub_step<0, false, true, true, kFp6, false, true, kPfK>(vr(j), sr(j), 1, T, ln, half, magic,
+  sub_step<0, false, true, true, kFp6, false, true, kPfK>(vr(j), ss(j, j), 1, T, ln, half, magic,
                                                           pre, [](int, Pre&) {});
   sub_step<1, false, true, false, kFp6, false, false, kPfK>(vr(j), nullptr, 0, T, ln, half,
                                                             magic, pre, [](int, Pre&) {});
@@ -1152,7 +1185,7 @@ void k_attention_hm(Geometry g) {
 // hands blocks to whichever CU is free. At 129,024 keys the chaining build was 5-6 % slower, from
 // a static split of the blocks over CUs that run at different speeds and from the extra
 // per-step work of the stage wrap.
-constexpr uint32_t kPersistMaxStages = 64;
+constexpr uint32_t kPersistMaxStages = kTabStages;
 bool chain_blocks(const Geometry& g) {
   return (g.tokens + kKeys - 1) / kKeys <= kPersistMaxStages;
 }
