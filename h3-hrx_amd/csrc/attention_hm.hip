@@ -925,7 +925,8 @@ void k_attention_hm(Geometry g) {
   const uint32_t q_limit = kCross ? g.q_tokens : g.tokens;  // readable query rows
   const uint32_t q_cap = kCross ? g.q_capacity : g.capacity;
   // The Q^T operand and scale of this lane's query in block `w`.
-  auto load_q = [&](Tile& T, const WaveBlock& w) {
+  // The Q^T operand of this lane's query in block `w`; returns the query's scale.
+  auto load_q_codes = [&](Tile& T, const WaveBlock& w) -> float {
     const uint32_t qq = w.q0 + n;
     const uint32_t q_read = qq < q_limit ? qq : q_limit - 1;
     const int32_t* src =
@@ -945,10 +946,13 @@ void k_attention_hm(Geometry g) {
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) T.q[dc] = *reinterpret_cast<const v4i*>(src + 8 * dc + 4 * half);
     }
-    T.qsl = (kTm ? g.qs[(size_t)q_read * g.qs_row + w.head] : g.qs[(size_t)w.head * q_cap + q_read]) *
-            kLog2e;
+    return kTm ? g.qs[(size_t)q_read * g.qs_row + w.head] : g.qs[(size_t)w.head * q_cap + q_read];
+  };
+  auto set_q_scale = [&](Tile& T, float qs) {
+    T.qsl = qs * kLog2e;
     T.cq = kFp6 ? 0.0f : -(kMagic * T.qsl);
   };
+  auto load_q = [&](Tile& T, const WaveBlock& w) { set_q_scale(T, load_q_codes(T, w)); };
 
   bool chained = false;  // this block's first stages were staged by the previous block
   bool have_q = false;   // this block's Q was loaded by the previous block
@@ -958,6 +962,13 @@ void k_attention_hm(Geometry g) {
   uint32_t keep_carry[2] = {0u, 0u};
   uint32_t tab_head = ~0u;  // the key/value head whose scale pairs fill stab
   Tile T;
+  if constexpr (kTab) {
+    // Every block's Q is loaded before the last barrier of the block before it (the first
+    // block's here, waited for at once), so no wait for Q stands in step -1, where it would also
+    // wait for the previous block's output stores (vmcnt counts both, in order).
+    load_q(T, wave_block(xcd * g.per_xcd + local));
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+  }
 
   for (;;) {
   const uint32_t logical = xcd * g.per_xcd + local;
@@ -1004,7 +1015,7 @@ void k_attention_hm(Geometry g) {
     L3.keep = keep_carry[1];
   }
 
-  if (!have_q) load_q(T, wb);
+  if (!kTab && !have_q) load_q(T, wb);
   T.negm = 1.0e30f;
   T.l = 0.0f;
   zero_all(std::make_integer_sequence<int, 64>{});
@@ -1041,7 +1052,9 @@ void k_attention_hm(Geometry g) {
                                                       [&](int c, Pre& next) {
     if (!kTab && c == 0)
       store_stage_scales<kCross, kFp6>(s2s, sg, L2.ks, L2.keep, 2 * kKeys, g.tokens);
-    if (c == kBarK) step_barrier<kWaitPrevStep<kCross, kTab>>();
+    // with the scales resident, every staging load older than step -1's has landed (the
+    // prologue's barrier, or the previous block's last one, waited for them all): LDS work only
+    if (c == kBarK) step_barrier<kTab ? kWaitLds : kWaitPrevStep<kCross, kTab>>();
     next_step_reads<kFp6, kBarK>(c, next, k1s, ss(0, 0), ln);
   });
   // Key scales (and mask bytes) in registers until their store: those loaded in step j (stage
@@ -1105,7 +1118,10 @@ void k_attention_hm(Geometry g) {
 
   // ---- last step (j = n_stages - 1): PV of tiles 2j and 2j+1, the probabilities of 2j+1 between
   // (its scales came in `pre`; its K reads there are unused). Tile 2j+1 may hold keys past the
-  // sequence: the masked path.
+  // sequence: the masked path. With the scales resident, the next block's Q codes are loaded
+  // first (no QK is left in this block), so that this step's last barrier covers them.
+  float qs_next = 0.0f;
+  if (kTab && has_next) qs_next = load_q_codes(T, wave_block(xcd * g.per_xcd + next_local));
   sub_step<0, false, true, true, kFp6, false, true, kPfK>(vr(j), ss(j, j), 1, T, ln, half, magic,
                                                           pre, [](int, Pre&) {});
   sub_step<1, false, true, false, kFp6, false, false, kPfK>(vr(j), nullptr, 0, T, ln, half,
@@ -1116,7 +1132,8 @@ void k_attention_hm(Geometry g) {
   // The next block's Q, loaded now (this block's QK is done) so that it lands during the
   // epilogue and ahead of the stores below.
   const float l_here = T.l;
-  if (has_next) load_q(T, wave_block(xcd * g.per_xcd + next_local));
+  if (kTab && has_next) set_q_scale(T, qs_next);
+  if (!kTab && has_next) load_q(T, wave_block(xcd * g.per_xcd + next_local));
 
   // ---- normalise and store rows < min(token_count, tokens). O^T gives each lane one query and
   // 8-byte pieces of its channels, so the rows are first transposed through the wave's LDS stage
