@@ -393,6 +393,26 @@ int vsa_attention_i8_ws(const h3_attention_cfg* cfg, uint32_t token_count, uint3
   return attention_common("VSA attention", cfg, token_count, heads, qi, qs, ki, ks, vt, out,
                           stream, kModeTokenI8Vsa, 0.0f, routes, lengths, workspace);
 }
+
+int vsa_gather_pool(const h3_vsa_cfg* cfg, h3_view src, h3_view lengths, h3_view x, h3_view y,
+                    h3_view means, h3_stream stream) {
+  const char* stage = "VSA gather";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t n = cfg->padded, t = cfg->tokens, w = cfg->width, b = cfg->blocks;
+  h3_view views[5] = {src, x, y, lengths, means};
+  size_t need[5] = {n * 4, t * w * 2, n * w * 2, b * 4, b * w * 4};
+  if ((st = check_bindings(stage, views, need, 5))) return st;
+  if ((st = check_aligned16(stage, {x, y, means}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_vsa_gather_pool(cfg->tokens, cfg->blocks, cfg->width,
+                                                static_cast<const int32_t*>(src.ptr),
+                                                static_cast<const int32_t*>(lengths.ptr),
+                                                static_cast<const uint16_t*>(x.ptr),
+                                                static_cast<uint16_t*>(y.ptr),
+                                                static_cast<float*>(means.ptr),
+                                                reinterpret_cast<hipStream_t>(stream)));
+}
 }  // namespace h3
 
 using namespace h3;

@@ -157,6 +157,14 @@ hipError_t launch_vsa_scatter(uint32_t tokens, uint32_t padded, uint32_t width,
                               hipStream_t stream);
 hipError_t launch_vsa_pool(uint32_t blocks, uint32_t width, const int32_t* lengths,
                            const uint16_t* x, float* means, hipStream_t stream);
+// launch_vsa_gather then launch_vsa_pool on its output, in one kernel (padded = 64 * blocks).
+hipError_t launch_vsa_gather_pool(uint32_t tokens, uint32_t blocks, uint32_t width,
+                                  const int32_t* src, const int32_t* lengths, const uint16_t* x,
+                                  uint16_t* y, float* means, hipStream_t stream);
+// h3_vsa_gather(cfg, src, x, y) then h3_vsa_pool(cfg, lengths, y, means), with the checks of
+// both, in one kernel (abi.cpp).
+int vsa_gather_pool(const h3_vsa_cfg* cfg, h3_view src, h3_view lengths, h3_view x, h3_view y,
+                    h3_view means, h3_stream stream);
 hipError_t launch_vsa_scores(uint32_t blocks, uint32_t heads, const float* qm, const float* km,
                              float* scores, hipStream_t stream);
 hipError_t launch_vsa_route(uint32_t blocks, uint32_t heads, uint32_t prefix, uint32_t topk,

@@ -86,6 +86,46 @@ __global__ __launch_bounds__(kThreads) void k_vsa_pool(const int32_t* __restrict
   out[1] = make_float4(acc[4] / lf, acc[5] / lf, acc[6] / lf, acc[7] / lf);
 }
 
+// h3_vsa_gather, then h3_vsa_pool of the gathered rows, in one pass (the runtime's q and k): a
+// thread owns eight consecutive channels of one cube, copies the cube's 64 rows (a zero row
+// where src[i] >= tokens) and sums the first `len` of the values it wrote, in row order. The
+// rows and the means are those of the two kernels run one after the other, bit for bit, and the
+// gathered rows are not read back.
+__global__ __launch_bounds__(kThreads) void k_vsa_gather_pool(const int32_t* __restrict__ src,
+                                                              const int32_t* __restrict__ lengths,
+                                                              const uint4* __restrict__ x,
+                                                              uint4* __restrict__ y,
+                                                              float4* __restrict__ means,
+                                                              uint32_t tokens, uint32_t chunks) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t c = blockIdx.y * kThreads + threadIdx.x;
+  if (c >= chunks) return;
+  const int len_raw = lengths[b];
+  const int len = len_raw < 0 ? 0 : len_raw > 64 ? 64 : len_raw;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int32_t* sb = src + (size_t)64 * b;
+  uint4* yb = y + (size_t)64 * b * chunks + c;
+#pragma unroll 8
+  for (int j = 0; j < 64; ++j) {
+    const uint32_t s = (uint32_t)sb[j];
+    const uint4 v = s < tokens ? x[(size_t)s * chunks + c] : zero4();
+    yb[(size_t)j * chunks] = v;
+    if (j < len) {
+      const v4f lo = widen4(make_uint2(v.x, v.y), H3_ELEM_F16);
+      const v4f hi = widen4(make_uint2(v.z, v.w), H3_ELEM_F16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i] = acc[i] + lo[i];
+        acc[4 + i] = acc[4 + i] + hi[i];
+      }
+    }
+  }
+  const float lf = (float)len;
+  float4* out = means + ((size_t)b * chunks + c) * 2;
+  out[0] = make_float4(acc[0] / lf, acc[1] / lf, acc[2] / lf, acc[3] / lf);
+  out[1] = make_float4(acc[4] / lf, acc[5] / lf, acc[6] / lf, acc[7] / lf);
+}
+
 // h3_vsa_scores: scores[h][q][j] = fma chain over d = 0..127 of qm[q][128h+d] * km[j][128h+d].
 // A workgroup computes a 64 x 64 tile of one head, a thread 4 x 4 outputs, with the channels
 // staged through LDS 32 at a time (transposed, so a thread reads 4 q or 4 j values per load).
@@ -382,6 +422,17 @@ hipError_t launch_vsa_pool(uint32_t blocks, uint32_t width, const int32_t* lengt
   hipLaunchKernelGGL(k_vsa_pool, dim3(blocks, (chunks + kThreads - 1) / kThreads), dim3(kThreads),
                      0, stream, lengths, reinterpret_cast<const uint4*>(x),
                      reinterpret_cast<float4*>(means), chunks);
+  return hipGetLastError();
+}
+
+hipError_t launch_vsa_gather_pool(uint32_t tokens, uint32_t blocks, uint32_t width,
+                                  const int32_t* src, const int32_t* lengths, const uint16_t* x,
+                                  uint16_t* y, float* means, hipStream_t stream) {
+  const uint32_t chunks = width / 8;
+  hipLaunchKernelGGL(k_vsa_gather_pool, dim3(blocks, (chunks + kThreads - 1) / kThreads),
+                     dim3(kThreads), 0, stream, src, lengths, reinterpret_cast<const uint4*>(x),
+                     reinterpret_cast<uint4*>(y), reinterpret_cast<float4*>(means), tokens,
+                     chunks);
   return hipGetLastError();
 }
 

@@ -301,15 +301,16 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
     return set_error(H3_ERR_ARGUMENT, "VSA: layer %u outside [0, %u)", layer, r->layers);
   const h3_vsa_cfg* c = &r->cfg;
   int st;
-  // src/vsa/device.rs:209-225: gather q, k, v into the cube layout
-  if ((st = h3_vsa_gather(c, r->src, q, r->q, stream)) ||
-      (st = h3_vsa_gather(c, r->src, k, r->k, stream)) ||
-      (st = h3_vsa_gather(c, r->src, v, r->v, stream)))
+  // src/vsa/device.rs:215-238: gather q, k, v into the cube layout, and the block means of q and
+  // k (and of v, which a gate reads, 388-398), each mean from the pass that writes its rows: the
+  // same rows and means as a gather followed by a pool, without reading the rows back
+  if ((st = vsa_gather_pool(c, r->src, r->lengths, q, r->q, r->qm, stream)) ||
+      (st = vsa_gather_pool(c, r->src, r->lengths, k, r->k, r->km, stream)) ||
+      (st = gate.ptr ? vsa_gather_pool(c, r->src, r->lengths, v, r->v, r->vm, stream)
+                     : h3_vsa_gather(c, r->src, v, r->v, stream)))
     return st;
-  // 226-263: block means, block scores, routes
-  if ((st = h3_vsa_pool(c, r->lengths, r->q, r->qm, stream)) ||
-      (st = h3_vsa_pool(c, r->lengths, r->k, r->km, stream)) ||
-      (st = h3_vsa_scores(c, r->qm, r->km, r->scores, stream)) ||
+  // 239-261: block scores, routes
+  if ((st = h3_vsa_scores(c, r->qm, r->km, r->scores, stream)) ||
       (st = h3_vsa_route(c, r->scores, r->routes, stream)))
     return st;
   if (r->bits == 16) {
@@ -331,10 +332,8 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
     if ((st = h3_vsa_kmean(c->width, c->blocks, r->km, mean, stream))) return st;
   }
   if (gate.ptr) {
-    // 372-434: value means, coarse attention, gated scatter
-    if ((st = h3_vsa_pool(c, r->lengths, r->v, r->vm, stream)) ||
-        (st = h3_vsa_coarse(c, r->scores, r->vm, r->coarse, stream)))
-      return st;
+    // 399-434: coarse attention over the value means, gated scatter
+    if ((st = h3_vsa_coarse(c, r->scores, r->vm, r->coarse, stream))) return st;
     return h3_vsa_gated_scatter(c, r->inverse, r->out, gate, r->coarse, out, stream);
   }
   // 435-445

@@ -381,9 +381,13 @@ def test_runtime_reproduces_the_reference_device_test(dev):
     b = vsa.buffers(0)
     gq = read(b.q, np.uint16, (n, w))
     assert np.array_equal(gq, O.vsa_gather(src, t, data[0]))
+    gk0 = read(b.k, np.uint16, (n, w))
+    assert np.array_equal(gk0, O.vsa_gather(src, t, data[1]))
+    assert np.array_equal(read(b.v, np.uint16, (n, w)), O.vsa_gather(src, t, data[2]))
     qm = read(b.qm, np.float32, (nb, w))
     km = read(b.km, np.float32, (nb, w))
     assert np.array_equal(qm.view(np.uint32), O.vsa_pool(lengths, gq).view(np.uint32))
+    assert np.array_equal(km.view(np.uint32), O.vsa_pool(lengths, gk0).view(np.uint32))
     scores = read(b.scores, np.float32, (heads, nb, nb))
     assert np.array_equal(scores.view(np.uint32), O.vsa_scores(qm, km, heads).view(np.uint32))
     routes = read(b.routes, np.int32, (heads, nb, nb))
