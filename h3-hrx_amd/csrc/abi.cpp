@@ -413,6 +413,26 @@ int vsa_gather_pool(const h3_vsa_cfg* cfg, h3_view src, h3_view lengths, h3_view
                                                 static_cast<float*>(means.ptr),
                                                 reinterpret_cast<hipStream_t>(stream)));
 }
+
+int vsa_gather_transpose(const h3_vsa_cfg* cfg, h3_view src, h3_view x, h3_view y, h3_view vt,
+                         h3_stream stream) {
+  const char* stage = "VSA gather";
+  int st = check_vsa_cfg(stage, cfg);
+  if (st) return st;
+  const size_t n = cfg->padded, t = cfg->tokens, w = cfg->width;
+  h3_view views[4] = {src, x, y, vt};
+  size_t need[4] = {n * 4, t * w * 2, n * w * 2, w * n * 2};
+  if ((st = check_bindings(stage, views, need, 4))) return st;
+  if ((st = check_aligned16(stage, {x, y}))) return st;
+  if ((st = device_ready(stage))) return st;
+  return launched(stage, launch_gather_transpose(cfg->width, cfg->padded,
+                                                 static_cast<const int32_t*>(src.ptr),
+                                                 cfg->tokens,
+                                                 static_cast<const uint16_t*>(x.ptr),
+                                                 static_cast<uint16_t*>(y.ptr),
+                                                 static_cast<uint16_t*>(vt.ptr),
+                                                 reinterpret_cast<hipStream_t>(stream)));
+}
 }  // namespace h3
 
 using namespace h3;

@@ -165,6 +165,15 @@ hipError_t launch_vsa_gather_pool(uint32_t tokens, uint32_t blocks, uint32_t wid
 // both, in one kernel (abi.cpp).
 int vsa_gather_pool(const h3_vsa_cfg* cfg, h3_view src, h3_view lengths, h3_view x, h3_view y,
                     h3_view means, h3_stream stream);
+// The VSA gather of f16 rows x -> gathered ([rows][width], rows a multiple of 64) and the V^T
+// transpose of the gathered rows -> out ([width][rows] f16) from one read of x (prepare.hip).
+hipError_t launch_gather_transpose(uint32_t width, uint32_t rows, const int32_t* src,
+                                   uint32_t src_rows, const uint16_t* x, uint16_t* gathered,
+                                   uint16_t* out, hipStream_t stream);
+// h3_vsa_gather(cfg, src, x, y) then h3_transpose_f16 of y into vt ([width][padded]), with the
+// checks of both, in one kernel (abi.cpp).
+int vsa_gather_transpose(const h3_vsa_cfg* cfg, h3_view src, h3_view x, h3_view y, h3_view vt,
+                         h3_stream stream);
 hipError_t launch_vsa_scores(uint32_t blocks, uint32_t heads, const float* qm, const float* km,
                              float* scores, hipStream_t stream);
 hipError_t launch_vsa_route(uint32_t blocks, uint32_t heads, uint32_t prefix, uint32_t topk,

@@ -793,11 +793,18 @@ __global__ __launch_bounds__(kColmeanThreads) void k_rope_colmean(
 // x [rows][row_stride] (width columns at col_offset) -> out [width][capacity] f16 through a
 // 64x64 LDS tile (rows padded to 66 halves). Output columns [rows, clear_to) are zeroed,
 // columns >= clear_to are left alone (kernels/transpose_f16.loom, transpose_qkv_v_f16.loom).
+// kGather: row r of the input is row src[r] of x (a zero row where src[r] >= src_rows), and each
+// loaded piece is also written, as loaded, to gathered[r][c] (the VSA runtime's gathered v,
+// [rows][width], and its V^T from one read of x).
+template <bool kGather>
 __global__ __launch_bounds__(256) void k_transpose(const uint16_t* __restrict__ x,
                                                    uint16_t* __restrict__ out, uint32_t rows,
                                                    uint32_t clear_to, uint32_t width,
                                                    uint32_t capacity, uint32_t row_stride,
-                                                   uint32_t col_offset, uint32_t elem) {
+                                                   uint32_t col_offset, uint32_t elem,
+                                                   const int32_t* __restrict__ src,
+                                                   uint32_t src_rows,
+                                                   uint16_t* __restrict__ gathered) {
   __shared__ uint16_t tile[64][64 + 2];
   const uint32_t c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
   // load: 64 rows x 64 columns, lane -> row i/16 (+16k), columns 4*(i%16)..+3
@@ -808,7 +815,16 @@ __global__ __launch_bounds__(256) void k_transpose(const uint16_t* __restrict__ 
     const uint32_t c = c0 + lc;
     uint16_t v[4] = {0, 0, 0, 0};
     if (r < rows && c < width) {
-      uint2 bits = *reinterpret_cast<const uint2*>(x + (size_t)r * row_stride + col_offset + c);
+      uint2 bits;
+      if (kGather) {
+        const uint32_t sr = (uint32_t)src[r];
+        bits = sr < src_rows
+                   ? *reinterpret_cast<const uint2*>(x + (size_t)sr * row_stride + col_offset + c)
+                   : make_uint2(0u, 0u);
+        *reinterpret_cast<uint2*>(gathered + (size_t)r * width + c) = bits;
+      } else {
+        bits = *reinterpret_cast<const uint2*>(x + (size_t)r * row_stride + col_offset + c);
+      }
       if (elem == H3_ELEM_BF16) {
         v4f f = widen4(bits, elem);
         v4h hv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3]};
@@ -965,9 +981,19 @@ hipError_t launch_transpose(uint32_t width, uint32_t row_capacity, uint32_t row_
   if (clear_to > row_capacity) clear_to = row_capacity;
   if (clear_to == 0) return hipSuccess;
   dim3 grid(div_up(width, 64), div_up(clear_to, 64));
-  hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, stream,
+  hipLaunchKernelGGL(k_transpose<false>, grid, dim3(256), 0, stream,
                      reinterpret_cast<const uint16_t*>(x), out, rows, clear_to, width,
-                     row_capacity, row_stride, col_offset, elem);
+                     row_capacity, row_stride, col_offset, elem, nullptr, 0u, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_transpose(uint32_t width, uint32_t rows, const int32_t* src,
+                                   uint32_t src_rows, const uint16_t* x, uint16_t* gathered,
+                                   uint16_t* out, hipStream_t stream) {
+  // rows is a multiple of 64 (the VSA layout's padded row count), so every row is loaded
+  dim3 grid(div_up(width, 64), div_up(rows, 64));
+  hipLaunchKernelGGL(k_transpose<true>, grid, dim3(256), 0, stream, x, out, rows, rows, width,
+                     rows, width, 0u, (uint32_t)H3_ELEM_F16, src, src_rows, gathered);
   return hipGetLastError();
 }
 

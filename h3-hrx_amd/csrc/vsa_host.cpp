@@ -303,11 +303,14 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
   int st;
   // src/vsa/device.rs:215-238: gather q, k, v into the cube layout, and the block means of q and
   // k (and of v, which a gate reads, 388-398), each mean from the pass that writes its rows: the
-  // same rows and means as a gather followed by a pool, without reading the rows back
+  // same rows and means as a gather followed by a pool, without reading the rows back. Without a
+  // gate the INT8 attention's v is gathered below, by the pass that writes V^T.
+  const bool v_with_vt = r->bits != 16 && !gate.ptr;
   if ((st = vsa_gather_pool(c, r->src, r->lengths, q, r->q, r->qm, stream)) ||
       (st = vsa_gather_pool(c, r->src, r->lengths, k, r->k, r->km, stream)) ||
-      (st = gate.ptr ? vsa_gather_pool(c, r->src, r->lengths, v, r->v, r->vm, stream)
-                     : h3_vsa_gather(c, r->src, v, r->v, stream)))
+      (st = gate.ptr    ? vsa_gather_pool(c, r->src, r->lengths, v, r->v, r->vm, stream)
+            : v_with_vt ? H3_OK
+                        : h3_vsa_gather(c, r->src, v, r->v, stream)))
     return st;
   // 239-261: block scores, routes
   if ((st = h3_vsa_scores(c, r->qm, r->km, r->scores, stream)) ||
@@ -323,7 +326,9 @@ int h3_vsa_attend(h3_vsa* r, uint32_t layer, h3_view q, h3_view k, h3_view v, h3
     h3_view& mean = r->means[layer];
     if ((st = h3_prepare_qk_i8(&r->prep_q, c->padded, r->q, r->zero, r->qi, r->qs, stream)) ||
         (st = h3_prepare_qk_i8(&r->prep_k, c->padded, r->k, mean, r->ki, r->ks, stream)) ||
-        (st = h3_transpose_f16(&r->transpose, c->padded, c->padded, r->v, r->vt, stream)) ||
+        (st = v_with_vt ? vsa_gather_transpose(c, r->src, v, r->v, r->vt, stream)
+                        : h3_transpose_f16(&r->transpose, c->padded, c->padded, r->v, r->vt,
+                                           stream)) ||
         (st = vsa_attention_i8_ws(&r->attention, c->padded, c->heads, r->qi, r->qs, r->ki, r->ks,
                                   r->vt, r->out, r->routes, r->lengths, r->ws,
                                   reinterpret_cast<hipStream_t>(stream))))

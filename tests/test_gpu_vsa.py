@@ -383,7 +383,9 @@ def test_runtime_reproduces_the_reference_device_test(dev):
     assert np.array_equal(gq, O.vsa_gather(src, t, data[0]))
     gk0 = read(b.k, np.uint16, (n, w))
     assert np.array_equal(gk0, O.vsa_gather(src, t, data[1]))
-    assert np.array_equal(read(b.v, np.uint16, (n, w)), O.vsa_gather(src, t, data[2]))
+    gv = O.vsa_gather(src, t, data[2])
+    assert np.array_equal(read(b.v, np.uint16, (n, w)), gv)
+    assert np.array_equal(read(b.vt, np.uint16, (w, n)), np.ascontiguousarray(gv.T))
     qm = read(b.qm, np.float32, (nb, w))
     km = read(b.km, np.float32, (nb, w))
     assert np.array_equal(qm.view(np.uint32), O.vsa_pool(lengths, gq).view(np.uint32))
